@@ -1,0 +1,277 @@
+"""ctypes binding of the CPU oracle (oracle/libntc_oracle.so) and of the reference build
+(oracle/_ref/libntc_ref*.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+leg, never by the product package. Every helper takes numpy arrays and returns numpy arrays.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "libntc_oracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libntc_ref.so")
+REF_FAST_SO = os.path.join(HERE, "_ref", "libntc_ref_fast.so")
+
+MAX_LEVELS, MAX_POS, MAX_OUT, MAX_HIDDEN = 3, 16, 12, 8
+NS_LAT, NS_MLP, NS_BATCH_PIX, NS_BATCH_TEX = 1, 2, 3, 4
+
+
+class OrLevel(C.Structure):
+    _fields_ = [("W", C.c_int), ("H", C.c_int), ("C", C.c_int), ("nearest", C.c_int), ("off", C.c_longlong)]
+
+
+class OrModel(C.Structure):
+    _fields_ = [("W", C.c_int), ("H", C.c_int), ("nout", C.c_int), ("nlev", C.c_int),
+                ("lv", OrLevel * MAX_LEVELS), ("npos", C.c_int), ("pos", C.c_int * MAX_POS),
+                ("nin", C.c_int), ("nhidden", C.c_int), ("hidden", C.c_int * MAX_HIDDEN),
+                ("leak", C.c_float), ("clamp_out", C.c_int), ("cw", C.c_float * MAX_OUT), ("wsum", C.c_float)]
+
+
+class OrDct(C.Structure):
+    _fields_ = [("C", C.c_int), ("BW", C.c_int), ("BH", C.c_int), ("dc_step", C.c_int), ("deadzone", C.c_int),
+                ("lo_w16", C.c_int), ("lam_t16", C.c_float * 16), ("step", C.POINTER(C.c_int)),
+                ("code", C.POINTER(C.c_uint8)), ("sym", C.POINTER(C.c_int16))]
+
+
+class OrTrainCfg(C.Structure):
+    _fields_ = [("seed", C.c_uint64), ("mlp_pairs", C.c_int), ("mlp_batch", C.c_int), ("mlp_sigma", C.c_float),
+                ("mlp_lr", C.c_float), ("lat_pairs", C.c_int), ("lat_sigma", C.c_float), ("lat_lr", C.c_float),
+                ("qat", C.c_int), ("qat_ch", C.c_int * 16), ("fd_from", C.c_int), ("fd_h", C.c_float)]
+
+
+class OrTrainState(C.Structure):
+    _fields_ = [("z", C.POINTER(C.c_float)), ("p", C.POINTER(C.c_float)), ("wm", C.POINTER(C.c_float)),
+                ("wv", C.POINTER(C.c_float)), ("wt", C.c_int), ("zm", C.POINTER(C.c_float)),
+                ("zv", C.POINTER(C.c_float)), ("zt", C.c_int), ("lat_step_no", C.c_int)]
+
+
+@dataclass
+class Model:
+    """A decoder layout: image size, latent levels (W, H, C, nearest), positional kinds, MLP."""
+    W: int
+    H: int
+    levels: list            # [(W, H, C, nearest), ...]
+    hidden: list
+    T: int = 1
+    pos: list = field(default_factory=lambda: [0])   # 0 = uv, 1 = lv1local
+    leak: float = 0.01
+    clamp_out: bool = False
+    weights: list = None    # per-texture loss weight
+
+    @property
+    def nout(self):
+        return 3 * self.T
+
+    @property
+    def nin(self):
+        return sum(l[2] for l in self.levels) + 2 * len(self.pos)
+
+    def offsets(self):
+        off, o = [], 0
+        for (w, h, c, _) in self.levels:
+            off.append(o)
+            o += w * h * c
+        return off, o
+
+    @property
+    def nz(self):
+        return self.offsets()[1]
+
+    @property
+    def nparams(self):
+        n, cur = 0, self.nin
+        for h in self.hidden:
+            n += h * cur + h
+            cur = h
+        return n + self.nout * cur + self.nout
+
+    def cw(self):
+        w = self.weights or [1.0] * self.T
+        return [float(w[c // 3]) for c in range(self.nout)], float(np.float32(sum(np.float32(x) for x in w)))
+
+    def to_c(self) -> OrModel:
+        m = OrModel()
+        m.W, m.H, m.nout, m.nlev = self.W, self.H, self.nout, len(self.levels)
+        off, _ = self.offsets()
+        for l, (w, h, c, nr) in enumerate(self.levels):
+            m.lv[l] = OrLevel(w, h, c, int(bool(nr)), off[l])
+        m.npos = len(self.pos)
+        for q, k in enumerate(self.pos):
+            m.pos[q] = k
+        m.nin = self.nin
+        m.nhidden = len(self.hidden)
+        for l, h in enumerate(self.hidden):
+            m.hidden[l] = h
+        m.leak = self.leak
+        m.clamp_out = int(self.clamp_out)
+        cw, wsum = self.cw()
+        for c in range(self.nout):
+            m.cw[c] = cw[c]
+        m.wsum = wsum
+        return m
+
+
+def _f(a):
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def _d(a):
+    return a.ctypes.data_as(C.POINTER(C.c_double))
+
+
+def _i(a):
+    return a.ctypes.data_as(C.POINTER(C.c_int))
+
+
+def _load(path):
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built (run `make -C oracle` or __graft_entry__.build())")
+    return C.CDLL(path)
+
+
+_P = C.c_void_p
+_SIGS = {
+    "gauss": (C.c_float, [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64]),
+    "noise_u32": (C.c_uint32, [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64]),
+    "noise_uniform": (C.c_uint32, [C.c_uint32, C.c_uint32]),
+    "gauss_fill": (None, [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, C.c_longlong, _P]),
+    "gauss_radius": (C.c_float, [C.c_uint32]),
+    "gauss_cosine": (C.c_float, [C.c_uint32]),
+    "features": (None, [_P, _P, C.c_int, C.c_int, _P]),
+    "mlp_forward": (None, [_P, _P, _P, _P]),
+    "decode_full": (None, [_P, _P, _P, _P]),
+    "decode_err": (None, [_P, _P, _P, _P, _P]),
+    "loss_subset": (C.c_double, [_P, _P, _P, _P, _P, C.c_int]),
+    "draw_batch": (None, [C.c_uint64, C.c_int, C.c_int, C.c_int, _P]),
+    "mlp_es_eval": (None, [_P, _P, _P, _P, C.c_uint64, C.c_int, C.c_float, C.c_int, _P, C.c_int, _P, _P, _P, _P]),
+    "mlp_es_grad": (None, [C.c_longlong, C.c_int, C.c_uint64, C.c_int, C.c_float, _P, _P]),
+    "adam": (None, [_P, _P, _P, _P, C.c_longlong, C.c_float, C.c_int]),
+    "mlp_fd_eval": (None, [_P, _P, _P, _P, C.c_float, _P, C.c_int, _P, _P, _P]),
+    "fd_grad": (None, [C.c_longlong, _P, _P, _P]),
+    "lat_grad": (None, [_P, _P, _P, _P, _P, C.c_uint64, C.c_int, C.c_float, C.c_int, C.c_uint, _P, C.c_float,
+                        _P, _P, _P, _P]),
+    "qat_grid": (None, [_P]),
+    "qat_index": (C.c_int, [C.c_float, C.c_int]),
+    "qat_search": (None, [_P, _P, _P, _P, _P, _P]),
+    "qes_index": (C.c_int, [C.c_float, C.c_float, C.c_float, C.c_int]),
+    "qes_fit": (None, [_P, _P, C.c_int, _P, _P, _P, _P]),
+    "qes_snap_level": (C.c_longlong, [_P, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int]),
+    "dct_tables": (None, [_P, _P, _P]),
+    "dct_build_steps": (None, [C.c_int, C.c_int, _P]),
+    "dct_fwd8": (None, [_P, _P]),
+    "dct_inv8": (None, [_P, _P]),
+    "dct_quant_dc": (C.c_int, [C.c_float, C.c_int]),
+    "dct_quant_ac": (C.c_int, [C.c_float, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "dct_dequant_ac": (C.c_float, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "dct_block_bits": (C.c_int, [_P, C.c_int]),
+    "dct_quantize_block": (C.c_int, [_P, _P, C.c_int, C.c_float, C.c_int, C.c_int, C.c_int, _P, _P, _P]),
+    "dct_code_of_gain": (C.c_int, [C.c_double]),
+    "dct_snap_level0": (None, [_P, _P, _P, _P, _P, _P]),
+    "dct_recon_level0": (None, [_P, _P, _P, _P]),
+    "dct_probe_codes": (None, [_P, _P, _P, _P, _P]),
+    "dct_rate_pair": (None, [_P, _P, _P, _P, C.c_float, _P]),
+    "f32_to_f16": (C.c_uint16, [C.c_float, _P]),
+    "f16_to_f32": (C.c_float, [C.c_uint16]),
+    "q8_index": (C.c_int, [C.c_float, C.c_float, C.c_float, C.c_int]),
+}
+_ORACLE_ONLY = {
+    "gauss_fill", "gauss_radius", "gauss_cosine", "mlp_es_eval", "mlp_es_grad", "adam", "mlp_fd_eval",
+    "fd_grad", "lat_grad", "dct_tables", "round_fp16", "train_iter",
+}
+
+
+class Lib:
+    """One of the two CPU implementations: prefix 'or_' (the oracle) or 'ref_' (the reference)."""
+
+    def __init__(self, path, prefix):
+        self.lib = _load(path)
+        self.prefix = prefix
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(self.lib, prefix + name, None)
+            if fn is None:
+                continue
+            fn.restype = res
+            fn.argtypes = args
+            setattr(self, "_" + name, fn)
+        if prefix == "or_":
+            self.lib.or_train_iter.restype = C.c_double
+            self.lib.or_train_iter.argtypes = [_P, _P, _P, _P, C.c_int, C.c_int]
+            self.lib.or_round_fp16.restype = C.c_int
+            self.lib.or_round_fp16.argtypes = [_P, C.c_longlong, _P]
+            self.lib.or_dct_tables.argtypes = [_P, _P, _P]
+        else:
+            L = self.lib
+            L.ref_mlp_step.restype = C.c_double
+            L.ref_mlp_step.argtypes = [_P, _P, _P, _P, C.c_uint64, C.c_int, C.c_float, C.c_float, C.c_int, C.c_int,
+                                       _P, _P, _P, _P, _P]
+            L.ref_mlp_step_fd.restype = C.c_double
+            L.ref_mlp_step_fd.argtypes = [_P, _P, _P, _P, C.c_uint64, C.c_int, C.c_float, C.c_float, C.c_int,
+                                          _P, _P, _P, _P, _P]
+            L.ref_draw_batch.argtypes = [C.c_uint64, C.c_int, C.c_int, _P, _P]
+            L.ref_lat_step.argtypes = [_P, _P, _P, _P, C.c_uint64, C.c_int, C.c_float, C.c_float, C.c_int, C.c_int,
+                                       _P, _P, _P, _P]
+            L.ref_qat_search.argtypes = [_P, _P, _P, _P, _P]
+            L.ref_qat_grid.argtypes = [_P]
+            L.ref_dct_tables.argtypes = [_P, _P, _P]
+            L.ref_dct_selftest.restype = C.c_int
+            L.ref_ntcb_selfcheck.restype = C.c_int
+            L.ref_train_create.restype = C.c_void_p
+            L.ref_train_create.argtypes = [_P, _P, _P, _P, _P]
+            L.ref_train_iter.restype = C.c_double
+            L.ref_train_iter.argtypes = [C.c_void_p, C.c_int, C.c_int]
+            L.ref_train_get.argtypes = [C.c_void_p, _P, _P]
+            L.ref_train_destroy.argtypes = [C.c_void_p]
+            L.ref_omp_threads.restype = C.c_int
+
+    # ---- noise
+    def gauss(self, seed, stream, step, pair, index):
+        return self._gauss(seed, stream, step, pair, index)
+
+    def gauss_fill(self, seed, stream, step, pair, index0, n):
+        out = np.empty(n, np.float32)
+        self._gauss_fill(seed, stream, step, pair, index0, n, out.ctypes.data)
+        return out
+
+    # ---- decoder
+    def features(self, m: Model, z, px, py):
+        f = np.zeros(128, np.float32)
+        self._features(C.byref(m.to_c()), z.ctypes.data, px, py, f.ctypes.data)
+        return f[: m.nin]
+
+    def mlp_forward(self, m: Model, p, x):
+        out = np.zeros(12, np.float32)
+        self._mlp_forward(C.byref(m.to_c()), p.ctypes.data, np.ascontiguousarray(x, np.float32).ctypes.data,
+                          out.ctypes.data)
+        return out[: m.nout]
+
+    def decode_full(self, m: Model, p, z):
+        img = np.zeros(m.W * m.H * m.nout, np.float32)
+        self._decode_full(C.byref(m.to_c()), p.ctypes.data, z.ctypes.data, img.ctypes.data)
+        return img
+
+    def decode_err(self, m: Model, p, z, tgt):
+        err = np.zeros(m.W * m.H, np.float32)
+        self._decode_err(C.byref(m.to_c()), p.ctypes.data, z.ctypes.data, tgt.ctypes.data, err.ctypes.data)
+        return err
+
+    def loss_subset(self, m: Model, p, z, tgt, idx):
+        idx = np.ascontiguousarray(idx, np.int32)
+        return self._loss_subset(C.byref(m.to_c()), p.ctypes.data, z.ctypes.data, tgt.ctypes.data, idx.ctypes.data,
+                                 len(idx))
+
+
+def oracle() -> Lib:
+    return Lib(ORACLE_SO, "or_")
+
+
+def reference(fast: bool = False) -> Lib:
+    return Lib(REF_FAST_SO if fast else REF_SO, "ref_")
+
+
+def have_reference(fast: bool = False) -> bool:
+    return os.path.exists(REF_FAST_SO if fast else REF_SO)
