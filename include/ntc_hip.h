@@ -1,0 +1,138 @@
+/* C ABI of the MI355X (gfx950) ES training backend, exported by libntc_hip.so.
+ *
+ * One entry point per method of ntc_cuda::Trainer (include/ntc_cuda.h, which is
+ * declaration-compatible with the reference's cuda/ntc_cuda.h); each comment names the reference
+ * declaration it replaces. Plain C: opaque handle, plain pointers and sizes, host buffers only.
+ * The descriptor structs have exactly the layout of their C++ counterparts in ntc_cuda.h
+ * (checked with static_assert in the library), so a caller may pass either.
+ *
+ * Error behaviour follows the reference: ntc_trainer_init returns 0 and writes a reason for a
+ * model outside the envelope; any other misuse or device error prints a message and exits.
+ */
+#pragma once
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NTC_MAX_LEVELS 3
+#define NTC_MAX_POS 16
+#define NTC_MAX_OUT 12
+#define NTC_MAX_HIDDEN 8
+#define NTC_MAX_CH 16
+#define NTC_MAX_QES_CH 64
+#define NTC_MAX_DCT_CH 4
+
+typedef struct ntc_level_desc { int W, H, C; size_t off; bool nearest; } ntc_level_desc;   /* LevelDesc, cuda/ntc_cuda.h:25 */
+typedef struct ntc_pos_desc { int kind; } ntc_pos_desc;                                      /* PosDesc, cuda/ntc_cuda.h:26 */
+
+typedef struct ntc_model_desc {                     /* ModelDesc, cuda/ntc_cuda.h:29-52 */
+    int W, H;
+    int T;
+    int nlev; ntc_level_desc lv[NTC_MAX_LEVELS];
+    int npos; ntc_pos_desc pos[NTC_MAX_POS];
+    int nin, nout;
+    int nhidden; int hidden[NTC_MAX_HIDDEN];
+    float leak;
+    bool clamp_out;
+    float cw[NTC_MAX_OUT];
+    float wsum;
+    int qat_bits[NTC_MAX_CH];
+    int qat;
+    const float* qat_grid;
+    int qes_bits[NTC_MAX_LEVELS];
+    int dct, dct_C, dct_N, dct_dc_step;
+    int dct_q[NTC_MAX_DCT_CH];
+    const float* dct_basis;
+    const int* dct_zigzag;
+    int max_pairs;
+    int max_batch;
+    uint64_t seed;
+} ntc_model_desc;
+
+typedef struct ntc_qes_desc {                       /* QesDesc, cuda/ntc_cuda.h:57-63 */
+    int bits[NTC_MAX_LEVELS];
+    int live;
+    int frozen;
+    float lo[NTC_MAX_LEVELS][NTC_MAX_QES_CH], hi[NTC_MAX_LEVELS][NTC_MAX_QES_CH], range[NTC_MAX_LEVELS][NTC_MAX_QES_CH];
+    int grid_off[NTC_MAX_LEVELS][NTC_MAX_QES_CH];
+} ntc_qes_desc;
+
+typedef struct ntc_dct_desc {                       /* DctDesc, cuda/ntc_cuda.h:68-76 */
+    int live, C, BW, BH, N, dc_step;
+    int rate_es, rate_trunc; float rate_scale; float lam_t16[16];
+    int lo_w16;
+    int deadzone;
+} ntc_dct_desc;
+
+typedef struct ntc_trainer ntc_trainer;             /* an ntc_cuda::Trainer */
+
+/* Trainer::Trainer / ~Trainer (cuda/ntc_cuda.h:80-81) */
+ntc_trainer* ntc_trainer_create(void);
+void ntc_trainer_destroy(ntc_trainer* t);
+/* Trainer::init (cuda/ntc_cuda.h:85): 1 on success; 0 with a reason in why[0..why_cap) */
+int ntc_trainer_init(ntc_trainer* t, const ntc_model_desc* d, const float* z, const float* p, const float* target,
+                     char* why, size_t why_cap);
+/* Trainer::banner (cuda/ntc_cuda.h:86): writes at most cap bytes (NUL-terminated), returns the full length */
+size_t ntc_trainer_banner(const ntc_trainer* t, char* buf, size_t cap);
+
+/* Trainer::upload_model / download_model (cuda/ntc_cuda.h:88-89): z = nz floats, p = P floats */
+void ntc_trainer_upload_model(ntc_trainer* t, const float* z, const float* p);
+void ntc_trainer_download_model(ntc_trainer* t, float* z, float* p);
+/* Trainer::set_qes / snap_latent / shadow_pull / download_zq (cuda/ntc_cuda.h:93-96) */
+void ntc_trainer_set_qes(ntc_trainer* t, const ntc_qes_desc* q, const float* grid, size_t grid_n);
+void ntc_trainer_snap_latent(ntc_trainer* t);
+void ntc_trainer_shadow_pull(ntc_trainer* t, size_t off, size_t n, float f);
+void ntc_trainer_download_zq(ntc_trainer* t, float* zq);
+/* Trainer::set_dct / download_dct / download_dct_rate (cuda/ntc_cuda.h:100-106) */
+void ntc_trainer_set_dct(ntc_trainer* t, const ntc_dct_desc* d, const uint8_t* code, const int16_t* sym, const int* step);
+void ntc_trainer_download_dct(ntc_trainer* t, int16_t* sym, uint8_t* code);
+void ntc_trainer_download_dct_rate(ntc_trainer* t, int32_t* bits, int32_t* dbits_last_pair, int* ntrunc, int* nz_before,
+                                   int* hits, int* evals);
+
+/* Trainer::mlp_step / mlp_step_fd / reset_mlp_adam / mlp_stats (cuda/ntc_cuda.h:110-115) */
+void ntc_trainer_mlp_step(ntc_trainer* t, int it, float sigma, float lr, int N, int M);
+void ntc_trainer_mlp_step_fd(ntc_trainer* t, int it, float h, float lr, int M);
+void ntc_trainer_reset_mlp_adam(ntc_trainer* t);
+void ntc_trainer_mlp_stats(ntc_trainer* t, double* batch_loss, double* diff_std);
+
+/* Trainer::lat_step / qat_search / decode_full (cuda/ntc_cuda.h:118-123); z_host may be NULL */
+void ntc_trainer_lat_step(ntc_trainer* t, int it, float sigma, float lr, int K);
+void ntc_trainer_qat_search(ntc_trainer* t);
+void ntc_trainer_decode_full(ntc_trainer* t, const float* z_host, float* img);
+
+/* Trainer::debug_last_batch / debug_last_dl / debug_last_zgrad (cuda/ntc_cuda.h:127-129):
+ * copy at most cap values, return how many the trainer holds */
+size_t ntc_trainer_debug_last_batch(const ntc_trainer* t, int* bidx, size_t cap);
+size_t ntc_trainer_debug_last_dl(const ntc_trainer* t, double* dl, size_t cap);
+size_t ntc_trainer_debug_last_zgrad(const ntc_trainer* t, float* g, size_t cap);
+
+/* ---- Instrumentation and verification helpers. No counterpart in the reference: they serve the
+ * parity tests and the benchmark, and change no trainer state. ---- */
+/* sizeof of a descriptor as this library was compiled ("ntc_model_desc", "ntc_qes_desc", "ntc_dct_desc",
+ * "ntc_level_desc"), 0 for an unknown name: lets a binding check its mirror of the layouts */
+size_t ntc_abi_sizeof(const char* name);
+/* the member losses of the last ES step (pair i: member + is w + sigma eps_i, member - is w - sigma eps_i),
+ * or for a central-difference step the losses at w_j + h and w_j - h; returns the pair count */
+size_t ntc_trainer_debug_last_losses(const ntc_trainer* t, double* lplus, double* lminus, size_t cap);
+long long ntc_trainer_nparams(const ntc_trainer* t);
+long long ntc_trainer_nz(const ntc_trainer* t);
+void* ntc_trainer_stream(const ntc_trainer* t);        /* the hipStream_t every launch of this trainer uses */
+void ntc_trainer_synchronize(ntc_trainer* t);
+/* Per-kernel device time with HIP events recorded on the trainer's stream around each launch
+ * of the named kernel family ("pop_eval", "lat_pair", "qat_search", ...). */
+void ntc_trainer_set_profiling(ntc_trainer* t, int on);
+int ntc_trainer_kernel_time(ntc_trainer* t, const char* name, double* total_ms, long long* launches);
+/* the device's Gaussian draws for indices index0 .. index0 + n - 1 of one (seed, stream, step, pair) */
+void ntc_trainer_debug_gauss(ntc_trainer* t, uint32_t stream, uint32_t step, uint32_t pair, uint64_t index0, size_t n,
+                             float* out);
+/* the device's copy of the two Gaussian factors for 24-bit draws k0 .. k0 + n - 1:
+ * rad[k] = sqrtf(-2 logf((k + 1) / 2^24)), cosv[k] = cosf(2 pi k / 2^24) */
+void ntc_trainer_debug_noise_factors(ntc_trainer* t, uint32_t k0, size_t n, float* rad, float* cosv);
+
+#ifdef __cplusplus
+}
+#endif

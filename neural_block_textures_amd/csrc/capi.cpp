@@ -1,0 +1,174 @@
+// extern "C" entry points of libntc_hip.so: one per ntc_cuda::Trainer method (include/ntc_hip.h),
+// plus the instrumentation helpers the tests and the benchmark use.
+#include <stddef.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "ntc_hip.h"
+#include "trainer_impl.hpp"
+
+using ntc_cuda::Trainer;
+
+// The C descriptors must be the C++ ones byte for byte.
+#define NTC_SAME_FIELD(C, CPP, F) static_assert(offsetof(C, F) == offsetof(CPP, F), #C "." #F " is misplaced")
+static_assert(sizeof(ntc_level_desc) == sizeof(ntc_cuda::LevelDesc), "LevelDesc layout");
+NTC_SAME_FIELD(ntc_level_desc, ntc_cuda::LevelDesc, off);
+NTC_SAME_FIELD(ntc_level_desc, ntc_cuda::LevelDesc, nearest);
+static_assert(sizeof(ntc_model_desc) == sizeof(ntc_cuda::ModelDesc), "ModelDesc layout");
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, lv);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, npos);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, nin);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, hidden);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, leak);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, clamp_out);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, cw);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, wsum);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, qat_bits);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, qat_grid);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, qes_bits);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, dct_q);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, dct_basis);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, dct_zigzag);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, max_pairs);
+NTC_SAME_FIELD(ntc_model_desc, ntc_cuda::ModelDesc, seed);
+static_assert(sizeof(ntc_qes_desc) == sizeof(ntc_cuda::QesDesc), "QesDesc layout");
+NTC_SAME_FIELD(ntc_qes_desc, ntc_cuda::QesDesc, lo);
+NTC_SAME_FIELD(ntc_qes_desc, ntc_cuda::QesDesc, grid_off);
+static_assert(sizeof(ntc_dct_desc) == sizeof(ntc_cuda::DctDesc), "DctDesc layout");
+NTC_SAME_FIELD(ntc_dct_desc, ntc_cuda::DctDesc, rate_scale);
+NTC_SAME_FIELD(ntc_dct_desc, ntc_cuda::DctDesc, lam_t16);
+NTC_SAME_FIELD(ntc_dct_desc, ntc_cuda::DctDesc, deadzone);
+
+struct ntc_trainer { Trainer t; };
+
+static size_t copy_out(const std::string& s, char* buf, size_t cap) {
+    if (buf && cap) { const size_t n = std::min(cap - 1, s.size()); memcpy(buf, s.data(), n); buf[n] = 0; }
+    return s.size();
+}
+
+extern "C" {
+
+ntc_trainer* ntc_trainer_create(void) { return new ntc_trainer; }
+void ntc_trainer_destroy(ntc_trainer* t) { delete t; }
+
+int ntc_trainer_init(ntc_trainer* t, const ntc_model_desc* d, const float* z, const float* p, const float* target, char* why,
+                     size_t why_cap) {
+    std::string reason;
+    ntc_cuda::ModelDesc md;
+    memcpy((void*)&md, d, sizeof(md));
+    const bool ok = t->t.init(md, z, p, target, reason);
+    copy_out(ok ? std::string() : reason, why, why_cap);
+    return ok ? 1 : 0;
+}
+size_t ntc_trainer_banner(const ntc_trainer* t, char* buf, size_t cap) { return copy_out(t->t.banner(), buf, cap); }
+
+void ntc_trainer_upload_model(ntc_trainer* t, const float* z, const float* p) { t->t.upload_model(z, p); }
+void ntc_trainer_download_model(ntc_trainer* t, float* z, float* p) { t->t.download_model(z, p); }
+void ntc_trainer_set_qes(ntc_trainer* t, const ntc_qes_desc* q, const float* grid, size_t grid_n) {
+    t->t.set_qes(*reinterpret_cast<const ntc_cuda::QesDesc*>(q), grid, grid_n);
+}
+void ntc_trainer_snap_latent(ntc_trainer* t) { t->t.snap_latent(); }
+void ntc_trainer_shadow_pull(ntc_trainer* t, size_t off, size_t n, float f) { t->t.shadow_pull(off, n, f); }
+void ntc_trainer_download_zq(ntc_trainer* t, float* zq) { t->t.download_zq(zq); }
+void ntc_trainer_set_dct(ntc_trainer* t, const ntc_dct_desc* d, const uint8_t* code, const int16_t* sym, const int* step) {
+    t->t.set_dct(*reinterpret_cast<const ntc_cuda::DctDesc*>(d), code, sym, step);
+}
+void ntc_trainer_download_dct(ntc_trainer* t, int16_t* sym, uint8_t* code) { t->t.download_dct(sym, code); }
+void ntc_trainer_download_dct_rate(ntc_trainer* t, int32_t* bits, int32_t* dbits_last_pair, int* ntrunc, int* nz_before, int* hits,
+                                   int* evals) {
+    t->t.download_dct_rate(bits, dbits_last_pair, ntrunc, nz_before, hits, evals);
+}
+
+void ntc_trainer_mlp_step(ntc_trainer* t, int it, float sigma, float lr, int N, int M) { t->t.mlp_step(it, sigma, lr, N, M); }
+void ntc_trainer_mlp_step_fd(ntc_trainer* t, int it, float h, float lr, int M) { t->t.mlp_step_fd(it, h, lr, M); }
+void ntc_trainer_reset_mlp_adam(ntc_trainer* t) { t->t.reset_mlp_adam(); }
+void ntc_trainer_mlp_stats(ntc_trainer* t, double* batch_loss, double* diff_std) { t->t.mlp_stats(*batch_loss, *diff_std); }
+
+void ntc_trainer_lat_step(ntc_trainer* t, int it, float sigma, float lr, int K) { t->t.lat_step(it, sigma, lr, K); }
+void ntc_trainer_qat_search(ntc_trainer* t) { t->t.qat_search(); }
+void ntc_trainer_decode_full(ntc_trainer* t, const float* z_host, float* img) { t->t.decode_full(z_host, img); }
+
+size_t ntc_trainer_debug_last_batch(const ntc_trainer* t, int* bidx, size_t cap) {
+    std::vector<int> v; t->t.debug_last_batch(v);
+    if (bidx) memcpy(bidx, v.data(), std::min(cap, v.size()) * sizeof(int));
+    return v.size();
+}
+size_t ntc_trainer_debug_last_dl(const ntc_trainer* t, double* dl, size_t cap) {
+    std::vector<double> v; t->t.debug_last_dl(v);
+    if (dl) memcpy(dl, v.data(), std::min(cap, v.size()) * sizeof(double));
+    return v.size();
+}
+size_t ntc_trainer_debug_last_zgrad(const ntc_trainer* t, float* g, size_t cap) {
+    std::vector<float> v; t->t.debug_last_zgrad(v);
+    if (g) memcpy(g, v.data(), std::min(cap, v.size()) * sizeof(float));
+    return v.size();
+}
+
+size_t ntc_trainer_debug_last_losses(const ntc_trainer* t, double* lplus, double* lminus, size_t cap) {
+    auto& I = *t->t.im;
+    const size_t n = (size_t)I.last_N;
+    if (!n) return 0;
+    const size_t m = std::min(cap, n);
+    const int chunks = (I.last_M + I.last_chunk - 1) / I.last_chunk;
+    std::vector<double> part((size_t)2 * n * chunks);
+    NTC_CHECK(hipMemcpyAsync(part.data(), I.part, part.size() * sizeof(double), hipMemcpyDeviceToHost, I.stream));
+    NTC_CHECK(hipStreamSynchronize(I.stream));
+    const double norm = 3.0 * (double)I.d.wsum * (double)I.last_M;
+    for (size_t i = 0; i < m; i++) {
+        double a = 0.0, b = 0.0;
+        for (int c = 0; c < chunks; c++) { a += part[(2 * i) * chunks + c]; b += part[(2 * i + 1) * chunks + c]; }
+        if (lplus) lplus[i] = a / norm;
+        if (lminus) lminus[i] = b / norm;
+    }
+    return n;
+}
+size_t ntc_abi_sizeof(const char* name) {
+    const std::string n = name ? name : "";
+    if (n == "ntc_model_desc") return sizeof(ntc_model_desc);
+    if (n == "ntc_qes_desc") return sizeof(ntc_qes_desc);
+    if (n == "ntc_dct_desc") return sizeof(ntc_dct_desc);
+    if (n == "ntc_level_desc") return sizeof(ntc_level_desc);
+    return 0;
+}
+long long ntc_trainer_nparams(const ntc_trainer* t) { return t->t.im->P; }
+long long ntc_trainer_nz(const ntc_trainer* t) { return (long long)t->t.im->nz; }
+void* ntc_trainer_stream(const ntc_trainer* t) { return (void*)t->t.im->stream; }
+void ntc_trainer_synchronize(ntc_trainer* t) { if (t->t.im->stream) NTC_CHECK(hipStreamSynchronize(t->t.im->stream)); }
+
+void ntc_trainer_set_profiling(ntc_trainer* t, int on) {
+    auto& I = *t->t.im;
+    ntc_hip::resolve_times(I);
+    I.profiling = on != 0;
+    if (on) I.times.clear();
+}
+int ntc_trainer_kernel_time(ntc_trainer* t, const char* name, double* total_ms, long long* launches) {
+    auto& I = *t->t.im;
+    ntc_hip::resolve_times(I);
+    auto it = I.times.find(name);
+    if (it == I.times.end()) { *total_ms = 0.0; *launches = 0; return 0; }
+    *total_ms = it->second.total_ms; *launches = it->second.launches;
+    return 1;
+}
+
+void ntc_trainer_debug_gauss(ntc_trainer* t, uint32_t stream, uint32_t step, uint32_t pair, uint64_t index0, size_t n, float* out) {
+    auto& I = *t->t.im;
+    float* d = nullptr;
+    NTC_CHECK(hipMalloc(&d, std::max<size_t>(n, 1) * sizeof(float)));
+    ntc_hip::launch_debug_gauss(I, stream, step, pair, index0, n, d);
+    NTC_CHECK(hipMemcpyAsync(out, d, n * sizeof(float), hipMemcpyDeviceToHost, I.stream));
+    NTC_CHECK(hipStreamSynchronize(I.stream));
+    NTC_CHECK(hipFree(d));
+}
+void ntc_trainer_debug_noise_factors(ntc_trainer* t, uint32_t k0, size_t n, float* rad, float* cosv) {
+    auto& I = *t->t.im;
+    const size_t total = (size_t)1 << 24;
+    if ((size_t)k0 >= total) return;
+    if (n > total - k0) n = total - k0;
+    if (rad) NTC_CHECK(hipMemcpyAsync(rad, I.noise.rad + k0, n * sizeof(float), hipMemcpyDeviceToHost, I.stream));
+    if (cosv) NTC_CHECK(hipMemcpyAsync(cosv, I.noise.cosv + k0, n * sizeof(float), hipMemcpyDeviceToHost, I.stream));
+    NTC_CHECK(hipStreamSynchronize(I.stream));
+}
+
+}   // extern "C"

@@ -1,0 +1,180 @@
+// Latent-side kernels of the gfx950 ES backend: the latent Gaussians of one step, the antithetic
+// pair evaluation over the full image, the footprint gather that turns per-pixel loss differences
+// into the latent gradient, and the exhaustive --qat selector search.
+//
+// Reference semantics (main.cpp): LatentTrainer::step_impl 1974-2044 (perturb texels, decode_err
+// twice, raster-order scatter into the distinct taps, grad += w * eps), dct_rate_pass 1935-1952,
+// qat_search 2088-2139.
+#include "shapes.hpp"
+#include "trainer_impl.hpp"
+
+namespace ntc_hip {
+
+constexpr int kTPB = 256;
+
+__device__ __forceinline__ int level_of(const DevModel& m, long long i) {
+    int l = 0;
+    for (int q = 1; q < m.nlev; q++) if (i >= m.lv[q].off) l = q;
+    return l;
+}
+
+// eps[k][i] = gauss(seed, NS_LAT, step, k, i) for the ES-perturbed levels (0 elsewhere)
+__global__ void __launch_bounds__(kTPB) k_lat_eps(NoiseTables nt, DevModel m, uint64_t seed, uint32_t step, int K, unsigned mask,
+                                                 float* __restrict__ eps) {
+    const long long t = (long long)blockIdx.x * kTPB + threadIdx.x;
+    if (t >= (long long)K * m.nz) return;
+    const int k = (int)(t / m.nz);
+    const long long i = t - (long long)k * m.nz;
+    const int l = level_of(m, i);
+    eps[t] = ((mask >> l) & 1u) ? gauss_at(nt, noise_head(seed, NS_LAT, step, (uint32_t)k), (uint64_t)i) : 0.0f;
+}
+
+// One antithetic latent pair per blockIdx.y: the pixel's features are built from the decode
+// buffer with the pair's texels perturbed by +sg eps and by -sg eps (each texel value one fused
+// operation, as the reference perturbs the flat latent before sampling), two MLP forwards, and
+// dpix = (e+ - e-) * inv_px with the per-pixel errors fused in float (decode_err).
+template <class S>
+__global__ void __launch_bounds__(kTPB) k_lat_pair(DevModel m, const float* __restrict__ w, const float* __restrict__ zdec,
+                                                  const float* __restrict__ eps, const float* __restrict__ tgt, float sg,
+                                                  unsigned mask, float* __restrict__ dpix) {
+    const int p = blockIdx.x * kTPB + threadIdx.x;
+    if (p >= m.npix) return;
+    const int k = blockIdx.y;
+    const float* e = eps + (size_t)k * m.nz;
+    const int px = p % m.W, py = p / m.W;
+    const float* t = tgt + (size_t)p * m.nout;
+    float f[S::kMaxIn], o[S::kMaxOut];
+    features<S>(m, PerturbedLatent{ zdec, e, sg, mask }, px, py, f);
+    mlp_forward<S>(m, w, f, o);
+    const float ep = pixel_err_f(m, o, t);
+    features<S>(m, PerturbedLatent{ zdec, e, -sg, mask }, px, py, f);
+    mlp_forward<S>(m, w, f, o);
+    const float em = pixel_err_f(m, o, t);
+    dpix[(size_t)k * m.npix + p] = (ep - em) * m.inv_px;
+}
+
+// Footprint gather for one level (the gather form of the reference's raster-order scatter): one
+// thread per texel sums dpix over the pixel rectangle whose taps read the texel, in raster order,
+// then adds w * eps per channel, pair after pair. The rectangle comes from the host's range table
+// (built with the same tap arithmetic). With the --dct-lambda rate term, level 0 also receives
+// (rate_scale * dbits) * scale * eps right after each pair's mse term.
+__global__ void __launch_bounds__(kTPB) k_lat_gather(DevModel m, int level, int K, float scale, const float* __restrict__ dpix,
+                                                    const float* __restrict__ eps, const int* __restrict__ ranges,
+                                                    int rate, float rate_scale, int dct_bw, int dct_n,
+                                                    const int32_t* __restrict__ dbits, float* __restrict__ grad) {
+    const DevLevel& L = m.lv[level];
+    const int t = blockIdx.x * kTPB + threadIdx.x;
+    if (t >= L.W * L.H) return;
+    const int tx = t % L.W, ty = t / L.W;
+    const int* R = ranges + L.rng;
+    const int x0 = R[tx], x1 = R[L.W + tx], y0 = R[2 * L.W + ty], y1 = R[2 * L.W + L.H + ty];
+    const long long base = L.off + (long long)t * L.C;
+    const int blk = (ty / 8) * dct_bw + tx / 8;
+    for (int k = 0; k < K; k++) {
+        const float* dp = dpix + (size_t)k * m.npix;
+        float d = 0.0f;
+        for (int py = y0; py < y1; py++)
+            for (int px = x0; px < x1; px++) d += dp[(size_t)py * m.W + px];
+        const float wgt = d * scale;
+        const float* e = eps + (size_t)k * m.nz;
+        for (int c = 0; c < L.C; c++) grad[base + c] = __builtin_fmaf(wgt, e[base + c], grad[base + c]);
+        if (rate) {
+            const int32_t* db = dbits + (size_t)k * dct_n + (size_t)blk * L.C;
+            for (int c = 0; c < L.C; c++)
+                grad[base + c] = __builtin_fmaf(__fmul_rn(__fmul_rn(rate_scale, (float)db[c]), scale), e[base + c], grad[base + c]);
+        }
+    }
+}
+
+// qat_index (main.cpp:2060-2064): lround of the grid coordinate, clamped
+__device__ __forceinline__ int qat_index(float v, int bits) {
+    const int levels = (1 << bits) - 1;
+    const int k = (int)roundf((v + 1.0f) * 0.5f * (float)levels);
+    return clampi(k, 0, levels);
+}
+
+// Exact per-texel search on the discrete nearest level 0 (qat_search): one thread per texel;
+// channels in order, the current grid value first, then every other value with strict <; the
+// cell loss is the double sum over the cell's pixels in raster order. The winner is written to
+// the decode buffer at once, so the next channel's features see it. Texels own disjoint cells, so
+// threads never read each other's level-0 values.
+template <class S>
+__global__ void __launch_bounds__(kTPB) k_qat_search(DevModel m, const float* __restrict__ w, float* __restrict__ zdec,
+                                                    const float* __restrict__ tgt, const int* __restrict__ ranges,
+                                                    const int* __restrict__ qat_bits, const float* __restrict__ grid) {
+    const DevLevel& L = m.lv[0];
+    const int t = blockIdx.x * kTPB + threadIdx.x;
+    if (t >= L.W * L.H) return;
+    const int tx = t % L.W, ty = t / L.W;
+    const int* R = ranges + L.rng;
+    const int x0 = R[tx], x1 = R[L.W + tx], y0 = R[2 * L.W + ty], y1 = R[2 * L.W + L.H + ty];
+    if (x0 >= x1 || y0 >= y1) return;
+    float* zt = zdec + L.off + (size_t)t * L.C;
+    constexpr int CMAX = S::kFixed ? S::kC0 : 16;
+#pragma unroll
+    for (int c = 0; c < CMAX; c++) {
+        if (c >= L.C) continue;
+        const int bits = qat_bits[c], levels = (1 << bits) - 1;
+        const float* g = grid + bits * 257;
+        auto cell_loss = [&](float val) {
+            double sum = 0.0;
+            for (int py = y0; py < y1; py++)
+                for (int px = x0; px < x1; px++) {
+                    float f[S::kMaxIn], o[S::kMaxOut];
+                    features<S>(m, PlainLatent{ zdec }, px, py, f);
+                    f[c] = val;
+                    mlp_forward<S>(m, w, f, o);
+                    sum += pixel_err_d(m, o, tgt + ((size_t)py * m.W + px) * m.nout);
+                }
+            return sum;
+        };
+        int best_k = qat_index(zt[c], bits);
+        double best = cell_loss(g[best_k]);
+        for (int k = 0; k <= levels; k++) {
+            if (k == best_k) continue;
+            const double sk = cell_loss(g[k]);
+            if (sk < best) { best = sk; best_k = k; }
+        }
+        zt[c] = g[best_k];
+    }
+}
+
+// ---------------------------------------------------------------- launchers
+void launch_lat_eps(Impl& I, int K, unsigned mask) {
+    const size_t n = (size_t)K * I.nz;
+    ProfScope ps(I, "lat_eps");
+    hipLaunchKernelGGL(k_lat_eps, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, I.noise, I.dm, I.d.seed,
+                       (uint32_t)I.lat_step_no, K, mask, I.eps_lat);
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask) {
+    ProfScope ps(I, "lat_pair");
+    dispatch_shape(I.dm, [&](auto s) {
+        using S = decltype(s);
+        hipLaunchKernelGGL(k_lat_pair<S>, dim3(blocks_for(I.npix, kTPB), K), dim3(kTPB), 0, I.stream, I.dm, I.w, I.zdec, I.eps_lat,
+                           I.tgt, sigma, mask, I.dpix);
+    });
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_lat_gather(Impl& I, int level, int K, float scale, bool rate) {
+    const size_t ntx = (size_t)I.d.lv[level].W * I.d.lv[level].H;
+    ProfScope ps(I, "lat_gather");
+    hipLaunchKernelGGL(k_lat_gather, dim3(blocks_for(ntx, kTPB)), dim3(kTPB), 0, I.stream, I.dm, level, K, scale, I.dpix, I.eps_lat,
+                       I.ranges, rate ? 1 : 0, I.ddct.rate_scale, I.ddct.BW, I.ddct.n, I.dct_dbits, I.zgrad);
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_qat_search(Impl& I) {
+    const size_t ntx = (size_t)I.d.lv[0].W * I.d.lv[0].H;
+    ProfScope ps(I, "qat_search");
+    dispatch_shape(I.dm, [&](auto s) {
+        using S = decltype(s);
+        hipLaunchKernelGGL(k_qat_search<S>, dim3(blocks_for(ntx, kTPB)), dim3(kTPB), 0, I.stream, I.dm, I.w, I.zdec, I.tgt, I.ranges,
+                           I.qat_bits, I.qat_grid);
+    });
+    NTC_CHECK(hipGetLastError());
+}
+
+}   // namespace ntc_hip

@@ -1,0 +1,265 @@
+// MLP-side kernels of the gfx950 ES backend: minibatch draw, member weight sets, the population
+// evaluation, the ES and central-difference finishes, the ES weight update, Adam and the decode.
+//
+// Reference semantics (main.cpp): MlpTrainer::draw_batch 1825-1833, MlpTrainer::step 1836-1876,
+// MlpTrainer::step_fd 1890-1920, Adam::step 1799-1809, Decoder::decode_full 1712-1718.
+#include "shapes.hpp"
+#include "trainer_impl.hpp"
+
+namespace ntc_hip {
+
+constexpr int kTPB = 256;
+
+__global__ void __launch_bounds__(kTPB) k_fill(float* __restrict__ p, size_t n, float v) {
+    const size_t i = (size_t)blockIdx.x * kTPB + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// The minibatch (draw_batch with the counter draw): slot s -> pixel, its feature column
+// feat[.][s] and target column btgt[.][s] (structure of arrays, so the evaluation reads coalesced).
+template <class S>
+__global__ void __launch_bounds__(kTPB) k_batch(DevModel m, uint64_t head, int M, int Mcap, const float* __restrict__ zdec,
+                                               const float* __restrict__ tgt, int* __restrict__ bidx,
+                                               float* __restrict__ feat, float* __restrict__ btgt) {
+    const int s = blockIdx.x * kTPB + threadIdx.x;
+    if (s >= M) return;
+    const uint32_t u = (uint32_t)(noise_bits(head, (uint64_t)s) >> 32);
+    const int idx = (int)noise_uniform(u, (uint32_t)m.npix);
+    bidx[s] = idx;
+    float f[S::kMaxIn];
+    features<S>(m, PlainLatent{ zdec }, idx % m.W, idx / m.W, f);
+    if constexpr (S::kFixed) {
+#pragma unroll
+        for (int i = 0; i < S::kNin; i++) feat[(size_t)i * Mcap + s] = f[i];
+    } else {
+        for (int i = 0; i < m.nin; i++) feat[(size_t)i * Mcap + s] = f[i];
+    }
+    const float* t = tgt + (size_t)idx * m.nout;
+    for (int c = 0; c < m.nout; c++) btgt[(size_t)c * Mcap + s] = t[c];
+}
+
+// Member weights of one ES step: pair i, weight k -> w0 +- sigma * eps (one fused operation each,
+// main.cpp:1856), and eps itself for the update. The noise is the counter draw (NS_MLP, it, i, k).
+__global__ void __launch_bounds__(kTPB) k_perturb(NoiseTables nt, uint64_t seed, uint32_t step, int N, int P, float sigma,
+                                                 const float* __restrict__ w0, float* __restrict__ wsets,
+                                                 float* __restrict__ eps) {
+    const long long t = (long long)blockIdx.x * kTPB + threadIdx.x;
+    if (t >= (long long)N * P) return;
+    const int i = (int)(t / P), k = (int)(t - (long long)i * P);
+    const float e = gauss_at(nt, noise_head(seed, NS_MLP, step, (uint32_t)i), (uint64_t)k);
+    eps[t] = e;
+    const float w = w0[k];
+    wsets[(size_t)(2 * i) * P + k] = __builtin_fmaf(sigma, e, w);
+    wsets[(size_t)(2 * i + 1) * P + k] = __builtin_fmaf(-sigma, e, w);
+}
+
+// Weight sets of one central-difference step: set pair j < P has w_j + h and w_j - h (float-realized,
+// main.cpp:1905), pair P holds two copies of w for the unperturbed loss; hh[j] = wp - wm in double.
+__global__ void __launch_bounds__(kTPB) k_fd_sets(int P, float h, const float* __restrict__ w0, float* __restrict__ wsets,
+                                                 double* __restrict__ hh) {
+    const long long t = (long long)blockIdx.x * kTPB + threadIdx.x;
+    if (t >= (long long)(P + 1) * P) return;
+    const int j = (int)(t / P), k = (int)(t - (long long)j * P);
+    const float w = w0[k];
+    const bool hit = k == j;
+    const float wp = w + h, wm = w - h;
+    wsets[(size_t)(2 * j) * P + k] = hit ? wp : w;
+    wsets[(size_t)(2 * j + 1) * P + k] = hit ? wm : w;
+    if (hit) hh[j] = (double)wp - (double)wm;
+}
+
+// The population evaluation: block (pair, chunk) evaluates both members of the pair on the
+// chunk's minibatch slots; each slot's features are loaded once and run through the two weight
+// vectors, whose uniform addresses put the weights in SGPRs. Per-member weighted squared errors
+// are summed in double and reduced in a fixed order.
+template <class S>
+__global__ void __launch_bounds__(kTPB) k_pop_eval(DevModel m, const float* __restrict__ wsets, int M, int Mcap, int chunk,
+                                                  int chunks, const float* __restrict__ feat,
+                                                  const float* __restrict__ btgt, double* __restrict__ part) {
+    __shared__ double red[kTPB / 64];
+    const int pair = blockIdx.x, ch = blockIdx.y;
+    const float* __restrict__ wp = wsets + (size_t)(2 * pair) * m.P;
+    const float* __restrict__ wn = wp + m.P;
+    const int s0 = ch * chunk, s1 = min(M, s0 + chunk);
+    double ap = 0.0, an = 0.0;
+    for (int s = s0 + (int)threadIdx.x; s < s1; s += kTPB) {
+        float f[S::kMaxIn], t[S::kMaxOut], o[S::kMaxOut];
+        if constexpr (S::kFixed) {
+#pragma unroll
+            for (int i = 0; i < S::kNin; i++) f[i] = feat[(size_t)i * Mcap + s];
+#pragma unroll
+            for (int c = 0; c < S::kNout; c++) t[c] = btgt[(size_t)c * Mcap + s];
+        } else {
+            for (int i = 0; i < m.nin; i++) f[i] = feat[(size_t)i * Mcap + s];
+            for (int c = 0; c < m.nout; c++) t[c] = btgt[(size_t)c * Mcap + s];
+        }
+        mlp_forward<S>(m, wp, f, o);
+        ap += pixel_err_d(m, o, t);
+        mlp_forward<S>(m, wn, f, o);
+        an += pixel_err_d(m, o, t);
+    }
+    ap = block_sum<kTPB>(ap, red);
+    an = block_sum<kTPB>(an, red);
+    if (threadIdx.x == 0) {
+        part[(size_t)(2 * pair) * chunks + ch] = ap;
+        part[(size_t)(2 * pair + 1) * chunks + ch] = an;
+    }
+}
+
+// Per pair: member losses = chunk sums in chunk order / norm; dl = l+ - l-, lsum = (l+ + l-) / 2.
+__global__ void __launch_bounds__(kTPB) k_es_finish(const double* __restrict__ part, int chunks, int N, double norm,
+                                                   double* __restrict__ dl, double* __restrict__ lsum) {
+    const int i = blockIdx.x * kTPB + threadIdx.x;
+    if (i >= N) return;
+    double lp = 0.0, lm = 0.0;
+    for (int j = 0; j < chunks; j++) { lp += part[(size_t)(2 * i) * chunks + j]; lm += part[(size_t)(2 * i + 1) * chunks + j]; }
+    lp /= norm; lm /= norm;
+    dl[i] = lp - lm;
+    lsum[i] = 0.5 * (lp + lm);
+}
+
+// ES update direction (main.cpp:1868-1873): g[k] = sum over pairs in order of (float)dl_i * scale * eps_ik,
+// one fused multiply-add per pair.
+__global__ void __launch_bounds__(kTPB) k_es_grad(int N, int P, float scale, const double* __restrict__ dl,
+                                                 const float* __restrict__ eps, float* __restrict__ grad) {
+    const int k = blockIdx.x * kTPB + threadIdx.x;
+    if (k >= P) return;
+    float g = 0.0f;
+    for (int i = 0; i < N; i++) g = __builtin_fmaf(__fmul_rn((float)dl[i], scale), eps[(size_t)i * P + k], g);
+    grad[k] = g;
+}
+
+// Central differences: dl_j = L(w_j + h) - L(w_j - h), g_j = dl_j / hh_j; pair P gives L(w).
+__global__ void __launch_bounds__(kTPB) k_fd_finish(const double* __restrict__ part, int chunks, int P, double norm,
+                                                   const double* __restrict__ hh, double* __restrict__ dl,
+                                                   double* __restrict__ lsum, float* __restrict__ grad) {
+    const int j = blockIdx.x * kTPB + threadIdx.x;
+    if (j > P) return;
+    double lp = 0.0, lm = 0.0;
+    for (int c = 0; c < chunks; c++) { lp += part[(size_t)(2 * j) * chunks + c]; lm += part[(size_t)(2 * j + 1) * chunks + c]; }
+    lp /= norm; lm /= norm;
+    if (j == P) { lsum[0] = lp; return; }
+    const double d = lp - lm;
+    dl[j] = d;
+    grad[j] = (float)(d / hh[j]);
+}
+
+// Adam (main.cpp:1799-1809): m = fma(b1, m, (1 - b1) g), v = fma(b2, v, ((1 - b2) g) g),
+// theta -= (lr m^) / (sqrt(v^) + eps); c1, c2 come from the host's powf.
+__global__ void __launch_bounds__(kTPB) k_adam(float* __restrict__ theta, const float* __restrict__ g, float* __restrict__ m,
+                                              float* __restrict__ v, size_t n, float lr, float c1, float c2) {
+    const size_t i = (size_t)blockIdx.x * kTPB + threadIdx.x;
+    if (i >= n) return;
+    const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+    const float ob1 = 1.0f - b1, ob2 = 1.0f - b2;
+    const float gi = g[i];
+    const float mi = __builtin_fmaf(b1, m[i], __fmul_rn(ob1, gi));
+    const float vi = __builtin_fmaf(b2, v[i], __fmul_rn(__fmul_rn(ob2, gi), gi));
+    m[i] = mi; v[i] = vi;
+    const float mh = mi / c1, vh = vi / c2;
+    theta[i] = theta[i] - (lr * mh) / (__builtin_sqrtf(vh) + eps);
+}
+
+// Full decode (Decoder::decode_full): one pixel per thread.
+template <class S>
+__global__ void __launch_bounds__(kTPB) k_decode(DevModel m, const float* __restrict__ w, const float* __restrict__ z,
+                                                float* __restrict__ img) {
+    const int p = blockIdx.x * kTPB + threadIdx.x;
+    if (p >= m.npix) return;
+    float f[S::kMaxIn], o[S::kMaxOut];
+    features<S>(m, PlainLatent{ z }, p % m.W, p / m.W, f);
+    mlp_forward<S>(m, w, f, o);
+    float* dst = img + (size_t)p * m.nout;
+    for (int c = 0; c < m.nout; c++) dst[c] = o[c];
+}
+
+__global__ void __launch_bounds__(kTPB) k_debug_gauss(NoiseTables nt, uint64_t head, uint64_t index0, size_t n, float* __restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * kTPB + threadIdx.x;
+    if (i < n) out[i] = gauss_at(nt, head, index0 + i);
+}
+
+// ---------------------------------------------------------------- launchers
+void launch_fill(Impl& I, float* p, size_t n, float v) {
+    if (!n) return;
+    hipLaunchKernelGGL(k_fill, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, p, n, v);
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_batch(Impl& I, int it, int M) {
+    const uint64_t head = noise_head(I.d.seed, NS_BATCH_PIX, (uint32_t)it, 0);
+    ProfScope ps(I, "batch");
+    dispatch_shape(I.dm, [&](auto s) {
+        using S = decltype(s);
+        hipLaunchKernelGGL(k_batch<S>, dim3(blocks_for(M, kTPB)), dim3(kTPB), 0, I.stream, I.dm, head, M, I.Mcap, I.zdec, I.tgt,
+                           I.bidx, I.feat, I.btgt);
+    });
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_perturb(Impl& I, int it, float sigma, int N) {
+    const size_t n = (size_t)N * I.P;
+    ProfScope ps(I, "perturb");
+    hipLaunchKernelGGL(k_perturb, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, I.noise, I.d.seed, (uint32_t)it, N, I.P,
+                       sigma, I.w, I.wsets, I.eps_mlp);
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_fd_sets(Impl& I, float h) {
+    const size_t n = (size_t)(I.P + 1) * I.P;
+    ProfScope ps(I, "fd_sets");
+    hipLaunchKernelGGL(k_fd_sets, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, I.P, h, I.w, I.wsets, I.hh);
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks) {
+    ProfScope ps(I, "pop_eval");
+    dispatch_shape(I.dm, [&](auto s) {
+        using S = decltype(s);
+        hipLaunchKernelGGL(k_pop_eval<S>, dim3(pairs, chunks), dim3(kTPB), 0, I.stream, I.dm, I.wsets, M, I.Mcap, chunk, chunks,
+                           I.feat, I.btgt, I.part);
+    });
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_es_finish(Impl& I, int chunks, int N, double norm) {
+    hipLaunchKernelGGL(k_es_finish, dim3(blocks_for(N, kTPB)), dim3(kTPB), 0, I.stream, I.part, chunks, N, norm, I.dl, I.lsum);
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_es_grad(Impl& I, int /*it*/, float sigma, int N) {
+    const float scale = 1.0f / (2.0f * (float)N * sigma);
+    ProfScope ps(I, "es_grad");
+    hipLaunchKernelGGL(k_es_grad, dim3(blocks_for(I.P, kTPB)), dim3(kTPB), 0, I.stream, N, I.P, scale, I.dl, I.eps_mlp, I.wgrad);
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_fd_finish(Impl& I, int chunks, double norm) {
+    hipLaunchKernelGGL(k_fd_finish, dim3(blocks_for(I.P + 1, kTPB)), dim3(kTPB), 0, I.stream, I.part, chunks, I.P, norm, I.hh,
+                       I.dl, I.lsum, I.wgrad);
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_adam(Impl& I, float* theta, const float* g, float* m, float* v, size_t n, float lr, int t) {
+    const float c1 = 1.0f - powf(0.9f, (float)t), c2 = 1.0f - powf(0.999f, (float)t);
+    ProfScope ps(I, "adam");
+    hipLaunchKernelGGL(k_adam, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, theta, g, m, v, n, lr, c1, c2);
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_decode(Impl& I, const float* z) {
+    ProfScope ps(I, "decode");
+    dispatch_shape(I.dm, [&](auto s) {
+        using S = decltype(s);
+        hipLaunchKernelGGL(k_decode<S>, dim3(blocks_for(I.npix, kTPB)), dim3(kTPB), 0, I.stream, I.dm, I.w, z, I.img);
+    });
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_debug_gauss(Impl& I, uint32_t stream, uint32_t step, uint32_t pair, uint64_t index0, size_t n, float* out) {
+    if (!n) return;
+    const uint64_t head = noise_head(I.d.seed, stream, step, pair);
+    hipLaunchKernelGGL(k_debug_gauss, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, I.noise, head, index0, n, out);
+    NTC_CHECK(hipGetLastError());
+}
+
+}   // namespace ntc_hip

@@ -1,0 +1,153 @@
+// Host-side state of one ntc_cuda::Trainer on gfx950 and the launchers of its kernels.
+//
+// Layout in HBM (all buffers owned by the trainer, allocated at init or grown on first use):
+//   z, zq          latent shadow (Adam's) and the snapped decode copy (zq only with --qes / --dct-q);
+//                  zdec aliases whichever every decode reads; (y, x, c) per level, levels concatenated
+//   w              MLP parameters, per layer W[out][in] row-major then b[out]
+//   wsets          2 x sets x P: the member weight vectors of one ES step (w +- sigma eps_i) or of one
+//                  central-difference step (w with w_j +- h); read by the population evaluation
+//   eps_mlp        N x P Gaussians of the last ES step (consumed by the weight update)
+//   feat, btgt     the minibatch in structure-of-arrays form: feat[nin][Mcap], btgt[nout][Mcap]
+//   eps_lat, dpix  K x nz latent Gaussians and K x W*H per-pixel loss differences of one latent step
+//   tgt            W*H*nout target, interleaved as the caller's
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "device_common.hpp"
+#include "ntc_cuda.h"
+
+#define NTC_CHECK(x)                                                                                          \
+    do {                                                                                                      \
+        hipError_t e_ = (x);                                                                                  \
+        if (e_ != hipSuccess) {                                                                               \
+            fprintf(stderr, "HIP error %s at %s:%d: %s\n", #x, __FILE__, __LINE__, hipGetErrorString(e_));   \
+            exit(1);                                                                                          \
+        }                                                                                                     \
+    } while (0)
+
+namespace ntc_hip {
+
+// --dct-q level 0 as the kernels see it (by value)
+struct DevDct {
+    int live, C, BW, BH, dc_step, deadzone, lo_w16, rate_es, rate_trunc, n;   // n = BW * BH * C
+    float rate_scale;
+    float lam_t16[16];
+    float basis[64];     // [u * 8 + x], the caller's bit patterns
+    int zigzag[64];
+};
+
+struct KernelTimes {
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+    double total_ms = 0.0;
+    long long launches = 0;
+};
+
+}   // namespace ntc_hip
+
+struct ntc_cuda::Trainer::Impl {
+    ModelDesc d;
+    ntc_hip::DevModel dm{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    ntc_hip::NoiseTables noise{};
+    int P = 0;
+    size_t nz = 0, npix = 0;
+
+    float *z = nullptr, *zq = nullptr, *zdec = nullptr, *zgrad = nullptr, *zm = nullptr, *zv = nullptr, *ztmp = nullptr;
+    float *w = nullptr, *wgrad = nullptr, *wm = nullptr, *wv = nullptr;
+    float *tgt = nullptr, *img = nullptr;
+    float *feat = nullptr, *btgt = nullptr;
+    int* bidx = nullptr;
+    int Mcap = 0;
+    float* wsets = nullptr;
+    size_t wsets_cap = 0;      // floats
+    float* eps_mlp = nullptr;
+    double *part = nullptr, *dl = nullptr, *lsum = nullptr, *hh = nullptr;
+    size_t part_cap = 0;
+    int pairs_cap = 0;
+    float *eps_lat = nullptr, *dpix = nullptr;
+    int Kcap = 0;
+    int* ranges = nullptr;     // per level: xb[W] xe[W] yb[H] ye[H] (pixel footprint of each texel row / column)
+    float* qat_grid = nullptr; // 9 x 257
+    int* qat_bits = nullptr;   // MAX_CH
+
+    bool qes = false;
+    ntc_cuda::QesDesc* qes_dev = nullptr;
+    float* qgrid = nullptr;
+
+    bool dct = false, dct_live = false, dct_rate_es = false, dct_rate_trunc = false;
+    ntc_hip::DevDct ddct{};
+    int16_t* dct_sym = nullptr;
+    uint8_t* dct_code = nullptr;
+    int* dct_step = nullptr;
+    int32_t *dct_bits = nullptr, *dct_dbits = nullptr;   // dbits: Kcap x n (pair k's bit differences)
+    int* dct_cnt = nullptr;    // ntrunc, nz_before (last snap), hits (last lat_step)
+    int dct_evals = 0, dct_last_K = 0;
+
+    int mlp_t = 0, lat_t = 0, lat_step_no = 0;
+    int last_N = 0, last_M = 0, last_chunk = 1;
+    bool last_fd = false;
+
+    std::string dev_name, arch;
+    int cus = 0, rt_ver = 0;
+    const char* shape_name = "runtime";
+
+    bool profiling = false;
+    std::map<std::string, ntc_hip::KernelTimes> times;
+};
+
+namespace ntc_hip {
+using Impl = ntc_cuda::Trainer::Impl;
+
+// profiling: events around one launch on the trainer's stream
+struct ProfScope {
+    Impl& I; const char* name; hipEvent_t a = nullptr, b = nullptr;
+    ProfScope(Impl& I_, const char* n) : I(I_), name(n) {
+        if (I.profiling) { NTC_CHECK(hipEventCreate(&a)); NTC_CHECK(hipEventCreate(&b)); NTC_CHECK(hipEventRecord(a, I.stream)); }
+    }
+    ~ProfScope() {
+        if (I.profiling) { NTC_CHECK(hipEventRecord(b, I.stream)); I.times[name].pending.emplace_back(a, b); }
+    }
+};
+void resolve_times(Impl& I);
+
+inline int blocks_for(size_t n, int tpb) { return (int)((n + tpb - 1) / tpb); }
+
+// noise tables (one pair per device, filled from the host C library on first use)
+NoiseTables noise_tables_for_device(int device);
+
+// kernels_mlp.hip
+void launch_fill(Impl& I, float* p, size_t n, float v);
+void launch_batch(Impl& I, int it, int M);
+void launch_perturb(Impl& I, int it, float sigma, int N);
+void launch_fd_sets(Impl& I, float h);
+void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks);
+void launch_es_finish(Impl& I, int chunks, int N, double norm);
+void launch_es_grad(Impl& I, int it, float sigma, int N);
+void launch_fd_finish(Impl& I, int chunks, double norm);
+void launch_adam(Impl& I, float* theta, const float* g, float* m, float* v, size_t n, float lr, int t);
+void launch_decode(Impl& I, const float* z);
+void launch_debug_gauss(Impl& I, uint32_t stream, uint32_t step, uint32_t pair, uint64_t index0, size_t n, float* out);
+
+// kernels_latent.hip
+void launch_lat_eps(Impl& I, int K, unsigned mask);
+void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask);
+void launch_lat_gather(Impl& I, int level, int K, float scale, bool rate);
+void launch_qat_search(Impl& I);
+
+// kernels_quant.hip
+void launch_qes_snap(Impl& I);
+void launch_dct_clamp0(Impl& I);
+void launch_dct_snap(Impl& I);
+void launch_dct_recon(Impl& I);
+void launch_dct_rate_pairs(Impl& I, int K, float sigma);
+void launch_shadow_pull(Impl& I, size_t off, size_t n, float f);
+
+}   // namespace ntc_hip

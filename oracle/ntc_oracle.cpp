@@ -356,6 +356,10 @@ void or_gauss_fill(uint64_t seed, uint32_t stream, uint32_t step, uint32_t pair,
 }
 float or_gauss_radius(uint32_t k1) { return radius_of(k1); }
 float or_gauss_cosine(uint32_t k2) { return cosine_of(k2); }
+void or_gauss_factors(uint32_t k0, long long n, float* rad, float* cosv) {
+#pragma omp parallel for schedule(static)
+    for (long long i = 0; i < n; i++) { rad[i] = radius_of(k0 + (uint32_t)i); cosv[i] = cosine_of(k0 + (uint32_t)i); }
+}
 
 long long or_model_nparams(const OrModel* m) { return nparams(*m); }
 long long or_model_nz(const OrModel* m) { return nzof(*m); }
@@ -772,6 +776,11 @@ void or_dct_rate_pair(const OrDct* d, const OrLevel* L0, const float* z, const f
             }
             dbits[b * Q.C + c] = bb[0] - bb[1];
         }
+}
+
+// the host branch of --dct-shadow-pull, main.cpp:4142-4146 (the reference's build fuses the update)
+void or_shadow_pull(float* z, const float* zq, long long n, float f) {
+    for (long long i = 0; i < n; i++) z[i] = fmaf(f, zq[i] - z[i], z[i]);
 }
 
 // ntcb_f32_to_f16 / ntcb_f16_to_f32, main.cpp:2427-2455: binary16 with round-half-even

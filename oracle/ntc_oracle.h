@@ -67,6 +67,7 @@ void or_gauss_fill(uint64_t seed, uint32_t stream, uint32_t step, uint32_t pair,
 /* the two factors of the Gaussian for one 24-bit draw: sqrtf(-2 logf(u1)) and cosf(2 pi u2) */
 float or_gauss_radius(uint32_t k1);
 float or_gauss_cosine(uint32_t k2);
+void or_gauss_factors(uint32_t k0, long long n, float* rad, float* cosv);
 
 /* ---- model geometry and MLP ---- */
 long long or_model_nparams(const OrModel* m);
@@ -132,6 +133,9 @@ void or_dct_snap_level0(const OrDct* d, const OrLevel* L0, float* z, float* zq, 
 void or_dct_recon_level0(const OrDct* d, const OrLevel* L0, float* zq, int32_t* bits);
 void or_dct_probe_codes(const OrModel* m, const float* p, const float* zdec, const OrDct* d, uint8_t* code);
 void or_dct_rate_pair(const OrDct* d, const OrLevel* L0, const float* z, const float* eps0, float sg, int32_t* dbits);
+
+/* ---- --dct-shadow-pull (main.cpp:4142-4146): z += f * (zq - z) on n values */
+void or_shadow_pull(float* z, const float* zq, long long n, float f);
 
 /* ---- fp16 weight rounding (main.cpp:2427-2481) and post-hoc latent quantization (main.cpp:478-482) ---- */
 uint16_t or_f32_to_f16(float f, int* overflow);

@@ -116,6 +116,15 @@ class Model:
         return m
 
 
+def model_of(layout) -> OrModel:
+    """OrModel of any layout-like object (W, H, levels, hidden, T, pos, leak, clamp_out, weights)."""
+    if isinstance(layout, OrModel):
+        return layout
+    m = Model(layout.W, layout.H, list(layout.levels), list(layout.hidden), T=layout.T, pos=list(layout.pos),
+              leak=layout.leak, clamp_out=layout.clamp_out, weights=layout.weights)
+    return m.to_c()
+
+
 def _f(a):
     return a.ctypes.data_as(C.POINTER(C.c_float))
 
@@ -141,6 +150,8 @@ _SIGS = {
     "noise_uniform": (C.c_uint32, [C.c_uint32, C.c_uint32]),
     "gauss_fill": (None, [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, C.c_longlong, _P]),
     "gauss_radius": (C.c_float, [C.c_uint32]),
+    "gauss_factors": (None, [C.c_uint32, C.c_longlong, _P, _P]),
+    "shadow_pull": (None, [_P, _P, C.c_longlong, C.c_float]),
     "gauss_cosine": (C.c_float, [C.c_uint32]),
     "features": (None, [_P, _P, C.c_int, C.c_int, _P]),
     "mlp_forward": (None, [_P, _P, _P, _P]),
@@ -238,31 +249,96 @@ class Lib:
         return out
 
     # ---- decoder
-    def features(self, m: Model, z, px, py):
+    def features(self, m, z, px, py):
+        mc = model_of(m)
         f = np.zeros(128, np.float32)
-        self._features(C.byref(m.to_c()), z.ctypes.data, px, py, f.ctypes.data)
-        return f[: m.nin]
+        self._features(C.byref(mc), z.ctypes.data, px, py, f.ctypes.data)
+        return f[: mc.nin]
 
-    def mlp_forward(self, m: Model, p, x):
+    def mlp_forward(self, m, p, x):
+        mc = model_of(m)
         out = np.zeros(12, np.float32)
-        self._mlp_forward(C.byref(m.to_c()), p.ctypes.data, np.ascontiguousarray(x, np.float32).ctypes.data,
+        self._mlp_forward(C.byref(mc), p.ctypes.data, np.ascontiguousarray(x, np.float32).ctypes.data,
                           out.ctypes.data)
-        return out[: m.nout]
+        return out[: mc.nout]
 
-    def decode_full(self, m: Model, p, z):
-        img = np.zeros(m.W * m.H * m.nout, np.float32)
-        self._decode_full(C.byref(m.to_c()), p.ctypes.data, z.ctypes.data, img.ctypes.data)
+    def decode_full(self, m, p, z):
+        mc = model_of(m)
+        img = np.zeros(mc.W * mc.H * mc.nout, np.float32)
+        self._decode_full(C.byref(mc), p.ctypes.data, z.ctypes.data, img.ctypes.data)
         return img
 
-    def decode_err(self, m: Model, p, z, tgt):
-        err = np.zeros(m.W * m.H, np.float32)
-        self._decode_err(C.byref(m.to_c()), p.ctypes.data, z.ctypes.data, tgt.ctypes.data, err.ctypes.data)
+    def decode_err(self, m, p, z, tgt):
+        mc = model_of(m)
+        err = np.zeros(mc.W * mc.H, np.float32)
+        self._decode_err(C.byref(mc), p.ctypes.data, z.ctypes.data, tgt.ctypes.data, err.ctypes.data)
         return err
 
-    def loss_subset(self, m: Model, p, z, tgt, idx):
+    def loss_subset(self, m, p, z, tgt, idx):
         idx = np.ascontiguousarray(idx, np.int32)
-        return self._loss_subset(C.byref(m.to_c()), p.ctypes.data, z.ctypes.data, tgt.ctypes.data, idx.ctypes.data,
-                                 len(idx))
+        return self._loss_subset(C.byref(model_of(m)), p.ctypes.data, z.ctypes.data, tgt.ctypes.data,
+                                 idx.ctypes.data, len(idx))
+
+    # ---- oracle-only training pieces (prefix or_)
+    def draw_batch(self, seed, it, M, npix):
+        idx = np.empty(M, np.int32)
+        self._draw_batch(seed, it, M, npix, idx.ctypes.data)
+        return idx
+
+    def mlp_es_eval(self, m, p0, z, tgt, seed, it, sigma, N, idx):
+        """per pair: dl, lsum, l+, l- (MlpTrainer::step's pair loop)"""
+        idx = np.ascontiguousarray(idx, np.int32)
+        dl, ls, lp, lm = (np.zeros(N) for _ in range(4))
+        self._mlp_es_eval(C.byref(model_of(m)), p0.ctypes.data, z.ctypes.data, tgt.ctypes.data, seed, it, sigma, N,
+                          idx.ctypes.data, len(idx), dl.ctypes.data, ls.ctypes.data, lp.ctypes.data, lm.ctypes.data)
+        return dl, ls, lp, lm
+
+    def mlp_es_grad(self, P, N, seed, it, sigma, dl):
+        g = np.zeros(P, np.float32)
+        dl = np.ascontiguousarray(dl, np.float64)
+        self._mlp_es_grad(P, N, seed, it, sigma, dl.ctypes.data, g.ctypes.data)
+        return g
+
+    def adam(self, theta, g, m, v, lr, t):
+        """in place on theta, m, v (float32 arrays)"""
+        self._adam(theta.ctypes.data, np.ascontiguousarray(g, np.float32).ctypes.data, m.ctypes.data, v.ctypes.data,
+                   theta.size, lr, t)
+
+    def mlp_fd_eval(self, m, p0, z, tgt, h, idx):
+        idx = np.ascontiguousarray(idx, np.int32)
+        P = p0.size
+        dl, hh = np.zeros(P), np.zeros(P)
+        l0 = C.c_double()
+        self._mlp_fd_eval(C.byref(model_of(m)), p0.ctypes.data, z.ctypes.data, tgt.ctypes.data, h, idx.ctypes.data,
+                          len(idx), dl.ctypes.data, hh.ctypes.data, C.addressof(l0))
+        return dl, hh, l0.value
+
+    def fd_grad(self, dl, hh):
+        g = np.zeros(dl.size, np.float32)
+        self._fd_grad(dl.size, np.ascontiguousarray(dl).ctypes.data, np.ascontiguousarray(hh).ctypes.data,
+                      g.ctypes.data)
+        return g
+
+    def lat_grad(self, m, p, zdec, zshadow, tgt, seed, step_no, sigma, K, mask, dct=None, rate_scale=0.0,
+                 want_dpix=False):
+        mc = model_of(m)
+        nz = sum(mc.lv[l].W * mc.lv[l].H * mc.lv[l].C for l in range(mc.nlev))
+        g = np.zeros(nz, np.float32)
+        dpix = np.zeros(K * mc.W * mc.H, np.float32) if want_dpix else None
+        nbc = dct.BW * dct.BH * dct.C if dct is not None else 0
+        dbits = np.zeros(max(nbc, 1), np.int32)
+        hits = C.c_int()
+        self._lat_grad(C.byref(mc), p.ctypes.data, zdec.ctypes.data, zshadow.ctypes.data, tgt.ctypes.data, seed,
+                       step_no, sigma, K, mask, C.byref(dct) if dct is not None else None, rate_scale, g.ctypes.data,
+                       dpix.ctypes.data if dpix is not None else None, dbits.ctypes.data, C.addressof(hits))
+        return g, dpix, dbits[:nbc], hits.value
+
+    def qat_search(self, m, p, z, tgt, ch_bits, grid):
+        """in place on level 0 of z"""
+        bits = np.zeros(16, np.int32)
+        bits[: len(ch_bits)] = ch_bits
+        self._qat_search(C.byref(model_of(m)), p.ctypes.data, z.ctypes.data, tgt.ctypes.data, bits.ctypes.data,
+                         np.ascontiguousarray(grid, np.float32).ctypes.data)
 
 
 def oracle() -> Lib:

@@ -1,0 +1,181 @@
+"""HIP kernels through the C ABI against the oracle, on identical seeded inputs.
+
+Bars: noise, minibatch indices, --qes indices and values, DCT symbols / codes / planes / bit counts
+and Adam / ES-update arithmetic are bit-exact; per-member ES losses within 1e-5 relative (the
+north-star bar); decoded values within 2e-6 absolute (the device's expf against the host C
+library's is the only difference on this path); latent gradients within 1e-3 of their RMS (the
+reference's own --cuda-check bar, main.cpp:3088); qat selectors equal except on texels whose two
+candidates have cell losses equal to 1e-6 relative (main.cpp:3143-3144)."""
+import numpy as np
+import pytest
+
+from neural_block_textures_amd import synth
+from tests.gpu_common import LAYOUTS, data, rel, say, trainer
+
+pytestmark = pytest.mark.gpu
+NAMES = list(LAYOUTS)
+
+
+def test_noise_factors_exhaustive(orc):
+    """Every one of the 2^24 values of each Box-Muller factor on the device equals the host's."""
+    lay = LAYOUTS["rgb_16x2"]
+    z, p, tgt = data(lay, 1)
+    tr = trainer(lay, z, p, tgt)
+    n = 1 << 24
+    rad_d, cos_d = tr.debug_noise_factors(0, n)
+    rad_h, cos_h = np.empty(n, np.float32), np.empty(n, np.float32)
+    orc._gauss_factors(0, n, rad_h.ctypes.data, cos_h.ctypes.data)
+    assert np.array_equal(rad_d.view(np.uint32), rad_h.view(np.uint32))
+    assert np.array_equal(cos_d.view(np.uint32), cos_h.view(np.uint32))
+    for stream, step, pair in [(1, 0, 0), (2, 7, 4095), (3, 123456, 0), (1, 2**20, 3)]:
+        say("gauss stream", stream, step, pair)
+        g = tr.debug_gauss(stream, step, pair, 0, 1 << 20)
+        want = orc.gauss_fill(5, stream, step, pair, 0, 1 << 20)
+        assert np.array_equal(g.view(np.uint32), want.view(np.uint32))
+    g = tr.debug_gauss(2, 1, 1, 2**40 - 100, 200)
+    assert np.array_equal(g.view(np.uint32), orc.gauss_fill(5, 2, 1, 1, 2**40 - 100, 200).view(np.uint32))
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_decode(orc, name):
+    lay = LAYOUTS[name]
+    say("decode", name)
+    z, p, tgt = data(lay, 2)
+    tr = trainer(lay, z, p, tgt)
+    img = tr.decode_full()
+    want = orc.decode_full(lay, p, z)
+    if lay.clamp_out:
+        assert np.array_equal(img, want)
+    else:
+        assert np.abs(img - want).max() < 2e-6
+        assert (img == want).mean() > 0.95
+    z2 = (z * np.float32(0.5)).astype(np.float32)   # a host-supplied latent
+    assert np.abs(tr.decode_full(z2) - orc.decode_full(lay, p, z2)).max() < 2e-6
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_mlp_es_step(orc, name):
+    lay = LAYOUTS[name]
+    say("mlp es", name)
+    z, p, tgt = data(lay, 3)
+    N, M, seed, it, sigma, lr = 24, 1500, 5, 7, 0.02, 0.005
+    tr = trainer(lay, z, p, tgt, max_pairs=N, max_batch=M, seed=seed)
+    tr.mlp_step(it, sigma, lr, N, M)
+    idx = orc.draw_batch(seed, it, M, lay.W * lay.H)
+    assert np.array_equal(tr.debug_last_batch(), idx)
+    lp, lm = tr.debug_last_losses()
+    dl_o, _, lp_o, lm_o = orc.mlp_es_eval(lay, p, z, tgt, seed, it, sigma, N, idx)
+    assert rel(lp, lp_o).max() < 1e-5 and rel(lm, lm_o).max() < 1e-5
+    dl = tr.debug_last_dl()
+    assert np.abs(dl - dl_o).max() / np.sqrt((dl_o ** 2).mean()) < 1e-3
+    # the update from the device's own pair differences is the oracle's, bit for bit
+    g = orc.mlp_es_grad(p.size, N, seed, it, sigma, dl)
+    pw, m, v = p.copy(), np.zeros_like(p), np.zeros_like(p)
+    orc.adam(pw, g, m, v, lr, 1)
+    _, p_dev = tr.download_model()
+    assert np.array_equal(p_dev, pw)
+    loss, dstd = tr.mlp_stats()
+    assert abs(loss - 0.5 * (lp + lm).mean()) < 1e-12 and dstd > 0
+
+
+@pytest.mark.parametrize("name", ["rgb_16x2", "material", "runtime"])
+def test_mlp_es_two_steps_and_fd(orc, name):
+    lay = LAYOUTS[name]
+    say("mlp es+fd", name)
+    z, p, tgt = data(lay, 4)
+    N, M, seed = 8, 700, 9
+    tr = trainer(lay, z, p, tgt, max_pairs=N, max_batch=M, seed=seed)
+    pw, m, v = p.copy(), np.zeros_like(p), np.zeros_like(p)
+    for t, it in [(1, 3), (2, 4)]:
+        tr.mlp_step(it, 0.02, 0.005, N, M)
+        orc.adam(pw, orc.mlp_es_grad(p.size, N, seed, it, 0.02, tr.debug_last_dl()), m, v, 0.005, t)
+    _, p_dev = tr.download_model()
+    assert np.array_equal(p_dev, pw)
+    # central differences after an Adam reset, from the weights the ES steps left
+    tr.reset_mlp_adam()
+    h = np.float32(1e-3)
+    tr.mlp_step_fd(5, h, 0.005, M)
+    idx = orc.draw_batch(seed, 5, M, lay.W * lay.H)
+    dl_o, hh, l0 = orc.mlp_fd_eval(lay, pw, z, tgt, h, idx)
+    dl = tr.debug_last_dl()
+    lp, lm = tr.debug_last_losses()
+    assert dl.size == p.size
+    assert np.abs(dl - dl_o).max() / np.sqrt((dl_o ** 2).mean()) < 1e-3
+    assert rel(lp[0], l0) < 1e-3   # l(w_0 + h) against l(w): same batch, one weight moved by h
+    loss, _ = tr.mlp_stats()
+    assert rel(loss, l0) < 1e-5
+    pf, m0, v0 = pw.copy(), np.zeros_like(p), np.zeros_like(p)
+    orc.adam(pf, orc.fd_grad(dl, hh), m0, v0, 0.005, 1)
+    assert np.array_equal(tr.download_model()[1], pf)
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_latent_step(orc, name):
+    lay = LAYOUTS[name]
+    say("latent", name)
+    z, p, tgt = data(lay, 5)
+    K, seed, sigma, lr = 3, 7, 0.05, 0.02
+    tr = trainer(lay, z, p, tgt, seed=seed)
+    tr.lat_step(1, sigma, lr, K)
+    mask = (1 << len(lay.levels)) - 1
+    g_o, _, _, _ = orc.lat_grad(lay, p, z, z, tgt, seed, 0, sigma, K, mask)
+    g = tr.debug_last_zgrad()
+    rms = np.sqrt((g_o.astype(np.float64) ** 2).mean())
+    assert np.abs(g - g_o).max() < 1e-3 * rms
+    zz, m, v = z.copy(), np.zeros_like(z), np.zeros_like(z)
+    orc.adam(zz, g, m, v, lr, 1)
+    assert np.array_equal(tr.download_model()[0], zz)
+    # the second step keys its noise with step 1
+    tr.lat_step(2, sigma, lr, K)
+    g2_o, _, _, _ = orc.lat_grad(lay, p, zz, zz, tgt, seed, 1, sigma, K, mask)
+    assert np.abs(tr.debug_last_zgrad() - g2_o).max() < 1e-3 * np.sqrt((g2_o.astype(np.float64) ** 2).mean())
+
+
+QAT = {"material": [2, 3], "dct_plane": [1], "runtime": [2, 1, 3]}
+
+
+@pytest.mark.parametrize("name", list(QAT))
+def test_qat_search_and_frozen_level(orc, name):
+    lay = LAYOUTS[name]
+    bits = QAT[name]
+    say("qat", name)
+    grid = synth.qat_grid()
+    z, p, tgt = data(lay, 6)
+    n0 = lay.levels[0][0] * lay.levels[0][1] * lay.levels[0][2]
+    C0 = lay.levels[0][2]
+    lv0 = z[:n0].reshape(-1, C0)
+    for c in range(C0):
+        lv0[:, c] = synth.qat_snap(lv0[:, c], bits[c], grid)
+    z[:n0] = lv0.reshape(-1)
+    tr = trainer(lay, z, p, tgt, qat_bits=bits, qat_grid=grid)
+    # latent step with level 0 frozen: its gradient is exactly zero
+    tr.lat_step(1, 0.05, 0.0, 2)
+    g = tr.debug_last_zgrad()
+    assert not g[:n0].any()
+    mask = ((1 << len(lay.levels)) - 1) & ~1
+    g_o, _, _, _ = orc.lat_grad(lay, p, z, z, tgt, 5, 0, 0.05, 2, mask)
+    assert np.abs(g - g_o).max() < 1e-3 * np.sqrt((g_o.astype(np.float64) ** 2).mean())
+    tr.qat_search()
+    zg = tr.download_model()[0]
+    zc = z.copy()
+    orc.qat_search(lay, p, zc, tgt, bits, grid)
+    assert np.array_equal(zg[n0:], z[n0:])            # only level 0 moves
+    assert not np.array_equal(zc[:n0], z[:n0])        # the search did something
+    diff = np.nonzero((zg[:n0] != zc[:n0]).reshape(-1, C0).any(1))[0]
+    say("qat differing texels", diff.size, "of", n0 // C0)
+    assert diff.size <= max(2, n0 // C0 // 100)
+    if diff.size:   # each must be a near tie: equal cell losses to 1e-6 on the oracle
+        ec = orc.decode_err(lay, p, zc, tgt)
+        eg = orc.decode_err(lay, p, zg, tgt)
+        W0, H0 = lay.levels[0][0], lay.levels[0][1]
+        for t in diff:
+            tx, ty = t % W0, t // W0
+            xs = [px for px in range(lay.W) if min(W0 - 1, int(np.floor((px + 0.5) / lay.W * W0))) == tx]
+            ys = [py for py in range(lay.H) if min(H0 - 1, int(np.floor((py + 0.5) / lay.H * H0))) == ty]
+            cc = sum(float(ec[y * lay.W + x]) for y in ys for x in xs)
+            cg = sum(float(eg[y * lay.W + x]) for y in ys for x in xs)
+            assert abs(cc - cg) <= 1e-6 * max(cc, cg) + 1e-12
+    # every level-0 value is on its channel's grid
+    for c in range(C0):
+        col = zg[:n0].reshape(-1, C0)[:, c]
+        assert np.array_equal(synth.qat_snap(col, bits[c], grid), col)

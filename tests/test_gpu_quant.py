@@ -1,0 +1,195 @@
+"""--qes and --dct-q on the device against the oracle, exact (the reference's --cuda-check items 6
+and 7, main.cpp:3152-3216): the snapped copy, the symbols, the plane, the scale codes, the proxy
+bits, the truncation counts, the rate-pass bit differences and hit count."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from neural_block_textures_amd.trainer import DctDesc, Layout, QesDesc
+from oracle.oracle import OrDct, OrLevel
+from tests.gpu_common import LAYOUTS, data, say, trainer
+
+pytestmark = pytest.mark.gpu
+
+
+def qes_tables(orc, lay, z, bits_per_level):
+    q = QesDesc()
+    grid_all = []
+    off = 0
+    for l, bits in enumerate(bits_per_level):
+        w, h, c, nr = lay.levels[l]
+        if bits:
+            L = OrLevel(w, h, c, int(nr), 0)
+            lo, hi, rg = (np.zeros(c, np.float32) for _ in range(3))
+            grid = np.zeros(c << bits, np.float32)
+            orc._qes_fit(C.byref(L), z[off:].ctypes.data, bits, lo.ctypes.data, hi.ctypes.data, rg.ctypes.data,
+                         grid.ctypes.data)
+            q.bits[l] = bits
+            for ch in range(c):
+                q.lo[l][ch], q.hi[l][ch], q.range[l][ch] = lo[ch], hi[ch], rg[ch]
+                q.grid_off[l][ch] = sum(g.size for g in grid_all) + ch * (1 << bits)
+            grid_all.append(grid)
+        off += w * h * c
+    q.live, q.frozen = 1, 1
+    return q, np.concatenate(grid_all)
+
+
+def host_snap(orc, lay, q, grid, z):
+    """Decoder::qes_refresh on a copy of the shadow: (clamped shadow, snapped copy)"""
+    z = z.copy()
+    zq = z.copy()
+    off = 0
+    for l, (w, h, c, nr) in enumerate(lay.levels):
+        n = w * h * c
+        if q.bits[l]:
+            L = OrLevel(w, h, c, int(nr), 0)
+            lo = np.array(q.lo[l][:c], np.float32); hi = np.array(q.hi[l][:c], np.float32)
+            rg = np.array(q.range[l][:c], np.float32)
+            g = grid[q.grid_off[l][0]:q.grid_off[l][0] + (c << q.bits[l])].copy()
+            zl, zql = z[off:off + n].copy(), np.zeros(n, np.float32)
+            orc._qes_snap_level(C.byref(L), int(q.bits[l]), lo.ctypes.data, hi.ctypes.data, rg.ctypes.data,
+                                g.ctypes.data, zl.ctypes.data, zql.ctypes.data, 1)
+            z[off:off + n], zq[off:off + n] = zl, zql
+        off += n
+    return z, zq
+
+
+@pytest.mark.parametrize("name,bits", [("two_level", [0, 5]), ("rgb_24x2", [6]), ("runtime", [0, 3, 12])])
+def test_qes_snap(orc, name, bits):
+    lay = LAYOUTS[name]
+    say("qes", name, bits)
+    z, p, tgt = data(lay, 11)
+    tr = trainer(lay, z, p, tgt, qes_bits=bits)
+    assert np.array_equal(tr.download_zq(), z)          # not live yet: the copy is the shadow
+    q, grid = qes_tables(orc, lay, z, bits)
+    tr.set_qes(q, grid)
+    zs, zq = host_snap(orc, lay, q, grid, z)
+    assert np.array_equal(tr.download_zq(), zq)
+    tr.lat_step(1, 0.05, 0.05, 2)                       # Adam moves the shadow, then the frozen snap
+    zd, _ = tr.download_model()
+    zs2, zq2 = host_snap(orc, lay, q, grid, zd)
+    assert np.array_equal(zd, zs2)                      # the device already clamped the shadow
+    assert np.array_equal(tr.download_zq(), zq2)
+    assert (zq2 != zq).any()
+
+
+def dct_tables(orc):
+    b, zz, ak = np.zeros(64, np.float32), np.zeros(64, np.int32), np.zeros(16, np.float32)
+    orc.lib.or_dct_tables(b.ctypes.data, zz.ctypes.data, ak.ctypes.data)
+    return b, zz
+
+
+class HostDct:
+    """The host side of a DCT-coded level 0: codes, symbols, steps, bits (the oracle computes them)."""
+
+    def __init__(self, orc, lay, q, dc_step=4, deadzone=0, lam=0.0, lo16=4, rate="both"):
+        self.orc = orc
+        W, H, C0, _ = lay.levels[0]
+        self.L0 = OrLevel(W, H, C0, 1, 0)
+        self.C, self.BW, self.BH = C0, W // 8, H // 8
+        self.n = self.BW * self.BH * C0
+        self.steps = np.zeros(C0 * 1024, np.int32)
+        for c in range(C0):
+            orc._dct_build_steps(q[c], dc_step, self.steps[c * 1024:].ctypes.data)
+        self.code = np.zeros(self.n, np.uint8)
+        self.sym = np.zeros(self.n * 64, np.int16)
+        self.rate_es = lam > 0 and rate != "trunc"
+        self.rate_trunc = lam > 0 and rate != "es"
+        gk = lambda k: (14 / 64) * 2 ** (0.6 * k)
+        self.lam_t16 = np.array([np.float32(lam / (gk(k) * gk(k) * 16.0)) if self.rate_trunc else 0.0
+                                 for k in range(16)], np.float32)
+        self.rate_scale = np.float32(lam / (16.0 * 65025.0 * lay.W * lay.H)) if self.rate_es else np.float32(0)
+        self.d = OrDct()
+        self.d.C, self.d.BW, self.d.BH, self.d.dc_step, self.d.deadzone, self.d.lo_w16 = C0, self.BW, self.BH, dc_step, deadzone, lo16
+        for k in range(16):
+            self.d.lam_t16[k] = self.lam_t16[k]
+        self.d.step = self.steps.ctypes.data_as(C.POINTER(C.c_int))
+        self.d.code = self.code.ctypes.data_as(C.POINTER(C.c_uint8))
+        self.d.sym = self.sym.ctypes.data_as(C.POINTER(C.c_int16))
+        self.dc_step, self.deadzone, self.lo16 = dc_step, deadzone, lo16
+
+    def desc(self):
+        d = DctDesc()
+        d.live, d.C, d.BW, d.BH, d.N, d.dc_step = 1, self.C, self.BW, self.BH, 8, self.dc_step
+        d.rate_es, d.rate_trunc, d.rate_scale = int(self.rate_es), int(self.rate_trunc), self.rate_scale
+        for k in range(16):
+            d.lam_t16[k] = self.lam_t16[k]
+        d.lo_w16, d.deadzone = self.lo16, self.deadzone
+        return d
+
+    def probe(self, lay, p, zdec):
+        self.orc._dct_probe_codes(C.byref(__import__("oracle.oracle", fromlist=["model_of"]).model_of(lay)),
+                                  p.ctypes.data, zdec.ctypes.data, C.byref(self.d), self.code.ctypes.data)
+
+    def snap(self, z):
+        """dct_snap_level0 on a copy: (clamped shadow, plane, bits, counts); symbols land in self.sym"""
+        n0 = self.L0.W * self.L0.H * self.C
+        zs, zq = z[:n0].copy(), np.zeros(n0, np.float32)
+        bits, cnt = np.zeros(self.n, np.int32), np.zeros(3, np.int64)
+        self.orc._dct_snap_level0(C.byref(self.d), C.byref(self.L0), zs.ctypes.data, zq.ctypes.data, bits.ctypes.data,
+                                  cnt.ctypes.data)
+        return zs, zq, bits, cnt
+
+
+@pytest.mark.parametrize("C0,q,deadzone,lam,rate", [(1, [50], 0, 0.0, "both"), (1, [50], 0, 0.5, "both"),
+                                                    (2, [75, 30], 1, 0.3, "es"), (3, [90, 50, 20], 0, 0.4, "trunc")])
+def test_dct_plane(orc, C0, q, deadzone, lam, rate):
+    lay = Layout(64, 48, [(64, 48, C0, True), (16, 12, 4, False)], [32, 32] if C0 == 1 else [20, 12], leak=0.01)
+    say("dct", C0, q, deadzone, lam, rate)
+    z, p, tgt = data(lay, 12 + C0, zscale=0.7)
+    basis, zz = dct_tables(orc)
+    tr = trainer(lay, z, p, tgt, dct={"C": C0, "dc_step": 4, "q": q}, dct_basis=basis, dct_zigzag=zz)
+    n0 = 64 * 48 * C0
+    zc = np.clip(z[:n0], -1, 1)
+    zd, _ = tr.download_model()
+    assert np.array_equal(zd[:n0], zc) and np.array_equal(tr.download_zq()[:n0], zc)   # the pre-start clamp
+    H = HostDct(orc, lay, q, deadzone=deadzone, lam=lam, rate=rate)
+    H.probe(lay, p, np.concatenate([zc, z[n0:]]))
+    zs, zq, bits, cnt = H.snap(zd)
+    tr.set_dct(H.desc(), H.code, H.sym, H.steps)
+    assert np.array_equal(tr.download_zq()[:n0], zq)                  # k_dct_recon on the host's symbols
+    sym_d, code_d = tr.download_dct()
+    assert np.array_equal(sym_d, H.sym) and np.array_equal(code_d, H.code)
+    # a latent step with lr 0: the rate pass of every pair, then the snap of the unchanged shadow
+    K = 3
+    tr.lat_step(1, 0.05, 0.0, K)
+    zd2, _ = tr.download_model()
+    assert np.array_equal(zd2, zd)
+    bits_d, dbits_d, nt_d, nz_d, hits_d, evals_d = tr.download_dct_rate()
+    zdec = tr.download_zq()
+    g_o, _, dbits_o, hits_o = orc.lat_grad(lay, p, zdec, zd2, tgt, 5, 0, 0.05, K, 3,
+                                           dct=H.d if H.rate_es else None, rate_scale=float(H.rate_scale))
+    if H.rate_es:
+        assert np.array_equal(dbits_d, dbits_o) and hits_d == hits_o and evals_d == H.n * K
+        say("dct rate hits", hits_d, "of", H.n * K)
+    else:
+        assert evals_d == 0
+    g = tr.debug_last_zgrad()
+    assert np.abs(g - g_o).max() < 1e-3 * np.sqrt((g_o.astype(np.float64) ** 2).mean())
+    zs2, zq2, bits2, cnt2 = H.snap(zd2)
+    sym_d, _ = tr.download_dct()
+    assert np.array_equal(sym_d, H.sym) and np.array_equal(tr.download_zq()[:n0], zq2)
+    if lam > 0:
+        assert np.array_equal(bits_d, bits2) and nt_d == cnt2[0] and nz_d == cnt2[1]
+    # a step with lr > 0 moves the shadow; the device snap of it matches the host's
+    tr.lat_step(2, 0.05, 0.02, K)
+    zd3, _ = tr.download_model()
+    zs3, zq3, bits3, cnt3 = H.snap(zd3)
+    assert np.array_equal(zd3[:n0], zs3)
+    sym_d, _ = tr.download_dct()
+    assert np.array_equal(sym_d, H.sym) and np.array_equal(tr.download_zq()[:n0], zq3)
+    if lam > 0:
+        b3, _, nt3, nz3, _, _ = tr.download_dct_rate()
+        assert np.array_equal(b3, bits3) and (nt3, nz3) == (cnt3[0], cnt3[1])
+    # refit: new codes from the host through set_dct, then the shadow pull (main.cpp:4110-4136)
+    H.probe(lay, p, tr.download_zq())
+    zs4, zq4, _, _ = H.snap(zd3)
+    tr.set_dct(H.desc(), H.code, H.sym, H.steps)
+    assert np.array_equal(tr.download_zq()[:n0], zq4)
+    tr.shadow_pull(0, n0, 0.01)
+    zp = zd3[:n0].copy()
+    orc._shadow_pull(zp.ctypes.data, zq4.ctypes.data, n0, 0.01)
+    zs5, zq5, _, _ = H.snap(np.concatenate([zp, zd3[n0:]]))
+    zd5, _ = tr.download_model()
+    assert np.array_equal(zd5[:n0], zs5) and np.array_equal(tr.download_zq()[:n0], zq5)

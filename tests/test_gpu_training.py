@@ -1,0 +1,127 @@
+"""End-to-end: a short training run on the device against the oracle's CPU loop (final PSNR
+within 0.05 dB), and the benchmark workloads at their full sizes through
+size-independent properties (an unperturbed population has exactly zero loss differences and
+equal member losses; member losses of sampled pairs match the oracle on the device's own
+minibatch; frozen levels get exactly zero gradient; every --qat value stays on its grid)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from neural_block_textures_amd import synth
+from neural_block_textures_amd.configs import workloads
+from neural_block_textures_amd.trainer import Layout
+from oracle.oracle import OrTrainCfg, OrTrainState, model_of
+from tests.gpu_common import rel, say, trainer
+
+pytestmark = pytest.mark.gpu
+
+
+def psnr(img, tgt, T):
+    a = np.rint(np.clip(img, 0, 1) * 255.0)
+    b = np.rint(np.clip(tgt, 0, 1) * 255.0)
+    mse = ((a - b) ** 2).mean()
+    return 10 * np.log10(255.0 ** 2 / mse) if mse > 0 else 100.0
+
+
+@pytest.mark.parametrize("qat", [False, True])
+def test_trajectory_psnr(orc, qat):
+    if qat:
+        lay = Layout(64, 64, [(64, 64, 2, True), (16, 16, 4, False)], [32, 32], T=4, leak=0.01)
+        bits = [2, 2]
+        maps = synth.material(21, 64, 64)
+    else:
+        lay = Layout(64, 64, [(16, 16, 4, False)], [16, 16], leak=0.0)
+        bits = None
+        maps = [synth.rgb_texture(21, 64, 64)]
+    tgt = synth.target_from_maps(maps)
+    z, p = synth.init_model(lay, 21, qat_bits=bits)
+    N, M, iters, seed = 16, 2048, 25, 3
+    say("trajectory qat" if qat else "trajectory", iters)
+    tr = trainer(lay, z, p, tgt, max_pairs=N, max_batch=M, seed=seed, qat_bits=bits,
+                 qat_grid=synth.qat_grid() if qat else None)
+    cfg = OrTrainCfg()
+    cfg.seed, cfg.mlp_pairs, cfg.mlp_batch, cfg.mlp_sigma, cfg.mlp_lr = seed, N, M, 0.02, 0.005
+    cfg.lat_pairs, cfg.lat_sigma, cfg.lat_lr, cfg.fd_from, cfg.fd_h = 4, 0.05, 0.02, iters - 4, 1e-3
+    if qat:
+        cfg.qat = 2
+        cfg.qat_ch[0], cfg.qat_ch[1] = 2, 2
+    zo, po = z.copy(), p.copy()
+    wm, wv = np.zeros_like(p), np.zeros_like(p)
+    zm, zv = np.zeros_like(z), np.zeros_like(z)
+    st = OrTrainState()
+    F = lambda a: a.ctypes.data_as(C.POINTER(C.c_float))
+    st.z, st.p, st.wm, st.wv, st.zm, st.zv = F(zo), F(po), F(wm), F(wv), F(zm), F(zv)
+    mc = model_of(lay)
+    for it in range(1, iters + 1):
+        if it == cfg.fd_from:
+            tr.reset_mlp_adam()
+        if it >= cfg.fd_from:
+            tr.mlp_step_fd(it, np.float32(1e-3), 0.005, M)
+        else:
+            tr.mlp_step(it, 0.02, 0.005, N, M)
+        tr.lat_step(it, 0.05, 0.02, 4)
+        if qat:
+            tr.qat_search()
+        orc.lib.or_train_iter(C.byref(mc), C.byref(cfg), C.byref(st), tgt.ctypes.data, it, iters)
+    zg, pg = tr.download_model()
+    ps_gpu = psnr(tr.decode_full(), tgt, lay.T)
+    ps_cpu = psnr(orc.decode_full(lay, po, zo), tgt, lay.T)
+    ps_0 = psnr(orc.decode_full(lay, p, z), tgt, lay.T)
+    say(f"psnr start {ps_0:.3f} gpu {ps_gpu:.3f} cpu {ps_cpu:.3f}")
+    assert ps_cpu > ps_0 + 0.5          # training moved
+    assert abs(ps_gpu - ps_cpu) < 0.05
+
+
+def full_trainer(name, **kw):
+    w = workloads()[name]
+    lay = w.layout
+    maps = synth.material(w.seed, lay.W, lay.H) if lay.T == 4 else [synth.rgb_texture(w.seed, lay.W, lay.H)]
+    tgt = synth.target_from_maps(maps)
+    z, p = synth.init_model(lay, w.seed, qat_bits=w.qat_bits)
+    tr = trainer(lay, z, p, tgt, max_pairs=w.mlp_pairs, max_batch=w.mlp_batch, seed=w.seed, qat_bits=w.qat_bits,
+                 qat_grid=synth.qat_grid() if w.qat_bits else None, **kw)
+    return w, lay, tr, z, p, tgt
+
+
+@pytest.mark.parametrize("name", ["rgb512_two_level", "material512", "material2048"])
+def test_full_size_properties(orc, name):
+    say("full size", name)
+    w, lay, tr, z, p, tgt = full_trainer(name)
+    N, M = w.mlp_pairs, w.mlp_batch
+    tr.mlp_step(1, 0.0, 0.0, N, M)                     # sigma 0: every member is w itself
+    dl = tr.debug_last_dl()
+    lp, lm = tr.debug_last_losses()
+    assert dl.size == N and not dl.any()
+    assert np.all(lp == lp[0]) and np.all(lm == lp[0])
+    idx = tr.debug_last_batch()
+    assert rel(lp[0], orc.loss_subset(lay, p, z, tgt, idx)) < 1e-6
+    tr.mlp_step(2, w.mlp_sigma, w.mlp_lr, N, M)
+    lp, lm = tr.debug_last_losses()
+    idx = tr.debug_last_batch()
+    assert np.isfinite(lp).all() and np.isfinite(lm).all()
+    if M <= 65536:
+        s = np.float64(np.float32(w.mlp_sigma))
+        for i in (0, N // 2, N - 1):                    # sampled pairs on the device's own minibatch
+            eps = orc.gauss_fill(w.seed, 2, 2, i, 0, p.size).astype(np.float64)
+            # w +- sigma eps as one rounding (sigma * eps is exact in double)
+            wp = (p.astype(np.float64) + s * eps).astype(np.float32)
+            wm = (p.astype(np.float64) - s * eps).astype(np.float32)
+            assert rel(lp[i], orc.loss_subset(lay, wp, z, tgt, idx)) < 1e-5
+            assert rel(lm[i], orc.loss_subset(lay, wm, z, tgt, idx)) < 1e-5
+    assert np.isfinite(tr.download_model()[1]).all()
+    tr.lat_step(1, w.lat_sigma, w.lat_lr, w.lat_pairs)
+    g = tr.debug_last_zgrad()
+    assert np.isfinite(g).all()
+    n0 = lay.levels[0][0] * lay.levels[0][1] * lay.levels[0][2]
+    if w.qat_bits:
+        assert not g[:n0].any() and g[n0:].any()
+        tr.qat_search()
+        zq = tr.download_model()[0][:n0].reshape(-1, lay.levels[0][2])
+        grid = synth.qat_grid()
+        for c, b in enumerate(w.qat_bits):
+            assert np.array_equal(synth.qat_snap(zq[:, c], b, grid), zq[:, c])
+    else:
+        assert g[:n0].any()
+    img = tr.decode_full()
+    assert np.isfinite(img).all() and img.min() >= 0 and img.max() <= 1

@@ -1,0 +1,271 @@
+"""The oracle against known answers the reference itself holds (the --dct-selftest items of
+main.cpp:1374-1540 and the fp16 self-check of main.cpp:2456-2470) and against what the
+mathematics fixes (splitmix64's published outputs, Box-Muller moments, closed forms)."""
+import ctypes as C
+
+import numpy as np
+
+from oracle.oracle import Model, model_of
+
+JPEG_ZIGZAG = [0, 1, 8, 16, 9, 2, 3, 10, 17, 24, 32, 25, 18, 11, 4, 5, 12, 19, 26, 33, 40, 48, 41, 34, 27, 20, 13, 6, 7,
+               14, 21, 28, 35, 42, 49, 56, 57, 50, 43, 36, 29, 22, 15, 23, 30, 37, 44, 51, 58, 59, 52, 45, 38, 31, 39, 46,
+               53, 60, 61, 54, 47, 55, 62, 63]
+K1 = [[16, 11, 10, 16, 24, 40, 51, 61], [12, 12, 14, 19, 26, 58, 60, 55], [14, 13, 16, 24, 40, 57, 69, 56],
+      [14, 17, 22, 29, 51, 87, 80, 62], [18, 22, 37, 56, 68, 109, 103, 77], [24, 35, 55, 64, 81, 104, 113, 92],
+      [49, 64, 78, 87, 103, 121, 120, 101], [72, 92, 95, 98, 112, 100, 103, 99]]
+
+
+def tables(orc):
+    b, z, a = np.zeros(64, np.float32), np.zeros(64, np.int32), np.zeros(16, np.float32)
+    orc.lib.or_dct_tables(b.ctypes.data, z.ctypes.data, a.ctypes.data)
+    return b, z, a
+
+
+# ---------------------------------------------------------------- noise
+def test_splitmix64_published_outputs(orc):
+    # splitmix64 seeded with 0: the first two outputs of the published generator
+    assert orc.lib.or_mix64 and True
+    orc.lib.or_mix64.restype = C.c_uint64
+    orc.lib.or_mix64.argtypes = [C.c_uint64]
+    assert orc.lib.or_mix64(0) == 0xE220A8397B1DCDAF
+    assert orc.lib.or_mix64(0x9E3779B97F4A7C15) == 0x6E789E6AA1B965F4
+
+
+def test_gauss_factors_special_values(orc):
+    assert orc._gauss_radius((1 << 24) - 1) == 0.0          # u1 = 1: sqrt(-2 log 1) = 0
+    assert orc._gauss_cosine(0) == 1.0                      # cos 0
+    r0 = orc._gauss_radius(0)                               # u1 = 2^-24: sqrt(48 ln 2)
+    assert abs(r0 - np.sqrt(48 * np.log(2))) < 1e-5
+    assert abs(orc._gauss_cosine(1 << 23) + 1.0) < 1e-6     # cos(pi)
+
+
+def test_gauss_moments_and_uniform(orc):
+    x = orc.gauss_fill(7, 2, 3, 11, 0, 1 << 20).astype(np.float64)
+    assert abs(x.mean()) < 0.005 and abs(x.var() - 1.0) < 0.01
+    assert abs((x ** 4).mean() - 3.0) < 0.05                # Gaussian kurtosis
+    assert orc._noise_uniform(0xFFFFFFFF, 1000) == 999 and orc._noise_uniform(0, 1000) == 0
+    assert orc._noise_uniform(0x80000000, 10) == 5
+
+
+def test_batch_indices_in_range(orc):
+    idx = orc.draw_batch(3, 17, 100000, 1000)
+    assert idx.min() >= 0 and idx.max() < 1000
+    counts = np.bincount(idx, minlength=1000)
+    assert counts.min() > 50 and counts.max() < 160       # uniform draw with replacement
+
+
+# ---------------------------------------------------------------- DCT known answers (--dct-selftest)
+def test_dct_basis_and_ak_definitions(orc):
+    b, _, a = tables(orc)
+    for u in range(8):
+        for x in range(8):
+            alpha = np.sqrt(1 / 8) if u == 0 else np.sqrt(2 / 8)
+            assert b[u * 8 + x] == np.float32(alpha * np.cos(np.pi * (2 * x + 1) * u / 16))
+    for k in range(16):
+        assert a[k] == np.float32(1.0 / ((14 / 64) * 2 ** (0.6 * k)))
+
+
+def test_dct_zigzag_is_jpeg(orc):
+    _, z, _ = tables(orc)
+    assert list(z) == JPEG_ZIGZAG
+
+
+def test_dct_round_trip(orc):
+    rng = np.random.default_rng(12345)
+    mx = 0.0
+    for _ in range(300):
+        w = rng.uniform(0, 64, 64).astype(np.float32)
+        Cf, r = np.zeros(64, np.float32), np.zeros(64, np.float32)
+        orc._dct_fwd8(w.ctypes.data, Cf.ctypes.data)
+        orc._dct_inv8(Cf.ctypes.data, r.ctypes.data)
+        mx = max(mx, float(np.abs(r - w).max()))
+    assert mx < 1e-4
+
+
+def test_dct_steps_k1_at_q50(orc):
+    s = np.zeros(1024, np.int32)
+    orc._dct_build_steps(50, 4, s.ctypes.data)
+    # code k has level scale A_k; A_k = 1 has no code, so check q 50 through the entries of a unit scale:
+    orc.lib.or_dct_build_steps_scaled.argtypes = [C.c_int, C.c_float, C.c_int, C.c_void_p]
+    t = np.zeros(64, np.int32)
+    orc.lib.or_dct_build_steps_scaled(50, 1.0, 4, t.ctypes.data)
+    assert t[0] == 4
+    bad = sum(t[u * 8 + v] != K1[u][v] for u in range(8) for v in range(8) if u or v)
+    badT = sum(t[u * 8 + v] != K1[v][u] for u in range(8) for v in range(8) if u or v)
+    assert bad == 0 and badT > 0
+    orc.lib.or_dct_build_steps_scaled(100, 1.0, 1, t.ctypes.data)
+    assert all(t[1:] == 1)
+    q1 = np.zeros(1024, np.int32)
+    orc._dct_build_steps(1, 4, q1.ctypes.data)
+    ac = q1.reshape(16, 64)[:, 1:]
+    assert ac.min() >= 1 and ac.max() > 1000
+
+
+def test_dct_quantizer_cases(orc):
+    qa = lambda d, L, u, v, dz: orc._dct_quant_ac(d, L, u, v, dz)
+    dq = lambda q, L, u, v, dz: orc._dct_dequant_ac(q, L, u, v, dz)
+    L = 10
+    # dead zone with the first-order exemption
+    assert qa(0.4 * L, L, 1, 0, 1) == 0 and qa(0.6 * L, L, 1, 0, 1) == 1 and qa(0.6 * L, L, 2, 0, 1) == 0
+    assert qa(1.1 * L, L, 2, 0, 1) == 1 and qa(0.99 * L, L, 2, 0, 1) == 0 and qa(1.0 * L, L, 2, 0, 1) == 1
+    assert qa(-1.5 * L, L, 0, 2, 1) == -1
+    assert dq(1, L, 2, 0, 1) == 1.5 * L and dq(3, L, 1, 0, 1) == 3.0 * L and dq(-2, L, 2, 3, 1) == -2.5 * L
+    # plain rounding (--dct-deadzone 0)
+    assert qa(0.4 * L, L, 2, 0, 0) == 0 and qa(0.6 * L, L, 2, 0, 0) == 1 and qa(1.49 * L, L, 2, 0, 0) == 1
+    assert qa(1.5 * L, L, 2, 0, 0) == 2 and qa(-0.6 * L, L, 2, 0, 0) == -1 and qa(-1.5 * L, L, 0, 2, 0) == -2
+    assert qa(2000.0 * L, L, 2, 3, 0) == 1024 and qa(-2000.0 * L, L, 2, 3, 0) == -1024
+    assert dq(1, L, 2, 0, 0) == 1.0 * L and dq(-2, L, 2, 3, 0) == -2.0 * L
+    for k in range(1, 64):
+        for t in range(-30, 31):
+            x = float(np.float32(0.1 * t) * np.float32(L))
+            assert qa(x, L, k // 8, k % 8, 0) == -qa(-x, L, k // 8, k % 8, 0)
+    # DC: round half to even at its step
+    assert orc._dct_quant_dc(2.0, 4) == 0 and orc._dct_quant_dc(6.0, 4) == 2 and orc._dct_quant_dc(10.0, 4) == 2
+
+
+def test_dct_rate_cost_table_and_blocks(orc):
+    ref = [1, 3, 3, 5, 5, 5, 5, 7]
+    orc.lib.or_dct_c_run.argtypes = [C.c_int]
+    orc.lib.or_dct_c_mag.argtypes = [C.c_int]
+    for i in range(8):
+        assert orc.lib.or_dct_c_run(i) == 16 * ref[i] and orc.lib.or_dct_c_mag(i + 1) == 16 * ref[i]
+    assert orc.lib.or_dct_c_run(62) == 176 and orc.lib.or_dct_c_mag(256) == 272
+    z = JPEG_ZIGZAG
+    sym = np.zeros(64, np.int16)
+    sym[z[1]], sym[z[2]], sym[z[5]], sym[z[20]] = -3, 1, 7, -1
+    assert orc._dct_block_bits(sym.ctypes.data, 16) == 28 * 16         # hand-built block
+    lone = np.zeros(64, np.int16)
+    lone[z[63]] = 1
+    assert orc._dct_block_bits(lone.ctypes.data, 16) == 13 * 16        # no EOB
+    assert orc._dct_block_bits(np.zeros(64, np.int16).ctypes.data, 16) == 2 * 16
+
+
+def test_dct_truncation_cases(orc):
+    z = JPEG_ZIGZAG
+    st = np.full(64, 10, np.int32)
+    st[0] = 4
+
+    def run(Cf, lam):
+        sym = np.zeros(64, np.int16)
+        nt, nz = C.c_int(), C.c_int()
+        orc._dct_quantize_block(Cf.ctypes.data, st.ctypes.data, 4, lam, 16, 1, 0, sym.ctypes.data, C.addressof(nt),
+                                C.addressof(nz))
+        return sym, nt.value, nz.value
+
+    Cf = np.zeros(64, np.float32)
+    Cf[z[63]] = 12.0
+    s, nt, nz = run(Cf, 0.7)
+    assert s[z[63]] == 1 and nt == 0 and nz == 1
+    s, nt, _ = run(Cf, 0.8)
+    assert s[z[63]] == 0 and nt == 1
+    Cf = np.zeros(64, np.float32)
+    Cf[z[1]], Cf[z[3]], Cf[z[10]] = 25.0, 12.0, 30.0
+    s, nt, nz = run(Cf, 2.0)
+    assert (s[z[3]], nt, nz, s[z[1]], s[z[10]]) == (1, 0, 3, 3, 3)
+    s, nt, _ = run(Cf, 3.0)
+    assert (s[z[3]], nt, s[z[1]], s[z[10]]) == (0, 1, 3, 3)
+    s, nt, nz = run(Cf, 0.0)
+    assert (nt, nz, s[z[3]]) == (0, 0, 1)
+    Cf = np.zeros(64, np.float32)
+    Cf[z[1]] = 5.0
+    s, nt, nz = run(Cf, 1e-6)
+    assert (s[z[1]], nt, nz) == (0, 1, 1)
+
+
+def test_dct_scale_codes(orc):
+    g = lambda k: (14 / 64) * 2 ** (0.6 * k)
+    assert all(orc._dct_code_of_gain(g(k)) == k for k in range(16))
+    last, x = -1, 0.01
+    while x < 200:
+        k = orc._dct_code_of_gain(x)
+        assert k >= last
+        last, x = k, x * 1.02
+
+
+# ---------------------------------------------------------------- fp16 self-check (main.cpp:2456-2470)
+def test_fp16_selfcheck(orc):
+    ov = C.c_int()
+    f2h = lambda x: orc._f32_to_f16(x, C.addressof(ov))
+    for h in range(65536):
+        if ((h >> 10) & 0x1F) == 0x1F:
+            continue
+        ov.value = 0
+        assert f2h(orc._f16_to_f32(h)) == h and ov.value == 0
+    assert f2h(1.0) == 0x3C00 and f2h(-2.0) == 0xC000 and f2h(65504.0) == 0x7BFF
+    assert f2h(5.9604645e-8) == 0x0001 and f2h(2.9802322e-8) == 0x0000
+    assert f2h(1.00048828) == 0x3C00 and f2h(1.00073242) == 0x3C01
+    ov.value = 0
+    f2h(65520.0)
+    assert ov.value == 1
+
+
+# ---------------------------------------------------------------- closed forms
+def test_qat_grid_closed_form(orc):
+    g = np.zeros(9 * 257, np.float32)
+    orc._qat_grid(g.ctypes.data)
+    g = g.reshape(9, 257)
+    for b in range(1, 9):
+        L = (1 << b) - 1
+        assert g[b, 0] == -1.0 and g[b, L] == 1.0
+        assert np.allclose(g[b, : L + 1], -1 + 2 * np.arange(L + 1) / L, atol=1e-7)
+        for k in range(L + 1):
+            assert orc._qat_index(float(g[b, k]), b) == k
+
+
+def test_texel_center_sampling_is_exact(orc):
+    # W == LW (and H == LH): every pixel centre is a texel centre, so bilinear and nearest
+    # sampling return the texel values themselves
+    for nearest in (0, 1):
+        m = Model(12, 9, [(12, 9, 3, nearest)], [8], T=1, pos=[0])
+        z = np.random.default_rng(2).normal(size=m.nz).astype(np.float32)
+        for py in range(9):
+            for px in range(12):
+                f = orc.features(m, z, px, py)
+                assert np.array_equal(f[:3], z[(py * 12 + px) * 3:(py * 12 + px) * 3 + 3])
+                assert abs(f[3] - ((px + 0.5) / 12 * 2 - 1)) < 1e-6
+
+
+def test_mlp_forward_against_float64(orc):
+    m = Model(16, 16, [(4, 4, 5, 0)], [20, 12], T=2, pos=[0], leak=0.03)
+    rng = np.random.default_rng(4)
+    p = rng.normal(0, 0.4, m.nparams).astype(np.float32)
+    widths = [m.nin, 20, 12, m.nout]
+    for _ in range(50):
+        x = rng.normal(0, 1, m.nin).astype(np.float32)
+        a, o = x.astype(np.float64), 0
+        for l in range(1, 4):
+            W = p[o:o + widths[l] * widths[l - 1]].astype(np.float64).reshape(widths[l], widths[l - 1])
+            o += widths[l] * widths[l - 1]
+            b = p[o:o + widths[l]].astype(np.float64)
+            o += widths[l]
+            s = W @ a + b
+            a = np.where(s > 0, s, 0.03 * s) if l < 3 else 1 / (1 + np.exp(-s))
+        assert np.allclose(orc.mlp_forward(m, p, x), a, rtol=0, atol=2e-6)
+
+
+def test_adam_first_step_closed_form(orc):
+    rng = np.random.default_rng(9)
+    g = rng.normal(0, 1, 1000).astype(np.float32)
+    th = rng.normal(0, 1, 1000).astype(np.float32)
+    t0 = th.copy()
+    m, v = np.zeros_like(th), np.zeros_like(th)
+    orc.adam(th, g, m, v, 0.01, 1)
+    # m^ = g, v^ = g^2 on the first step: theta moves by lr * g / (|g| + eps)
+    assert np.allclose(t0 - th, 0.01 * np.sign(g), atol=2e-6)
+
+
+def test_es_gradient_follows_the_loss(orc):
+    # the antithetic ES estimate on many pairs points along the central-difference gradient
+    m = Model(16, 16, [(4, 4, 2, 0)], [6], T=1, pos=[0], leak=0.01)
+    rng = np.random.default_rng(5)
+    z = rng.normal(0, 0.3, m.nz).astype(np.float32)
+    p = rng.normal(0, 0.5, m.nparams).astype(np.float32)
+    tgt = rng.random(16 * 16 * 3).astype(np.float32)
+    idx = np.arange(256, dtype=np.int32)
+    N = 2000
+    dl, _, _, _ = orc.mlp_es_eval(m, p, z, tgt, 1, 1, 0.01, N, idx)
+    ges = orc.mlp_es_grad(p.size, N, 1, 1, 0.01, dl)
+    dlf, hh, _ = orc.mlp_fd_eval(m, p, z, tgt, np.float32(1e-3), idx)
+    gfd = orc.fd_grad(dlf, hh)
+    cos = float(ges @ gfd / (np.linalg.norm(ges) * np.linalg.norm(gfd)))
+    assert cos > 0.85
