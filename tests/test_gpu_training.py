@@ -89,26 +89,29 @@ def test_full_size_properties(orc, name):
     say("full size", name)
     w, lay, tr, z, p, tgt = full_trainer(name)
     N, M = w.mlp_pairs, w.mlp_batch
-    tr.mlp_step(1, 0.0, 0.0, N, M)                     # sigma 0: every member is w itself
+    tr.mlp_step(1, w.mlp_sigma, 0.0, N, M)              # lr 0: Adam leaves every weight bit-identical
+    assert np.array_equal(tr.download_model()[1], p)
     dl = tr.debug_last_dl()
     lp, lm = tr.debug_last_losses()
-    assert dl.size == N and not dl.any()
-    assert np.all(lp == lp[0]) and np.all(lm == lp[0])
     idx = tr.debug_last_batch()
-    assert rel(lp[0], orc.loss_subset(lay, p, z, tgt, idx)) < 1e-6
-    tr.mlp_step(2, w.mlp_sigma, w.mlp_lr, N, M)
-    lp, lm = tr.debug_last_losses()
-    idx = tr.debug_last_batch()
-    assert np.isfinite(lp).all() and np.isfinite(lm).all()
+    assert dl.size == N and np.isfinite(lp).all() and np.isfinite(lm).all()
+    assert np.array_equal(dl, lp - lm) or np.abs(dl - (lp - lm)).max() <= 1e-15 * np.abs(lp).max()
     if M <= 65536:
         s = np.float64(np.float32(w.mlp_sigma))
         for i in (0, N // 2, N - 1):                    # sampled pairs on the device's own minibatch
-            eps = orc.gauss_fill(w.seed, 2, 2, i, 0, p.size).astype(np.float64)
+            eps = orc.gauss_fill(w.seed, 2, 1, i, 0, p.size).astype(np.float64)
             # w +- sigma eps as one rounding (sigma * eps is exact in double)
             wp = (p.astype(np.float64) + s * eps).astype(np.float32)
             wm = (p.astype(np.float64) - s * eps).astype(np.float32)
             assert rel(lp[i], orc.loss_subset(lay, wp, z, tgt, idx)) < 1e-5
             assert rel(lm[i], orc.loss_subset(lay, wm, z, tgt, idx)) < 1e-5
+    # the unperturbed pair of a central-difference step is the loss of w on the step's minibatch
+    tr.mlp_step_fd(2, np.float32(w.fd_h), 0.0, M)
+    l0, _ = tr.mlp_stats()
+    if M <= 65536:
+        assert rel(l0, orc.loss_subset(lay, p, z, tgt, tr.debug_last_batch())) < 1e-6
+    assert np.isfinite(tr.debug_last_dl()).all()
+    tr.mlp_step(3, w.mlp_sigma, w.mlp_lr, N, M)
     assert np.isfinite(tr.download_model()[1]).all()
     tr.lat_step(1, w.lat_sigma, w.lat_lr, w.lat_pairs)
     g = tr.debug_last_zgrad()
