@@ -107,6 +107,8 @@ def main():
     ap.add_argument("--workload", default="material512")
     ap.add_argument("--fd-steps", type=int, default=5, help="extra timed --mlp-fd iterations, reported apart")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bounded CPU-baseline sample (0 = skip)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="FLOATS",
+                    help="only run a plain device copy of FLOATS floats three times (the reference for memory counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -122,6 +124,17 @@ def main():
 
     w = workloads()[args.workload]
     lay = w.layout
+    if args.copy_calibration:
+        from neural_block_textures_amd.trainer import Layout
+        small = Layout(8, 8, [(8, 8, 4, False)], [16, 16])
+        zc, pc = synth.init_model(small, 1)
+        tc = Trainer()
+        tc.init(Trainer.model_desc(small), zc, pc, np.zeros(8 * 8 * 3, np.float32), small)
+        n = args.copy_calibration & ~3
+        tc.debug_copy_calibration(n, 3)
+        tc.close()
+        print(json.dumps({"copy_calibration": {"floats": n, "bytes_read": 4 * n, "bytes_written": 4 * n, "reps": 3}}))
+        return
     log(f"bench: {w.name} {lay.W}x{lay.H}x{lay.T} levels {lay.levels} mlp {lay.nin}->{lay.hidden}->{lay.nout} "
         f"pairs {w.mlp_pairs} batch {w.mlp_batch}")
     maps = synth.material(w.seed, lay.W, lay.H) if lay.T == 4 else [synth.rgb_texture(w.seed, lay.W, lay.H)]
@@ -186,6 +199,14 @@ def main():
     roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": None,
                 "kernel": "k_pop_eval", "flop_per_launch": pop_flop, "ms_per_launch": pe["ms_mean"]}
+    # HBM bytes per launch from the committed counter runs (FETCH_SIZE and WRITE_SIZE, each scaled by the
+    # same counter's reading for a plain copy of known size): profiles/traffic_<workload>.json
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{w.name}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            t = json.load(f)
+        roofline["traffic"] = t.get("pop_eval_bytes_per_launch")
+        roofline["traffic_source"] = os.path.relpath(tpath, ROOT)
     cpu = None
     if args.cpu_seconds > 0:
         log(f"bench: CPU baseline for {args.cpu_seconds:.0f} s ...")

@@ -118,6 +118,8 @@ size_t ntc_abi_sizeof(const char* name);
 /* the member losses of the last ES step (pair i: member + is w + sigma eps_i, member - is w - sigma eps_i),
  * or for a central-difference step the losses at w_j + h and w_j - h; returns the pair count */
 size_t ntc_trainer_debug_last_losses(const ntc_trainer* t, double* lplus, double* lminus, size_t cap);
+/* the MLP weight gradient of the last ES or central-difference step (before Adam), P floats */
+size_t ntc_trainer_debug_last_wgrad(const ntc_trainer* t, float* g, size_t cap);
 long long ntc_trainer_nparams(const ntc_trainer* t);
 long long ntc_trainer_nz(const ntc_trainer* t);
 void* ntc_trainer_stream(const ntc_trainer* t);        /* the hipStream_t every launch of this trainer uses */
@@ -129,6 +131,9 @@ int ntc_trainer_kernel_time(ntc_trainer* t, const char* name, double* total_ms, 
 /* the device's Gaussian draws for indices index0 .. index0 + n - 1 of one (seed, stream, step, pair) */
 void ntc_trainer_debug_gauss(ntc_trainer* t, uint32_t stream, uint32_t step, uint32_t pair, uint64_t index0, size_t n,
                              float* out);
+/* runs a plain device copy of n floats (n a multiple of 4) reps times on the trainer's stream:
+ * the known-size reference that converts a profile's memory counters into bytes */
+void ntc_trainer_debug_copy_calibration(ntc_trainer* t, size_t n, int reps);
 /* the device's copy of the two Gaussian factors for 24-bit draws k0 .. k0 + n - 1:
  * rad[k] = sqrtf(-2 logf((k + 1) / 2^24)), cosv[k] = cosf(2 pi k / 2^24) */
 void ntc_trainer_debug_noise_factors(ntc_trainer* t, uint32_t k0, size_t n, float* rad, float* cosv);

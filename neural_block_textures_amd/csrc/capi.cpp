@@ -124,6 +124,15 @@ size_t ntc_trainer_debug_last_losses(const ntc_trainer* t, double* lplus, double
     }
     return n;
 }
+size_t ntc_trainer_debug_last_wgrad(const ntc_trainer* t, float* g, size_t cap) {
+    auto& I = *t->t.im;
+    const size_t n = (size_t)I.P;
+    if (g && cap) {
+        NTC_CHECK(hipMemcpyAsync(g, I.wgrad, std::min(cap, n) * sizeof(float), hipMemcpyDeviceToHost, I.stream));
+        NTC_CHECK(hipStreamSynchronize(I.stream));
+    }
+    return n;
+}
 size_t ntc_abi_sizeof(const char* name) {
     const std::string n = name ? name : "";
     if (n == "ntc_model_desc") return sizeof(ntc_model_desc);
@@ -160,6 +169,18 @@ void ntc_trainer_debug_gauss(ntc_trainer* t, uint32_t stream, uint32_t step, uin
     NTC_CHECK(hipMemcpyAsync(out, d, n * sizeof(float), hipMemcpyDeviceToHost, I.stream));
     NTC_CHECK(hipStreamSynchronize(I.stream));
     NTC_CHECK(hipFree(d));
+}
+void ntc_trainer_debug_copy_calibration(ntc_trainer* t, size_t n, int reps) {
+    auto& I = *t->t.im;
+    n &= ~(size_t)3;
+    float *a = nullptr, *b = nullptr;
+    NTC_CHECK(hipMalloc(&a, std::max<size_t>(n, 4) * sizeof(float)));
+    NTC_CHECK(hipMalloc(&b, std::max<size_t>(n, 4) * sizeof(float)));
+    NTC_CHECK(hipMemsetAsync(a, 0, n * sizeof(float), I.stream));
+    for (int r = 0; r < reps; r++) ntc_hip::launch_copy_calibration(I, a, b, n);
+    NTC_CHECK(hipStreamSynchronize(I.stream));
+    NTC_CHECK(hipFree(a));
+    NTC_CHECK(hipFree(b));
 }
 void ntc_trainer_debug_noise_factors(ntc_trainer* t, uint32_t k0, size_t n, float* rad, float* cosv) {
     auto& I = *t->t.im;

@@ -118,14 +118,35 @@ __global__ void __launch_bounds__(kTPB) k_es_finish(const double* __restrict__ p
     lsum[i] = 0.5 * (lp + lm);
 }
 
-// ES update direction (main.cpp:1868-1873): g[k] = sum over pairs in order of (float)dl_i * scale * eps_ik,
-// one fused multiply-add per pair.
-__global__ void __launch_bounds__(kTPB) k_es_grad(int N, int P, float scale, const double* __restrict__ dl,
-                                                 const float* __restrict__ eps, float* __restrict__ grad) {
+// ES update direction (main.cpp:1868-1873): g[k] = sum over pairs of ((float)dl_i * scale) * eps_ik, one
+// fused multiply-add per pair. The reference sums the N pairs of a weight in one sequential chain, which
+// leaves only P threads for N * P reads; here block (weight tile, segment) runs four chains of kChain
+// pairs, one per wave, and the chains are added in a fixed order (waves, then segments), so the sum is
+// deterministic and differs from the single chain only in rounding.
+constexpr int kChain = 32;
+__global__ void __launch_bounds__(kTPB) k_es_grad_part(int N, int P, float scale, const double* __restrict__ dl,
+                                                      const float* __restrict__ eps, float* __restrict__ part) {
+    __shared__ float lds[kTPB / 64][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int k = blockIdx.x * 64 + lane;
+    const int i0 = (blockIdx.y * (kTPB / 64) + wave) * kChain, i1 = min(N, i0 + kChain);
+    float g = 0.0f;
+    if (k < P)
+        for (int i = i0; i < i1; i++) g = __builtin_fmaf(__fmul_rn((float)dl[i], scale), eps[(size_t)i * P + k], g);
+    lds[wave][lane] = g;
+    __syncthreads();
+    if (wave == 0 && k < P) {
+        float s = lds[0][lane];
+#pragma unroll
+        for (int q = 1; q < kTPB / 64; q++) s += lds[q][lane];
+        part[(size_t)blockIdx.y * P + k] = s;
+    }
+}
+__global__ void __launch_bounds__(kTPB) k_es_grad_final(int P, int segs, const float* __restrict__ part, float* __restrict__ grad) {
     const int k = blockIdx.x * kTPB + threadIdx.x;
     if (k >= P) return;
-    float g = 0.0f;
-    for (int i = 0; i < N; i++) g = __builtin_fmaf(__fmul_rn((float)dl[i], scale), eps[(size_t)i * P + k], g);
+    float g = part[k];
+    for (int s = 1; s < segs; s++) g += part[(size_t)s * P + k];
     grad[k] = g;
 }
 
@@ -171,6 +192,20 @@ __global__ void __launch_bounds__(kTPB) k_decode(DevModel m, const float* __rest
     mlp_forward<S>(m, w, f, o);
     float* dst = img + (size_t)p * m.nout;
     for (int c = 0; c < m.nout; c++) dst[c] = o[c];
+}
+
+// A plain copy of known size, the reference point that turns the memory counters of a profile
+// into bytes (n4 float4 values read once and written once).
+__global__ void __launch_bounds__(kTPB) k_copy_calibration(const float4* __restrict__ src, float4* __restrict__ dst, size_t n4) {
+    for (size_t i = (size_t)blockIdx.x * kTPB + threadIdx.x; i < n4; i += (size_t)gridDim.x * kTPB) dst[i] = src[i];
+}
+
+void launch_copy_calibration(Impl& I, const float* src, float* dst, size_t n) {
+    const size_t n4 = n / 4;
+    ProfScope ps(I, "copy_calibration");
+    hipLaunchKernelGGL(k_copy_calibration, dim3((unsigned)std::min<size_t>(blocks_for(n4, kTPB), 8192)), dim3(kTPB), 0, I.stream,
+                       (const float4*)src, (float4*)dst, n4);
+    NTC_CHECK(hipGetLastError());
 }
 
 __global__ void __launch_bounds__(kTPB) k_debug_gauss(NoiseTables nt, uint64_t head, uint64_t index0, size_t n, float* __restrict__ out) {
@@ -228,8 +263,18 @@ void launch_es_finish(Impl& I, int chunks, int N, double norm) {
 
 void launch_es_grad(Impl& I, int /*it*/, float sigma, int N) {
     const float scale = 1.0f / (2.0f * (float)N * sigma);
+    const int per_block = kChain * (kTPB / 64);
+    const int segs = (N + per_block - 1) / per_block;
+    if ((size_t)segs * I.P > I.gpart_cap) {   // sized at init for max_pairs; N never exceeds it
+        fprintf(stderr, "ntc_hip backend: ES update partials exceed their buffer\n");
+        exit(1);
+    }
     ProfScope ps(I, "es_grad");
-    hipLaunchKernelGGL(k_es_grad, dim3(blocks_for(I.P, kTPB)), dim3(kTPB), 0, I.stream, N, I.P, scale, I.dl, I.eps_mlp, I.wgrad);
+    float* part = I.gpart;
+    hipLaunchKernelGGL(k_es_grad_part, dim3(blocks_for(I.P, 64), segs), dim3(kTPB), 0, I.stream, N, I.P, scale, I.dl, I.eps_mlp,
+                       part);
+    NTC_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(k_es_grad_final, dim3(blocks_for(I.P, kTPB)), dim3(kTPB), 0, I.stream, I.P, segs, part, I.wgrad);
     NTC_CHECK(hipGetLastError());
 }
 

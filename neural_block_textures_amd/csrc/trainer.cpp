@@ -121,7 +121,7 @@ Trainer::~Trainer() {
         dev_free(I.z); dev_free(I.zq); dev_free(I.zgrad); dev_free(I.zm); dev_free(I.zv); dev_free(I.ztmp);
         dev_free(I.w); dev_free(I.wgrad); dev_free(I.wm); dev_free(I.wv);
         dev_free(I.tgt); dev_free(I.img); dev_free(I.feat); dev_free(I.btgt); dev_free(I.bidx);
-        dev_free(I.wsets); dev_free(I.eps_mlp); dev_free(I.part); dev_free(I.dl); dev_free(I.lsum); dev_free(I.hh);
+        dev_free(I.wsets); dev_free(I.eps_mlp); dev_free(I.gpart); dev_free(I.part); dev_free(I.dl); dev_free(I.lsum); dev_free(I.hh);
         dev_free(I.eps_lat); dev_free(I.dpix); dev_free(I.ranges); dev_free(I.qat_grid); dev_free(I.qat_bits);
         dev_free(I.qes_dev); dev_free(I.qgrid);
         dev_free(I.dct_sym); dev_free(I.dct_code); dev_free(I.dct_step); dev_free(I.dct_bits); dev_free(I.dct_dbits); dev_free(I.dct_cnt);
@@ -269,6 +269,8 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
     dev_alloc(&I.feat, (size_t)I.Mcap * d.nin); dev_alloc(&I.btgt, (size_t)I.Mcap * d.nout); dev_alloc(&I.bidx, (size_t)I.Mcap);
     I.pairs_cap = d.max_pairs;
     dev_alloc(&I.eps_mlp, (size_t)I.pairs_cap * I.P);
+    I.gpart_cap = (size_t)((I.pairs_cap + 127) / 128) * I.P;
+    dev_alloc(&I.gpart, I.gpart_cap);
     ensure_wsets(I, (size_t)2 * I.pairs_cap * I.P);
     ensure_part(I, (size_t)2 * std::max(I.pairs_cap, I.P + 1) * 4);
     dev_alloc(&I.dl, (size_t)std::max(I.pairs_cap, I.P)); dev_alloc(&I.lsum, (size_t)I.pairs_cap); dev_alloc(&I.hh, (size_t)I.P);

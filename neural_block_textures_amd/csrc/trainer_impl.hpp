@@ -69,6 +69,8 @@ struct ntc_cuda::Trainer::Impl {
     float* wsets = nullptr;
     size_t wsets_cap = 0;      // floats
     float* eps_mlp = nullptr;
+    float* gpart = nullptr;    // segment partials of the ES update: ceil(max_pairs / 128) x P
+    size_t gpart_cap = 0;
     double *part = nullptr, *dl = nullptr, *lsum = nullptr, *hh = nullptr;
     size_t part_cap = 0;
     int pairs_cap = 0;
@@ -135,6 +137,7 @@ void launch_fd_finish(Impl& I, int chunks, double norm);
 void launch_adam(Impl& I, float* theta, const float* g, float* m, float* v, size_t n, float lr, int t);
 void launch_decode(Impl& I, const float* z);
 void launch_debug_gauss(Impl& I, uint32_t stream, uint32_t step, uint32_t pair, uint64_t index0, size_t n, float* out);
+void launch_copy_calibration(Impl& I, const float* src, float* dst, size_t n);
 
 // kernels_latent.hip
 void launch_lat_eps(Impl& I, int K, unsigned mask);

@@ -94,6 +94,7 @@ def library() -> C.CDLL:
             "ntc_trainer_debug_last_zgrad": (C.c_size_t, [P, P, C.c_size_t]),
             "ntc_abi_sizeof": (C.c_size_t, [C.c_char_p]),
             "ntc_trainer_debug_last_losses": (C.c_size_t, [P, P, P, C.c_size_t]),
+            "ntc_trainer_debug_last_wgrad": (C.c_size_t, [P, P, C.c_size_t]),
             "ntc_trainer_nparams": (C.c_longlong, [P]),
             "ntc_trainer_nz": (C.c_longlong, [P]),
             "ntc_trainer_stream": (P, [P]),
@@ -102,6 +103,7 @@ def library() -> C.CDLL:
             "ntc_trainer_kernel_time": (C.c_int, [P, C.c_char_p, P, P]),
             "ntc_trainer_debug_gauss": (None, [P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, C.c_size_t, P]),
             "ntc_trainer_debug_noise_factors": (None, [P, C.c_uint32, C.c_size_t, P, P]),
+            "ntc_trainer_debug_copy_calibration": (None, [P, C.c_size_t, C.c_int]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -345,6 +347,11 @@ class Trainer:
         self._lib.ntc_trainer_debug_last_losses(self._h, lp.ctypes.data, lm.ctypes.data, n)
         return lp, lm
 
+    def debug_last_wgrad(self):
+        out = np.empty(self.P, np.float32)
+        self._lib.ntc_trainer_debug_last_wgrad(self._h, out.ctypes.data, self.P)
+        return out
+
     def debug_last_zgrad(self):
         out = np.empty(self.nz, np.float32)
         self._lib.ntc_trainer_debug_last_zgrad(self._h, out.ctypes.data, self.nz)
@@ -362,6 +369,9 @@ class Trainer:
         return rad, cosv
 
     # ---- instrumentation
+    def debug_copy_calibration(self, n, reps=1):
+        self._lib.ntc_trainer_debug_copy_calibration(self._h, n, reps)
+
     def synchronize(self):
         self._lib.ntc_trainer_synchronize(self._h)
 
