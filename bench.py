@@ -113,7 +113,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py runs on one GPU only (asked for {max(args.gpus, world)}): this backend has no multi-GPU path; "
-              "see DESIGN.md for how the work would shard", file=sys.stderr)
+              "the population would shard over pairs with one all-gather of the pair differences", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

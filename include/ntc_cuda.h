@@ -4,7 +4,7 @@
 // the namespace, the envelope constants, the five descriptor structs (field names, order, types
 // and defaults) and every Trainer method keep their names and meaning, so the reference's
 // main.cpp compiles against this header unchanged and links against libntc_hip.so in place of
-// the CUDA static library (see INTEGRATION.md). The name "ntc_cuda" is kept only because main.cpp
+// the CUDA static library. The name "ntc_cuda" is kept only because main.cpp
 // spells it; nothing behind it uses CUDA. Plain C++: no HIP types leak into this header.
 //
 // Reference: cuda/ntc_cuda.h:14-20 (constants), :23 (PosKindDev), :25-52 (LevelDesc, PosDesc,

@@ -45,26 +45,26 @@ def _rgb(W, H, levels, hidden, **kw):
 
 def workloads() -> dict:
     return {
-        # configs[0]: CPU-reference plumbing run, 256x256 RGB, 64x64x4 bilinear, 16,16, population 64
+        # CPU-reference plumbing run, 256x256 RGB, 64x64x4 bilinear, 16,16, population 64
         "rgb256": Workload("rgb256", _rgb(256, 256, [(64, 64, 4, False)], [16, 16]), mlp_pairs=32, mlp_batch=65536,
                            mlp_sigma=0.01, iters=200, seed=11,
                            notes="full-image loss read as a 65536-slot minibatch drawn with replacement"),
-        # configs[1]: 512x512 RGB, 128x128x8 + 32x32x4 bilinear, 32,32, population 1024 over 64K-pixel batches
+        # 512x512 RGB, 128x128x8 + 32x32x4 bilinear, 32,32, population 1024 over 64K-pixel batches
         "rgb512_two_level": Workload("rgb512_two_level",
                                      _rgb(512, 512, [(128, 128, 8, False), (32, 32, 4, False)], [32, 32]),
                                      mlp_pairs=512, mlp_batch=65536, iters=2000, seed=12,
                                      notes="post-hoc 8-bit latent quantization is a host statistic"),
-        # configs[2]: 4 x 512x512 material, --qat 2 512x512x2 nearest + 128x128x4 bilinear, 32,32, population 8192
+        # 4 x 512x512 material, --qat 2 512x512x2 nearest + 128x128x4 bilinear, 32,32, population 8192
         "material512": Workload("material512",
                                 Layout(512, 512, [(512, 512, 2, True), (128, 128, 4, False)], [32, 32], T=4,
                                        pos=[PK_UV], leak=0.01),
                                 mlp_pairs=4096, mlp_batch=4096, iters=8000, qat_bits=[2, 2], fd_iters=50,
                                 fp16_end=True, seed=13, textures=4),
-        # configs[3]: 512x512 RGB, --dct-q 50 plane 512x512x1 + 128x128x4, 32,32, population 4096
+        # 512x512 RGB, --dct-q 50 plane 512x512x1 + 128x128x4, 32,32, population 4096
         "dct512": Workload("dct512", Layout(512, 512, [(512, 512, 1, True), (128, 128, 4, False)], [32, 32], T=1,
                                             pos=[PK_UV], leak=0.01),
                            mlp_pairs=2048, mlp_batch=4096, iters=4000, dct_q=[50], seed=14),
-        # configs[4]: 4 x 2048x2048 maps, 1024x1024x4 + 256x256x8 bilinear, 64,64, population 16384, 256K batches
+        # 4 x 2048x2048 maps, 1024x1024x4 + 256x256x8 bilinear, 64,64, population 16384, 256K batches
         "material2048": Workload("material2048",
                                  Layout(2048, 2048, [(1024, 1024, 4, False), (256, 256, 8, False)], [64, 64], T=4,
                                         pos=[PK_UV], leak=0.0),

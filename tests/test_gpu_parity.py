@@ -2,7 +2,7 @@
 
 Bars: noise, minibatch indices, --qes indices and values, DCT symbols / codes / planes / bit counts
 and Adam / ES-update arithmetic are bit-exact; per-member ES losses within 1e-5 relative (the
-north-star bar); decoded values within 2e-6 absolute (the device's expf against the host C
+task's bar); decoded values within 2e-6 absolute (the device's expf against the host C
 library's is the only difference on this path); latent gradients within 1e-3 of their RMS (the
 reference's own --cuda-check bar, main.cpp:3088); qat selectors equal except on texels whose two
 candidates have cell losses equal to 1e-6 relative (main.cpp:3143-3144)."""

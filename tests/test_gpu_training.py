@@ -1,5 +1,5 @@
 """End-to-end: a short training run on the device against the oracle's CPU loop (final PSNR
-within 0.05 dB), and the benchmark workloads at their full sizes through
+within 0.05 dB, the task's bar), and the benchmark workloads at their full sizes through
 size-independent properties (an unperturbed population has exactly zero loss differences and
 equal member losses; member losses of sampled pairs match the oracle on the device's own
 minibatch; frozen levels get exactly zero gradient; every --qat value stays on its grid)."""
