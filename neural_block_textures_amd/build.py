@@ -20,8 +20,12 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libntc_hip.so")
-SOURCES = ["kernels_mlp.hip", "kernels_latent.hip", "kernels_quant.hip", "trainer.cpp", "noise_tables.cpp", "capi.cpp"]
+SOURCES = ["kernels_pop.hip", "kernels_mlp.hip", "kernels_latent.hip", "kernels_quant.hip", "trainer.cpp", "noise_tables.cpp", "capi.cpp"]
 ARCH = "gfx950"
+# The matrix-core population evaluation takes maxima of values that are never NaN for a finite
+# model (the reference's own build assumes no NaNs either, -ffast-math): with the IEEE mode bit
+# off, v_max_f32 needs no canonicalising copies of its operands.
+EXTRA = {"kernels_pop.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"]}
 
 
 def hipcc() -> str:
@@ -36,10 +40,12 @@ def flags(src: str) -> list[str]:
          "-Wno-unused-result", "-Wno-unknown-pragmas"]
     if src.endswith(".hip"):
         f += [f"--offload-arch={ARCH}", "-x", "hip", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-              "-munsafe-fp-atomics"]
+              "-munsafe-fp-atomics",
+              # matrix-core results straight into VGPRs: no AGPR copies between a layer and its activation
+              "-mllvm", "-amdgpu-mfma-vgpr-form"]
     else:
         f += ["-D__HIP_PLATFORM_AMD__"]
-    return f
+    return f + EXTRA.get(src, [])
 
 
 def build(verbose: bool = False, jobs: int = 4) -> str:

@@ -246,8 +246,7 @@ void launch_fd_sets(Impl& I, float h) {
     NTC_CHECK(hipGetLastError());
 }
 
-void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks) {
-    ProfScope ps(I, "pop_eval");
+void launch_pop_eval_valu(Impl& I, int pairs, int M, int chunk, int chunks) {
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         hipLaunchKernelGGL(k_pop_eval<S>, dim3(pairs, chunks), dim3(kTPB), 0, I.stream, I.dm, I.wsets, M, I.Mcap, chunk, chunks,

@@ -1,0 +1,179 @@
+// The population evaluation (MlpTrainer::step's member losses, main.cpp:1848-1861) on the FP32
+// matrix cores of gfx950, for the fixed shapes whose hidden width is a multiple of 16; other
+// shapes use the VALU kernel of kernels_mlp.hip.
+//
+// On this chip an FP32 matrix instruction and a VALU instruction do not run concurrently on a
+// SIMD (a 16x16x4 f32 step costs 32 cycles, a VALU instruction 4, and their mixes take the sum),
+// so everything around the matrix operations is counted in instructions: the activation is one
+// v_max_f32 (this file is compiled with relaxed NaN handling and the IEEE mode bit off, so the
+// maximum needs no canonicalising copies); the sigmoid is the hardware exp2 and reciprocal; tile
+// inputs are loaded with a wave-uniform SGPR base and loop-invariant 32-bit lane offsets.
+//
+// Block (pair, chunk) has four waves: wave w evaluates member 2 pair + (w & 1) on the 16-slot
+// tiles 2 j + (w >> 1) of the chunk, two tiles at a time, the next two tiles' inputs loading
+// while the current ones compute. Each lane adds the float terms cw (d d) (main.cpp:1747) of its
+// output channels into a double; the two waves of a member are added in a fixed order.
+#include "mfma_mlp.hpp"
+#include "shapes.hpp"
+#include "trainer_impl.hpp"
+
+namespace ntc_hip {
+
+constexpr int kPopWaves = 4, kPopU = 2;
+
+// global-memory views: an SGPR base plus a 32-bit lane offset becomes one global_load
+typedef __attribute__((address_space(1))) const char GChar;
+typedef __attribute__((address_space(1))) const float GFloat;
+
+template <class S>
+struct PopTileIn {
+    float b1[kPopU][MfmaShape<S>::kKs1];
+    float t[kPopU][4];
+};
+
+// Inputs of tiles (j, j + 1) of this wave: base = slot of tile j for lane 0 (uniform).
+template <class S>
+__device__ __forceinline__ void pop_load(PopTileIn<S>& in, const float* base_f, const float* base_t, const uint32_t (&fo)[MfmaShape<S>::kKs1],
+                                         const uint32_t (&to)[4]) {
+    using Q = MfmaShape<S>;
+    const GChar* bf = (const GChar*)uniform_ptr(base_f);
+    const GChar* bt = (const GChar*)uniform_ptr(base_t);
+#pragma unroll
+    for (int u = 0; u < kPopU; u++) {
+#pragma unroll
+        for (int ks = 0; ks < Q::kKs1; ks++) in.b1[u][ks] = *(const GFloat*)(bf + fo[ks] + 128 * u);
+#pragma unroll
+        for (int r = 0; r < 4; r++) in.t[u][r] = *(const GFloat*)(bt + to[r] + 128 * u);
+    }
+}
+
+// 1 / (1 + e^-s) from the hardware exp2 and reciprocal (each within about 1 ulp)
+__device__ __forceinline__ float sigmoid_hw(float s) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(s * -1.44269504088896341f));
+}
+
+template <class S, bool LeakUnit, bool Clamp>
+__global__ void __launch_bounds__(64 * kPopWaves) k_pop_mfma(DevModel m, const float* __restrict__ wsets, int M, int Mcap,
+                                                           int chunk, int chunks, const float* __restrict__ feat,
+                                                           const float* __restrict__ btgt, double* __restrict__ part) {
+    using Q = MfmaShape<S>;
+    __shared__ double red[kPopWaves];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int pair = blockIdx.x, ch = blockIdx.y, sgn = wave & 1, half = wave >> 1;
+    const int i16 = lane & 15, g = lane >> 4;
+    MfmaWeights<S> W;
+    mfma_load<S>(W, wsets + (size_t)(2 * pair + sgn) * m.P, lane);
+    float cw[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        cw[r] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < Q::kNout; c++) if (4 * g + r == c) cw[r] = m.cw[c];
+    }
+    // lane byte offsets of the feature rows 4 ks + g and target rows 4 g + r (rows past the last
+    // one are clamped to it: their weights, or their channel weights cw, are zero)
+    uint32_t fo[Q::kKs1], to[4];
+#pragma unroll
+    for (int ks = 0; ks < Q::kKs1; ks++) fo[ks] = 4u * ((uint32_t)min(4 * ks + g, Q::kIn - 1) * (uint32_t)Mcap + (uint32_t)i16);
+#pragma unroll
+    for (int r = 0; r < 4; r++) to[r] = 4u * ((uint32_t)min(4 * g + r, Q::kNout - 1) * (uint32_t)Mcap + (uint32_t)i16);
+    const int s0 = ch * chunk, s1 = min(M, s0 + chunk);
+    const int tiles = (s1 - s0 + 15) >> 4;
+    const int mine = (tiles - half + 1) >> 1;   // this wave's tiles: 2 j + half, j < mine
+    double e = 0.0;
+    PopTileIn<S> cur;
+    pop_load<S>(cur, feat + s0 + 16 * half, btgt + s0 + 16 * half, fo, to);
+    for (int j = 0; j < mine; j += kPopU) {
+        PopTileIn<S> nxt;
+        if (j + kPopU < mine) {
+            const int sn = s0 + 16 * (2 * (j + kPopU) + half);
+            pop_load<S>(nxt, feat + sn, btgt + sn, fo, to);
+        }
+        if constexpr (Q::kIn % 4 != 0) {   // inputs past nin are zero
+#pragma unroll
+            for (int u = 0; u < kPopU; u++)
+                if (4 * (Q::kKs1 - 1) + g >= Q::kIn) cur.b1[u][Q::kKs1 - 1] = 0.0f;
+        }
+        f4v o[kPopU];
+        mfma_forward<S, kPopU, LeakUnit>(W, cur.b1, m.leak, o);
+#pragma unroll
+        for (int u = 0; u < kPopU; u++) {
+            const int st = s0 + 16 * (2 * (j + u) + half);   // first slot of the tile (uniform)
+            float term[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float y = Clamp ? __builtin_amdgcn_fmed3f(o[u][r] + 0.5f, 0.0f, 1.0f) : sigmoid_hw(o[u][r]);
+                const float d = y - cur.t[u][r];
+                term[r] = __fmul_rn(cw[r], __fmul_rn(d, d));
+            }
+            if (j + u < mine) {
+                if (st + 16 <= s1) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) e += (double)term[r];
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) e += st + i16 < s1 ? (double)term[r] : 0.0;
+                }
+            }
+        }
+        cur = nxt;
+    }
+    e = wave_sum(e);
+    if (lane == 0) red[wave] = e;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        part[(size_t)(2 * pair) * chunks + ch] = red[0] + red[2];
+        part[(size_t)(2 * pair + 1) * chunks + ch] = red[1] + red[3];
+    }
+}
+
+bool pop_on_matrix_cores(const Impl& I) {
+    bool ok = false;
+    dispatch_shape(I.dm, [&](auto s) { ok = MfmaShape<decltype(s)>::kOk; });
+    return ok;
+}
+
+int pop_chunk(const Impl& I, int pairs, int M) {
+    if (pop_on_matrix_cores(I)) {
+        // at least 2048 blocks where the population allows, at least 256 slots per chunk
+        const int want = std::max(1, std::min((2048 + pairs - 1) / pairs, M / 256));
+        const int chunk = ((M + want - 1) / want + 15) & ~15;
+        return std::max(chunk, 16);
+    }
+    return std::min(M, 1024);
+}
+
+template <class S, bool LeakUnit>
+static void launch_pop_mfma(Impl& I, int pairs, int M, int chunk, int chunks) {
+    auto kern = I.dm.clamp_out ? k_pop_mfma<S, LeakUnit, true> : k_pop_mfma<S, LeakUnit, false>;
+    hipLaunchKernelGGL(kern, dim3(pairs, chunks), dim3(64 * kPopWaves), 0, I.stream, I.dm, I.wsets, M, I.Mcap, chunk, chunks, I.feat,
+                       I.btgt, I.part);
+}
+
+void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks) {
+    ProfScope ps(I, "pop_eval");
+    if ((size_t)2 * pairs * chunks > I.part_cap) {
+        fprintf(stderr, "ntc_hip backend: population evaluation needs %d partial sums, buffer holds %zu\n", 2 * pairs * chunks,
+                I.part_cap);
+        exit(1);
+    }
+    if (!pop_on_matrix_cores(I)) {
+        launch_pop_eval_valu(I, pairs, M, chunk, chunks);
+        return;
+    }
+    if (chunk % 16 != 0) {
+        fprintf(stderr, "ntc_hip backend: matrix-core population evaluation needs 16-slot chunks (got %d)\n", chunk);
+        exit(1);
+    }
+    dispatch_shape(I.dm, [&](auto s) {
+        using S = decltype(s);
+        if constexpr (MfmaShape<S>::kOk) {
+            if (I.dm.leak >= 0.0f && I.dm.leak <= 1.0f) launch_pop_mfma<S, true>(I, pairs, M, chunk, chunks);
+            else launch_pop_mfma<S, false>(I, pairs, M, chunk, chunks);
+        }
+    });
+    NTC_CHECK(hipGetLastError());
+}
+
+}   // namespace ntc_hip

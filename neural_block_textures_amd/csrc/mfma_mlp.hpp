@@ -1,0 +1,164 @@
+// The MLP of the fixed shapes on the FP32 matrix cores of gfx950 (v_mfma_f32_16x16x4f32).
+//
+// One wave evaluates one member's MLP on a tile of 16 pixels at a time, with the member's
+// parameters held in VGPRs in the instruction's operand layout:
+//   A (16 x 4)  lane l holds A[l % 16][l / 16]        weights W[out][in]: out = 16 ot + l % 16
+//   B (4 x 16)  lane l holds B[l / 16][l % 16]        activations: unit 4 ks + l / 16 of pixel l % 16
+//   C/D (16x16) lane l, register r holds D[4 (l / 16) + r][l % 16]
+// On gfx950 this instruction computes D = C then D = fma(A[.][k], B[k][.], D) for k = 0..3 in
+// order, each step rounded (measured against host fmaf chains on 1 M random values, including
+// subnormal operands, with no difference). With C = the bias and the k-steps of a layer taken in
+// ascending input order, every unit is therefore the reference's s = b[j]; s = fma(w[j][i], a[i], s)
+// for i ascending (main.cpp:603-627), bit for bit.
+//
+// A layer's output comes back in the D layout (lane group g holds units 4g + r of a 16-unit
+// tile); the next layer wants lane group q to hold unit 4 ks + q. A 4 x 4 transpose across
+// (lane group, register) - two v_permlane32_swap and two v_permlane16_swap per 16-unit tile -
+// turns the activated D registers of tile t into the B operands of k-steps 4t .. 4t + 3.
+#pragma once
+#include "device_common.hpp"
+
+namespace ntc_hip {
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+template <class S, bool = S::kFixed>
+struct MfmaShape { static constexpr bool kOk = false; };
+template <class S>
+struct MfmaShape<S, true> {
+    static constexpr int kIn = S::kNin, kH = S::kH, kNL = S::kNL, kNout = S::kNout;
+    static constexpr bool kOk = kH % 16 == 0 && kNout <= 16 && kNL >= 1;
+    static constexpr int kKs1 = (kIn + 3) / 4;   // k-steps of the first layer (inputs padded with zeros)
+    static constexpr int kHt = kH / 16;          // 16-unit tiles of a hidden layer
+    static constexpr int kKsH = kH / 4;          // k-steps of a layer fed by a hidden layer
+    static constexpr int kDeep = kNL > 1 ? kNL - 1 : 1;
+};
+
+// One member's parameters in operand layout.
+template <class S>
+struct MfmaWeights {
+    using Q = MfmaShape<S>;
+    float a1[Q::kHt][Q::kKs1];
+    f4v c1[Q::kHt];
+    float ah[Q::kDeep][Q::kHt][Q::kKsH];
+    f4v ch[Q::kDeep][Q::kHt];
+    float ao[Q::kKsH];
+    f4v co;
+};
+
+// Gathers a member's flat parameter vector (per layer W[out][in] row-major, then b[out]) into
+// operand layout; lane = threadIdx.x % 64.
+template <class S>
+__device__ __forceinline__ void mfma_load(MfmaWeights<S>& W, const float* __restrict__ w, int lane) {
+    using Q = MfmaShape<S>;
+    constexpr int NIN = Q::kIn, H = Q::kH, NO = Q::kNout;
+    const int i16 = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int ot = 0; ot < Q::kHt; ot++) {
+#pragma unroll
+        for (int ks = 0; ks < Q::kKs1; ks++) {
+            const int in = 4 * ks + g;
+            W.a1[ot][ks] = in < NIN ? w[(16 * ot + i16) * NIN + in] : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) W.c1[ot][r] = w[H * NIN + 16 * ot + 4 * g + r];
+    }
+    const float* p = w + H * NIN + H;
+#pragma unroll
+    for (int l = 0; l < Q::kNL - 1; l++) {
+#pragma unroll
+        for (int ot = 0; ot < Q::kHt; ot++) {
+#pragma unroll
+            for (int ks = 0; ks < Q::kKsH; ks++) W.ah[l][ot][ks] = p[(16 * ot + i16) * H + 4 * ks + g];
+#pragma unroll
+            for (int r = 0; r < 4; r++) W.ch[l][ot][r] = p[H * H + 16 * ot + 4 * g + r];
+        }
+        p += H * H + H;
+    }
+#pragma unroll
+    for (int ks = 0; ks < Q::kKsH; ks++) W.ao[ks] = i16 < NO ? p[i16 * H + 4 * ks + g] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) W.co[r] = 4 * g + r < NO ? p[NO * H + 4 * g + r] : 0.0f;
+}
+
+__device__ __forceinline__ f4v mfma4(float a, float b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+
+// element (lane group g, register r) -> (lane group r, register g)
+__device__ __forceinline__ void transpose4(const f4v& v, float* y) {
+    const auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[0]), __float_as_uint(v[2]), false, false);
+    const auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[1]), __float_as_uint(v[3]), false, false);
+    const auto t01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+    const auto t23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+    y[0] = __uint_as_float(t01[0]); y[1] = __uint_as_float(t01[1]);
+    y[2] = __uint_as_float(t23[0]); y[3] = __uint_as_float(t23[1]);
+}
+
+// The activation of main.cpp:560, x > 0 ? x : leak x. For 0 <= leak <= 1 this is max(x, leak x)
+// bit for bit (also for signed zeros and NaN), one instruction fewer.
+template <bool LeakUnit>
+__device__ __forceinline__ float act(float x, float leak) {
+    if constexpr (LeakUnit) return fmaxf(x, leak * x);
+    else return x > 0.0f ? x : leak * x;
+}
+
+// U independent 16-pixel tiles through the MLP (interleaved, so one tile's activations overlap
+// the other's matrix operations): b1[u] = the first layer's B operands of tile u (input 4 ks + l / 16
+// of pixel l % 16, zero past nin); returns the output layer's pre-activations of each tile in D layout
+// (lane l, register r = output 4 (l / 16) + r of pixel l % 16). Every lane of the wave must be active.
+template <class S, int U, bool LeakUnit>
+__device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const float (&b1)[U][MfmaShape<S>::kKs1], float leak,
+                                             f4v (&o)[U]) {
+    using Q = MfmaShape<S>;
+    float x[U][Q::kKsH];
+    {
+        f4v acc[U][Q::kHt];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int ot = 0; ot < Q::kHt; ot++) acc[u][ot] = W.c1[ot];
+#pragma unroll
+        for (int ks = 0; ks < Q::kKs1; ks++)
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int ot = 0; ot < Q::kHt; ot++) acc[u][ot] = mfma4(W.a1[ot][ks], b1[u][ks], acc[u][ot]);
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int ot = 0; ot < Q::kHt; ot++) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[u][ot][r] = act<LeakUnit>(acc[u][ot][r], leak);
+                transpose4(acc[u][ot], x[u] + 4 * ot);
+            }
+    }
+#pragma unroll
+    for (int l = 0; l < Q::kNL - 1; l++) {
+        f4v acc[U][Q::kHt];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int ot = 0; ot < Q::kHt; ot++) acc[u][ot] = W.ch[l][ot];
+#pragma unroll
+        for (int ks = 0; ks < Q::kKsH; ks++)
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int ot = 0; ot < Q::kHt; ot++) acc[u][ot] = mfma4(W.ah[l][ot][ks], x[u][ks], acc[u][ot]);
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int ot = 0; ot < Q::kHt; ot++) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[u][ot][r] = act<LeakUnit>(acc[u][ot][r], leak);
+                transpose4(acc[u][ot], x[u] + 4 * ot);
+            }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) o[u] = W.co;
+#pragma unroll
+    for (int ks = 0; ks < Q::kKsH; ks++)
+#pragma unroll
+        for (int u = 0; u < U; u++) o[u] = mfma4(W.ao[ks], x[u][ks], o[u]);
+}
+
+}   // namespace ntc_hip

@@ -84,9 +84,6 @@ void ensure_lat(Impl& I, int K) {
 
 void sync(Impl& I) { NTC_CHECK(hipStreamSynchronize(I.stream)); }
 
-// minibatch slots per population-evaluation block
-int pop_chunk(int M) { return std::min(M, 1024); }
-
 }   // namespace
 
 namespace ntc_hip {
@@ -266,13 +263,14 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
     dev_alloc(&I.w, I.P); dev_alloc(&I.wgrad, I.P); dev_alloc(&I.wm, I.P); dev_alloc(&I.wv, I.P);
     dev_alloc(&I.tgt, I.npix * d.nout); dev_alloc(&I.img, I.npix * d.nout);
     I.Mcap = d.max_batch;
-    dev_alloc(&I.feat, (size_t)I.Mcap * d.nin); dev_alloc(&I.btgt, (size_t)I.Mcap * d.nout); dev_alloc(&I.bidx, (size_t)I.Mcap);
+    // 64 floats of slack: the matrix-core population evaluation reads whole 16-slot tiles
+    dev_alloc(&I.feat, (size_t)I.Mcap * d.nin + 64); dev_alloc(&I.btgt, (size_t)I.Mcap * d.nout + 64); dev_alloc(&I.bidx, (size_t)I.Mcap);
     I.pairs_cap = d.max_pairs;
     dev_alloc(&I.eps_mlp, (size_t)I.pairs_cap * I.P);
     I.gpart_cap = (size_t)((I.pairs_cap + 127) / 128) * I.P;
     dev_alloc(&I.gpart, I.gpart_cap);
     ensure_wsets(I, (size_t)2 * I.pairs_cap * I.P);
-    ensure_part(I, (size_t)2 * std::max(I.pairs_cap, I.P + 1) * 4);
+    ensure_part(I, (size_t)2 * (std::max(I.pairs_cap, I.P + 1) * 4 + 2048));
     dev_alloc(&I.dl, (size_t)std::max(I.pairs_cap, I.P)); dev_alloc(&I.lsum, (size_t)I.pairs_cap); dev_alloc(&I.hh, (size_t)I.P);
     if (d.qat > 0) {
         dev_alloc(&I.qat_grid, 9 * 257); dev_alloc(&I.qat_bits, MAX_CH);
@@ -389,7 +387,7 @@ void Trainer::mlp_step(int it, float sigma, float lr, int N, int M) {
     }
     launch_batch(I, it, M);
     launch_perturb(I, it, sigma, N);
-    const int chunk = pop_chunk(M), chunks = (M + chunk - 1) / chunk;
+    const int chunk = pop_chunk(I, N, M), chunks = (M + chunk - 1) / chunk;
     ensure_part(I, (size_t)2 * N * chunks);
     launch_pop_eval(I, N, M, chunk, chunks);
     launch_es_finish(I, chunks, N, 3.0 * (double)I.d.wsum * (double)M);
@@ -407,7 +405,7 @@ void Trainer::mlp_step_fd(int it, float h, float lr, int M) {
     launch_batch(I, it, M);
     ensure_wsets(I, (size_t)2 * (I.P + 1) * I.P);
     launch_fd_sets(I, h);
-    const int chunk = pop_chunk(M), chunks = (M + chunk - 1) / chunk;
+    const int chunk = pop_chunk(I, I.P + 1, M), chunks = (M + chunk - 1) / chunk;
     ensure_part(I, (size_t)2 * (I.P + 1) * chunks);
     launch_pop_eval(I, I.P + 1, M, chunk, chunks);
     launch_fd_finish(I, chunks, 3.0 * (double)I.d.wsum * (double)M);

@@ -130,7 +130,10 @@ void launch_fill(Impl& I, float* p, size_t n, float v);
 void launch_batch(Impl& I, int it, int M);
 void launch_perturb(Impl& I, int it, float sigma, int N);
 void launch_fd_sets(Impl& I, float h);
+// minibatch slots per population-evaluation block for a population of `pairs` pairs
+int pop_chunk(const Impl& I, int pairs, int M);
 void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks);
+void launch_pop_eval_valu(Impl& I, int pairs, int M, int chunk, int chunks);
 void launch_es_finish(Impl& I, int chunks, int N, double norm);
 void launch_es_grad(Impl& I, int it, float sigma, int N);
 void launch_fd_finish(Impl& I, int chunks, double norm);
