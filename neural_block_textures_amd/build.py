@@ -20,7 +20,7 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libntc_hip.so")
-SOURCES = ["kernels_pop.hip", "kernels_mlp.hip", "kernels_latent.hip", "kernels_quant.hip", "trainer.cpp", "noise_tables.cpp", "capi.cpp"]
+SOURCES = ["kernels_pop.hip", "kernels_mlp.hip", "kernels_latent.hip", "kernels_quant.hip", "trainer.cpp", "noise_fix.cpp", "capi.cpp"]
 ARCH = "gfx950"
 # The matrix-core population evaluation takes maxima of values that are never NaN for a finite
 # model (the reference's own build assumes no NaNs either, -ffast-math): with the IEEE mode bit

@@ -187,9 +187,16 @@ void ntc_trainer_debug_noise_factors(ntc_trainer* t, uint32_t k0, size_t n, floa
     const size_t total = (size_t)1 << 24;
     if ((size_t)k0 >= total) return;
     if (n > total - k0) n = total - k0;
-    if (rad) NTC_CHECK(hipMemcpyAsync(rad, I.noise.rad + k0, n * sizeof(float), hipMemcpyDeviceToHost, I.stream));
-    if (cosv) NTC_CHECK(hipMemcpyAsync(cosv, I.noise.cosv + k0, n * sizeof(float), hipMemcpyDeviceToHost, I.stream));
+    if (!n) return;
+    float *dr = nullptr, *dc = nullptr;
+    NTC_CHECK(hipMalloc(&dr, n * sizeof(float)));
+    NTC_CHECK(hipMalloc(&dc, n * sizeof(float)));
+    ntc_hip::launch_debug_factors(I, k0, n, dr, dc);
+    if (rad) NTC_CHECK(hipMemcpyAsync(rad, dr, n * sizeof(float), hipMemcpyDeviceToHost, I.stream));
+    if (cosv) NTC_CHECK(hipMemcpyAsync(cosv, dc, n * sizeof(float), hipMemcpyDeviceToHost, I.stream));
     NTC_CHECK(hipStreamSynchronize(I.stream));
+    NTC_CHECK(hipFree(dr));
+    NTC_CHECK(hipFree(dc));
 }
 
 }   // extern "C"

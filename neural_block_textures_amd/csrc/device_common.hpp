@@ -10,6 +10,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "noise_math.hpp"
+
 namespace ntc_hip {
 
 constexpr int kMaxLevels = 3, kMaxPos = 16, kMaxOut = 12, kMaxHidden = 8, kMaxWidth = 64;
@@ -38,10 +40,6 @@ struct DevModel {
     long long nz;        // latent floats
 };
 
-struct NoiseTables {
-    const float* rad;    // rad[k]  = sqrtf(-2 logf((k + 1) / 2^24)), from the host C library
-    const float* cosv;   // cosv[k] = cosf(2 pi k / 2^24), from the host C library
-};
 
 // ---------------------------------------------------------------- counter-based noise
 // The key and Box-Muller draw of the reference's cuda/ntc_noise.h:20-47: a splitmix64 output
@@ -62,9 +60,9 @@ __host__ __device__ __forceinline__ uint64_t noise_bits(uint64_t head, uint64_t 
 __host__ __device__ __forceinline__ uint32_t noise_uniform(uint32_t u, uint32_t n) { return (uint32_t)(((uint64_t)u * (uint64_t)n) >> 32); }
 // One standard normal draw: the 24-bit halves of the key select the two factors, whose product
 // is the reference's sqrtf(-2 logf(u1)) * cosf(2 pi u2) bit for bit (one IEEE multiply).
-__device__ __forceinline__ float gauss_at(const NoiseTables& nt, uint64_t head, uint64_t index) {
+__device__ __forceinline__ float gauss_at(const NoiseFix& fx, uint64_t head, uint64_t index) {
     const uint64_t h = noise_bits(head, index);
-    return __fmul_rn(nt.rad[(uint32_t)(h >> 40)], nt.cosv[(uint32_t)(h & 0xFFFFFFull)]);
+    return __fmul_rn(nm_radius(fx, (uint32_t)(h >> 40)), nm_cosine(fx, (uint32_t)(h & 0xFFFFFFull)));
 }
 
 // ---------------------------------------------------------------- geometry (main.cpp:507-547)

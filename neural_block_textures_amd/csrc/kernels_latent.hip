@@ -19,7 +19,7 @@ __device__ __forceinline__ int level_of(const DevModel& m, long long i) {
 }
 
 // eps[k][i] = gauss(seed, NS_LAT, step, k, i) for the ES-perturbed levels (0 elsewhere)
-__global__ void __launch_bounds__(kTPB) k_lat_eps(NoiseTables nt, DevModel m, uint64_t seed, uint32_t step, int K, unsigned mask,
+__global__ void __launch_bounds__(kTPB) k_lat_eps(NoiseFix nt, DevModel m, uint64_t seed, uint32_t step, int K, unsigned mask,
                                                  float* __restrict__ eps) {
     const long long t = (long long)blockIdx.x * kTPB + threadIdx.x;
     if (t >= (long long)K * m.nz) return;

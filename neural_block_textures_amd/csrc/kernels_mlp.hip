@@ -40,7 +40,7 @@ __global__ void __launch_bounds__(kTPB) k_batch(DevModel m, uint64_t head, int M
 
 // Member weights of one ES step: pair i, weight k -> w0 +- sigma * eps (one fused operation each,
 // main.cpp:1856), and eps itself for the update. The noise is the counter draw (NS_MLP, it, i, k).
-__global__ void __launch_bounds__(kTPB) k_perturb(NoiseTables nt, uint64_t seed, uint32_t step, int N, int P, float sigma,
+__global__ void __launch_bounds__(kTPB) k_perturb(NoiseFix nt, uint64_t seed, uint32_t step, int N, int P, float sigma,
                                                  const float* __restrict__ w0, float* __restrict__ wsets,
                                                  float* __restrict__ eps) {
     const long long t = (long long)blockIdx.x * kTPB + threadIdx.x;
@@ -208,7 +208,15 @@ void launch_copy_calibration(Impl& I, const float* src, float* dst, size_t n) {
     NTC_CHECK(hipGetLastError());
 }
 
-__global__ void __launch_bounds__(kTPB) k_debug_gauss(NoiseTables nt, uint64_t head, uint64_t index0, size_t n, float* __restrict__ out) {
+__global__ void __launch_bounds__(kTPB) k_debug_factors(NoiseFix nt, uint32_t k0, size_t n, float* __restrict__ rad,
+                                                       float* __restrict__ cosv) {
+    const size_t i = (size_t)blockIdx.x * kTPB + threadIdx.x;
+    if (i >= n) return;
+    rad[i] = nm_radius(nt, k0 + (uint32_t)i);
+    cosv[i] = nm_cosine(nt, k0 + (uint32_t)i);
+}
+
+__global__ void __launch_bounds__(kTPB) k_debug_gauss(NoiseFix nt, uint64_t head, uint64_t index0, size_t n, float* __restrict__ out) {
     const size_t i = (size_t)blockIdx.x * kTPB + threadIdx.x;
     if (i < n) out[i] = gauss_at(nt, head, index0 + i);
 }
@@ -303,6 +311,11 @@ void launch_debug_gauss(Impl& I, uint32_t stream, uint32_t step, uint32_t pair, 
     if (!n) return;
     const uint64_t head = noise_head(I.d.seed, stream, step, pair);
     hipLaunchKernelGGL(k_debug_gauss, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, I.noise, head, index0, n, out);
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_debug_factors(Impl& I, uint32_t k0, size_t n, float* rad, float* cosv) {
+    hipLaunchKernelGGL(k_debug_factors, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, I.noise, k0, n, rad, cosv);
     NTC_CHECK(hipGetLastError());
 }
 

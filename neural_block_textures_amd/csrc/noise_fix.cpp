@@ -1,0 +1,78 @@
+// The correction bits of the device's Gaussian draw, built on the host from its own C library and
+// copied to each device once per process (2 x 2 MiB, kept until the process ends).
+//
+// For every argument k of each Box-Muller factor the host compares its C library's logf / cosf
+// with the rounded double value of noise_math.hpp; where they differ it checks that the library's
+// value is the float neighbour on the side of the double value, and sets bit k. A C library for
+// which that rule fails anywhere is reported at init: the device could not reproduce its draws.
+#include <math.h>
+
+#include <algorithm>
+#include <atomic>
+#include <map>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "trainer_impl.hpp"
+
+namespace ntc_hip {
+
+namespace {
+std::mutex g_mutex;
+std::map<int, NoiseFix> g_fix;
+}
+
+bool noise_fix_for_device(int device, NoiseFix& out, std::string& why) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    auto it = g_fix.find(device);
+    if (it != g_fix.end()) { out = it->second; return true; }
+    const uint32_t n = 1u << 24, words = n / 32;
+    std::vector<uint32_t> lfix(words, 0u), cfix(words, 0u);
+    std::atomic<uint32_t> bad_log{0xFFFFFFFFu}, bad_cos{0xFFFFFFFFu};
+    const unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    std::vector<std::thread> pool;
+    for (unsigned t = 0; t < nt; t++)
+        pool.emplace_back([&, t]() {
+            const uint32_t w0 = (uint32_t)((uint64_t)words * t / nt), w1 = (uint32_t)((uint64_t)words * (t + 1) / nt);
+            for (uint32_t w = w0; w < w1; w++) {
+                uint32_t lb = 0, cb = 0;
+                for (uint32_t j = 0; j < 32; j++) {
+                    const uint32_t k = 32 * w + j;
+                    const float lg = logf(nm_u1(k));
+                    const double dl = nm_log_u1(k);
+                    if ((float)dl != lg) {
+                        if (nm_toward((float)dl, dl) != lg) bad_log = k;
+                        lb |= 1u << j;
+                    }
+                    const float cg = cosf(nm_angle(k));
+                    const double dc = nm_cos(nm_angle(k));
+                    if ((float)dc != cg) {
+                        if (nm_toward((float)dc, dc) != cg) bad_cos = k;
+                        cb |= 1u << j;
+                    }
+                }
+                lfix[w] = lb; cfix[w] = cb;
+            }
+        });
+    for (auto& th : pool) th.join();
+    if (bad_log != 0xFFFFFFFFu || bad_cos != 0xFFFFFFFFu) {
+        char buf[256];
+        snprintf(buf, sizeof buf, "the host C library's %s differs from the rounded value by more than one float at argument %u; "
+                 "the device noise cannot reproduce it", bad_log != 0xFFFFFFFFu ? "logf" : "cosf",
+                 bad_log != 0xFFFFFFFFu ? (unsigned)bad_log : (unsigned)bad_cos);
+        why = buf;
+        return false;
+    }
+    uint32_t *l = nullptr, *c = nullptr;
+    NTC_CHECK(hipMalloc(&l, (size_t)words * sizeof(uint32_t)));
+    NTC_CHECK(hipMalloc(&c, (size_t)words * sizeof(uint32_t)));
+    NTC_CHECK(hipMemcpy(l, lfix.data(), (size_t)words * sizeof(uint32_t), hipMemcpyHostToDevice));
+    NTC_CHECK(hipMemcpy(c, cfix.data(), (size_t)words * sizeof(uint32_t), hipMemcpyHostToDevice));
+    out = NoiseFix{ l, c };
+    g_fix[device] = out;
+    return true;
+}
+
+}   // namespace ntc_hip

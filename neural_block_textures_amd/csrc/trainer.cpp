@@ -198,8 +198,8 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
     NTC_CHECK(hipGetDeviceProperties(&prop, I.device));
     I.dev_name = prop.name; I.arch = prop.gcnArchName; I.cus = prop.multiProcessorCount;
     NTC_CHECK(hipRuntimeGetVersion(&I.rt_ver));
+    if (!noise_fix_for_device(I.device, I.noise, why)) return false;
     NTC_CHECK(hipStreamCreateWithFlags(&I.stream, hipStreamNonBlocking));
-    I.noise = noise_tables_for_device(I.device);
 
     // ---- model description
     I.npix = (size_t)d.W * d.H;

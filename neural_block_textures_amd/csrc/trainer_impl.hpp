@@ -56,7 +56,7 @@ struct ntc_cuda::Trainer::Impl {
     ntc_hip::DevModel dm{};
     int device = 0;
     hipStream_t stream = nullptr;
-    ntc_hip::NoiseTables noise{};
+    ntc_hip::NoiseFix noise{};
     int P = 0;
     size_t nz = 0, npix = 0;
 
@@ -123,7 +123,9 @@ void resolve_times(Impl& I);
 inline int blocks_for(size_t n, int tpb) { return (int)((n + tpb - 1) / tpb); }
 
 // noise tables (one pair per device, filled from the host C library on first use)
-NoiseTables noise_tables_for_device(int device);
+// the device's noise correction bits (built once per device); false with a reason if the host's
+// C library cannot be reproduced
+bool noise_fix_for_device(int device, NoiseFix& out, std::string& why);
 
 // kernels_mlp.hip
 void launch_fill(Impl& I, float* p, size_t n, float v);
@@ -140,6 +142,8 @@ void launch_fd_finish(Impl& I, int chunks, double norm);
 void launch_adam(Impl& I, float* theta, const float* g, float* m, float* v, size_t n, float lr, int t);
 void launch_decode(Impl& I, const float* z);
 void launch_debug_gauss(Impl& I, uint32_t stream, uint32_t step, uint32_t pair, uint64_t index0, size_t n, float* out);
+// the device's two noise factors for arguments k0 .. k0 + n - 1 (device buffers)
+void launch_debug_factors(Impl& I, uint32_t k0, size_t n, float* rad, float* cosv);
 void launch_copy_calibration(Impl& I, const float* src, float* dst, size_t n);
 
 // kernels_latent.hip
