@@ -128,6 +128,79 @@ __global__ void __launch_bounds__(64 * kPopWaves) k_pop_mfma(DevModel m, const f
     }
 }
 
+// The latent pair evaluation (LatentTrainer::step_impl, main.cpp:1990-2007) on the matrix cores:
+// block (512 or 256 pixels, pair k). Phase 1: the threads build the features of each pixel with the
+// pair's texels perturbed by +sg eps and by -sg eps (features<S>, as the VALU kernel) into LDS.
+// Phase 2: each wave evaluates a quarter of the pixels in 16-pixel tiles, the + and - members of
+// a tile together; each pixel's error is the reference's float fma chain over its channels in
+// ascending order (decode_err), and dpix = (e+ - e-) * inv_px.
+// pixels per block: 512, or 256 for wide inputs (LDS)
+template <class S>
+constexpr int lat_pix() { return MfmaShape<S>::kIn <= 8 ? 512 : 256; }
+
+template <class S>
+__device__ __forceinline__ float out_of(float s, bool clamp) {
+    return clamp ? __builtin_amdgcn_fmed3f(s + 0.5f, 0.0f, 1.0f) : sigmoid_hw(s);
+}
+
+template <class S, bool LeakUnit, bool Clamp>
+__global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* __restrict__ w, const float* __restrict__ zdec,
+                                                      const float* __restrict__ eps, const float* __restrict__ tgt, float sg,
+                                                      unsigned mask, float* __restrict__ dpix) {
+    using Q = MfmaShape<S>;
+    constexpr int NIN = Q::kIn, NO = Q::kNout, kLatPix = lat_pix<S>(), LDW = kLatPix + 4;
+    __shared__ float F[2][NIN][LDW];
+    const int k = blockIdx.y, p0 = blockIdx.x * kLatPix;
+    const float* e = eps + (size_t)k * m.nz;
+    for (int q = threadIdx.x; q < kLatPix; q += 256) {
+        const int p = min(p0 + q, m.npix - 1);
+        float f[S::kMaxIn];
+        features<S>(m, PerturbedLatent{ zdec, e, sg, mask }, p % m.W, p / m.W, f);
+#pragma unroll
+        for (int i = 0; i < NIN; i++) F[0][i][q] = f[i];
+        features<S>(m, PerturbedLatent{ zdec, e, -sg, mask }, p % m.W, p / m.W, f);
+#pragma unroll
+        for (int i = 0; i < NIN; i++) F[1][i][q] = f[i];
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
+    MfmaWeights<S> W;
+    mfma_load<S>(W, w, lane);
+    float cw[4];
+    lane_cw<NO>(m.cw, g, cw);
+    float* out = dpix + (size_t)k * m.npix;
+    for (int u = 0; u < kLatPix / 64; u++) {   // kLatPix / 64 tiles of 16 pixels per wave
+        const int col = (kLatPix / 4) * wave + 16 * u + i16;
+        const int p = p0 + col;
+        const int pr = min(p, m.npix - 1);
+        float b1[2][Q::kKs1];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+            for (int ks = 0; ks < Q::kKs1; ks++) {
+                const int kk = 4 * ks + g;
+                const float v = F[s2][min(kk, NIN - 1)][col];
+                b1[s2][ks] = kk < NIN ? v : 0.0f;
+            }
+        float t[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) t[r] = tgt[(size_t)pr * NO + min(4 * g + r, NO - 1)];
+        f4v o[2];
+        mfma_forward<S, 2, LeakUnit>(W, b1, m.leak, o);
+        float dd[2][4];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float d = out_of<S>(o[s2][r], Clamp) - t[r];
+                dd[s2][r] = __fmul_rn(d, d);
+            }
+        const float ep = chain_err_f<NO>(dd[0], cw, lane);
+        const float em = chain_err_f<NO>(dd[1], cw, lane);
+        if (g == (NO - 1) / 4 && p < m.npix) out[p] = __fmul_rn(ep - em, m.inv_px);
+    }
+}
+
 bool pop_on_matrix_cores(const Impl& I) {
     bool ok = false;
     dispatch_shape(I.dm, [&](auto s) { ok = MfmaShape<decltype(s)>::kOk; });
@@ -171,6 +244,32 @@ void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks) {
         if constexpr (MfmaShape<S>::kOk) {
             if (I.dm.leak >= 0.0f && I.dm.leak <= 1.0f) launch_pop_mfma<S, true>(I, pairs, M, chunk, chunks);
             else launch_pop_mfma<S, false>(I, pairs, M, chunk, chunks);
+        }
+    });
+    NTC_CHECK(hipGetLastError());
+}
+
+bool lat_pair_on_matrix_cores(const Impl& I) { return pop_on_matrix_cores(I); }
+
+template <class S, bool LeakUnit>
+static void launch_lat_mfma(Impl& I, int K, float sigma, unsigned mask) {
+    auto kern = I.dm.clamp_out ? k_lat_pair_mfma<S, LeakUnit, true> : k_lat_pair_mfma<S, LeakUnit, false>;
+    constexpr int kLatPix = lat_pix<S>();
+    hipLaunchKernelGGL(kern, dim3((unsigned)((I.npix + kLatPix - 1) / kLatPix), K), dim3(256), 0, I.stream, I.dm, I.w, I.zdec,
+                       I.eps_lat, I.tgt, sigma, mask, I.dpix);
+}
+
+void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask) {
+    ProfScope ps(I, "lat_pair");
+    if (!lat_pair_on_matrix_cores(I)) {
+        launch_lat_pair_valu(I, K, sigma, mask);
+        return;
+    }
+    dispatch_shape(I.dm, [&](auto s) {
+        using S = decltype(s);
+        if constexpr (MfmaShape<S>::kOk) {
+            if (I.dm.leak >= 0.0f && I.dm.leak <= 1.0f) launch_lat_mfma<S, true>(I, K, sigma, mask);
+            else launch_lat_mfma<S, false>(I, K, sigma, mask);
         }
     });
     NTC_CHECK(hipGetLastError());

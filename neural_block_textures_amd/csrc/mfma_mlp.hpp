@@ -161,4 +161,60 @@ __device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const floa
         for (int u = 0; u < U; u++) o[u] = mfma4(W.ao[ks], x[u][ks], o[u]);
 }
 
+
+// ---- per-pixel error across the output tile
+// Lane (g, j) holds the output units 4 g + r of pixel j; the reference sums a pixel's channels
+// in ascending order. The running sum starts in lane group 0, each group adds its (up to) four
+// channels and hands the sum to the next group (ds_bpermute from lane - 16); the result is valid
+// in the lanes of group (NO - 1) / 4.
+__device__ __forceinline__ int lane_below_addr(int lane) { return ((lane - 16) & 63) << 2; }
+
+// decode_err (main.cpp:1731-1732): e = fma(cw, d d, e), float
+template <int NO>
+__device__ __forceinline__ float chain_err_f(const float (&dd)[4], const float (&cw)[4], int lane) {
+    constexpr int NG = (NO + 3) / 4;
+    const int from = lane_below_addr(lane);
+    float e = 0.0f;
+#pragma unroll
+    for (int gg = 0; gg < NG; gg++) {
+        if (gg > 0) e = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(e)));
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (4 * gg + r < NO) e = __builtin_fmaf(cw[r], dd[r], e);
+    }
+    return e;
+}
+
+// loss_subset's per-pixel terms (main.cpp:1747): s += (double)(cw (d d)), double
+template <int NO>
+__device__ __forceinline__ double chain_err_d(const float (&dd)[4], const float (&cw)[4], int lane) {
+    constexpr int NG = (NO + 3) / 4;
+    const int from = lane_below_addr(lane);
+    double e = 0.0;
+#pragma unroll
+    for (int gg = 0; gg < NG; gg++) {
+        if (gg > 0) {
+            const long long b = __double_as_longlong(e);
+            const int lo = __builtin_amdgcn_ds_bpermute(from, (int)(b & 0xFFFFFFFFll));
+            const int hi = __builtin_amdgcn_ds_bpermute(from, (int)(b >> 32));
+            e = __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (4 * gg + r < NO) e += (double)__fmul_rn(cw[r], dd[r]);
+    }
+    return e;
+}
+
+// the channel weights of this lane's output units (0 past nout)
+template <int NO>
+__device__ __forceinline__ void lane_cw(const float* cwm, int g, float (&cw)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        cw[r] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NO; c++) if (4 * g + r == c) cw[r] = cwm[c];
+    }
+}
+
 }   // namespace ntc_hip

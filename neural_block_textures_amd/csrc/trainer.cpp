@@ -219,6 +219,12 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
         }
         ranges.insert(ranges.end(), xb.begin(), xb.end()); ranges.insert(ranges.end(), xe.begin(), xe.end());
         ranges.insert(ranges.end(), yb.begin(), yb.end()); ranges.insert(ranges.end(), ye.begin(), ye.end());
+        if (l == 0) {   // level 0 with one pixel per texel (texel x covers exactly pixel x): the selector search's per-pixel form
+            bool unit = L.nearest && L.W == d.W && L.H == d.H;
+            for (int x = 0; unit && x < L.W; x++) unit = xb[x] == x && xe[x] == x + 1;
+            for (int y = 0; unit && y < L.H; y++) unit = yb[y] == y && ye[y] == y + 1;
+            I.lv0_unit_cells = unit;
+        }
     }
     for (int q = 0; q < d.npos; q++) m.pos[q] = d.pos[q].kind;
     for (int l = 0; l < d.nhidden; l++) m.hidden[l] = d.hidden[l];

@@ -79,6 +79,7 @@ struct ntc_cuda::Trainer::Impl {
     int* ranges = nullptr;     // per level: xb[W] xe[W] yb[H] ye[H] (pixel footprint of each texel row / column)
     float* qat_grid = nullptr; // 9 x 257
     int* qat_bits = nullptr;   // MAX_CH
+    bool lv0_unit_cells = false;   // level 0 nearest at the image's size: every texel's cell is its own pixel
 
     bool qes = false;
     ntc_cuda::QesDesc* qes_dev = nullptr;
@@ -148,6 +149,7 @@ void launch_copy_calibration(Impl& I, const float* src, float* dst, size_t n);
 
 // kernels_latent.hip
 void launch_lat_eps(Impl& I, int K, unsigned mask);
+void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask);
 void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask);
 void launch_lat_gather(Impl& I, int level, int K, float scale, bool rate);
 void launch_qat_search(Impl& I);
