@@ -1,23 +1,28 @@
 #!/usr/bin/env python3
-"""Benchmark: ES training iterations of one benchmark workload on one MI355X, with the
-reference's OpenMP CPU path timed beside it.
+"""Benchmark: ES training iterations of the benchmark workloads on one MI355X, with the
+reference's OpenMP CPU path timed beside them.
 
 A step is one ES iteration of the reference's per-iteration call sequence (main.cpp:4121-4148):
-MLP ES step, latent ES step, then the --qat selector search when the workload has one. Inputs are
-synthetic (neural_block_textures_amd/synth.py) and resident on the device before timing starts.
+MLP ES step, latent ES step, then the --qat selector search when the workload has one (a live
+--dct-q level 0 re-snaps and adds its rate pass inside the latent step). Inputs are synthetic
+(neural_block_textures_amd/synth.py) and resident on the device before timing starts.
 
     python bench.py [--steps K] [--warmup W] [--workload material512]
+    python bench.py --all-configs profiles/es_iterations_all_configs.md
 
-Prints one JSON line. value = every member-pixel MLP evaluation of the timed iterations (population,
-latent pairs, selector search) per second of wall time; roofline = the population-evaluation
-kernel's algorithmic FP32 FLOP per launch over its mean launch time (HIP events on the trainer's
-stream), against the MI355X FP32 peak.
+The default run prints one JSON line for material512. value = every member-pixel MLP evaluation
+of the timed iterations (population, latent pairs, selector search) per second of wall time;
+roofline = the population-evaluation kernel's algorithmic FP32 FLOP per launch over its mean launch
+time (HIP events on the trainer's stream), against the MI355X FP32 peak. --all-configs runs each of
+the five workloads (GPU ES iterations/s and a bounded sample of the reference's CPU loop) and
+writes a table.
 """
 from __future__ import annotations
 
 import argparse
 import ctypes as C
 import json
+import math
 import os
 import platform
 import sys
@@ -27,7 +32,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 FP32_PEAK_TFLOPS = 157.3
-HBM_PEAK_GBS = 8000.0
+METRIC = "member·pixel evals/sec + ES iterations/sec (512² 4-tex, pop 8192), % roofline"
+KERNELS = ("batch", "perturb", "pop_eval", "es_grad", "adam", "lat_eps", "lat_pair", "lat_gather", "qat_search", "decode",
+           "fd_sets", "qes_snap", "dct_snap", "dct_rate")
+DCT_CODE = 8          # the benchmark's constant scale code (the reference fits them from probes every 500 iterations)
+DCT_LAMBDA = 0.5      # the reference's default --dct-lambda at q 50: min(0.5, 7.5 S(q)^2)
+DCT_LO16 = 4          # the default --dct-lambda-lo 0.25 as round(16 W)
 
 
 def log(*a):
@@ -39,46 +49,113 @@ def macs(layout) -> int:
     return sum(w[i] * w[i + 1] for i in range(len(w) - 1))
 
 
-def evals_per_iter(w) -> dict:
+def evals_per_iter(w, pairs=None) -> dict:
     lay = w.layout
     npix = lay.W * lay.H
     active = [l for l in range(len(lay.levels)) if not (w.qat_bits and l == 0)]
-    e = {"population": 2 * w.mlp_pairs * w.mlp_batch, "latent": 2 * w.lat_pairs * npix if active else 0,
+    e = {"population": 2 * (pairs or w.mlp_pairs) * w.mlp_batch, "latent": 2 * w.lat_pairs * npix if active else 0,
          "qat": sum(1 << b for b in w.qat_bits) * npix if w.qat_bits else 0}
     e["total"] = sum(e.values())
     return e
 
 
-def cpu_model(lay):
-    from oracle.oracle import model_of
-    return model_of(lay)
+def inputs(w):
+    from neural_block_textures_amd import synth
+    lay = w.layout
+    maps = synth.material(w.seed, lay.W, lay.H) if lay.T == 4 else [synth.rgb_texture(w.seed, lay.W, lay.H)]
+    tgt = synth.target_from_maps(maps)
+    z, p = synth.init_model(lay, w.seed, qat_bits=w.qat_bits)
+    return z, p, tgt
 
 
-def cpu_baseline(w, z, p, tgt, seconds: float):
+def dct_host_state(w):
+    """codes, symbols, steps, lambda weights of the workload's DCT-coded level 0 (host side)"""
+    import numpy as np
+
+    from neural_block_textures_amd import dct_host
+    W0, H0, C0, _ = w.layout.levels[0]
+    n = (W0 // 8) * (H0 // 8) * C0
+    t16, scale = dct_host.lambda_weights(DCT_LAMBDA, w.layout.W, w.layout.H, True, True)
+    return {"C": C0, "BW": W0 // 8, "BH": H0 // 8, "n": n, "code": np.full(n, DCT_CODE, np.uint8),
+            "sym": np.zeros(n * 64, np.int16), "steps": np.concatenate([dct_host.steps(q, 4).reshape(-1) for q in w.dct_q]),
+            "lam_t16": t16, "rate_scale": scale}
+
+
+def make_trainer(w, z, p, tgt):
+    from neural_block_textures_amd import dct_host, synth
+    from neural_block_textures_amd.trainer import DctDesc, Trainer
+    lay = w.layout
+    kw = dict(max_pairs=w.mlp_pairs, max_batch=w.mlp_batch, seed=w.seed)
+    if w.qat_bits:
+        kw.update(qat_bits=w.qat_bits, qat_grid=synth.qat_grid())
+    if w.dct_q:
+        kw.update(dct={"C": lay.levels[0][2], "q": w.dct_q, "dc_step": 4}, dct_basis=dct_host.basis(),
+                  dct_zigzag=dct_host.zigzag())
+    tr = Trainer()
+    tr.init(Trainer.model_desc(lay, **kw), z, p, tgt, lay)
+    if w.dct_q:
+        h = dct_host_state(w)
+        d = DctDesc()
+        d.live, d.C, d.BW, d.BH, d.N, d.dc_step = 1, h["C"], h["BW"], h["BH"], 8, 4
+        d.rate_es, d.rate_trunc, d.rate_scale = 1, 1, h["rate_scale"]
+        for k in range(16):
+            d.lam_t16[k] = h["lam_t16"][k]
+        d.lo_w16, d.deadzone = DCT_LO16, 0
+        tr.set_dct(d, h["code"], h["sym"], h["steps"])
+    return tr
+
+
+def es_iter(tr, w, it):
+    tr.mlp_step(it, w.mlp_sigma, w.mlp_lr, w.mlp_pairs, w.mlp_batch)
+    tr.lat_step(it, w.lat_sigma, w.lat_lr, w.lat_pairs)
+    if w.qat_bits:
+        tr.qat_search()
+
+
+def cpu_baseline(w, z, p, tgt, seconds: float, pairs=None):
     """The reference's CPU training loop (main.cpp compiled with its own -O3 -ffast-math flags and
-    OpenMP, oracle/_ref/libntc_ref_fast.so) on the same inputs, for a bounded number of
-    iterations; falls back to the oracle's restatement when the reference build is absent."""
+    OpenMP, oracle/_ref/libntc_ref_fast.so) on the same inputs for a bounded number of iterations
+    (with `pairs` < the workload's population for a sample of a very large one); the oracle's
+    restatement where the reference build is absent."""
+    import numpy as np
+
     from oracle import oracle as O
-    mc = cpu_model(w.layout)
+    mc = O.model_of(w.layout)
     cfg = O.OrTrainCfg()
-    cfg.seed, cfg.mlp_pairs, cfg.mlp_batch, cfg.mlp_sigma, cfg.mlp_lr = w.seed, w.mlp_pairs, w.mlp_batch, w.mlp_sigma, w.mlp_lr
+    pairs = pairs or w.mlp_pairs
+    cfg.seed, cfg.mlp_pairs, cfg.mlp_batch, cfg.mlp_sigma, cfg.mlp_lr = w.seed, pairs, w.mlp_batch, w.mlp_sigma, w.mlp_lr
     cfg.lat_pairs, cfg.lat_sigma, cfg.lat_lr = w.lat_pairs, w.lat_sigma, w.lat_lr
     cfg.qat = max(w.qat_bits) if w.qat_bits else 0
     for c, b in enumerate(w.qat_bits or []):
         cfg.qat_ch[c] = b
     cfg.fd_from, cfg.fd_h = w.iters + 1, w.fd_h
-    ev = evals_per_iter(w)["total"]
+    ev = evals_per_iter(w, pairs)["total"]
+    keep = []
     if O.have_reference(fast=True):
-        ref = O.reference(fast=True)
-        L = ref.lib
-        h = L.ref_train_create(C.byref(mc), C.byref(cfg), z.ctypes.data, p.ctypes.data, tgt.ctypes.data)
+        L = O.reference(fast=True).lib
+        if w.dct_q:
+            h = dct_host_state(w)
+            d = O.OrDct()
+            d.C, d.BW, d.BH, d.dc_step, d.deadzone, d.lo_w16 = h["C"], h["BW"], h["BH"], 4, 0, DCT_LO16
+            for k in range(16):
+                d.lam_t16[k] = h["lam_t16"][k]
+            keep = [h["steps"], h["code"], h["sym"]]
+            d.step = h["steps"].ctypes.data_as(C.POINTER(C.c_int))
+            d.code = h["code"].ctypes.data_as(C.POINTER(C.c_uint8))
+            d.sym = h["sym"].ctypes.data_as(C.POINTER(C.c_int16))
+            hnd = L.ref_train_create_dct(C.byref(mc), C.byref(cfg), z.ctypes.data, p.ctypes.data, tgt.ctypes.data, C.byref(d),
+                                         DCT_LAMBDA, 1, 1)
+        else:
+            hnd = L.ref_train_create(C.byref(mc), C.byref(cfg), z.ctypes.data, p.ctypes.data, tgt.ctypes.data)
         threads = L.ref_omp_threads()
-        step = lambda it: L.ref_train_iter(h, it, w.iters)
+        step = lambda it: L.ref_train_iter(hnd, it, w.iters)
         kind = "reference"
     else:
+        if w.dct_q:
+            return None
         orc = O.oracle()
         st = O.OrTrainState()
-        arrs = [z.copy(), p.copy()] + [__import__("numpy").zeros_like(a) for a in (p, p, z, z)]
+        arrs = [z.copy(), p.copy()] + [np.zeros_like(a) for a in (p, p, z, z)]
         F = lambda a: a.ctypes.data_as(C.POINTER(C.c_float))
         st.z, st.p, st.wm, st.wv, st.zm, st.zv = (F(a) for a in arrs)
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
@@ -93,10 +170,123 @@ def cpu_baseline(w, z, p, tgt, seconds: float):
         if el >= seconds or its >= 1000:
             break
     if kind == "reference":
-        L.ref_train_destroy(h)
-    return {"value": ev * its / el, "unit": "member·pixel evals/s", "cores": threads, "kind": kind,
-            "sample": f"{its} ES iteration(s) of {w.name} (the full per-iteration sequence at full size), {el:.1f} s",
+        L.ref_train_destroy(hnd)
+    del keep
+    sample = f"{its} ES iteration(s) of {w.name} (the full per-iteration sequence at full size), {el:.1f} s"
+    if pairs != w.mlp_pairs:
+        sample = (f"{its} ES iteration(s) of {w.name} with {pairs} of its {w.mlp_pairs} pairs (population evaluation scaled "
+                  f"down, everything else at full size), {el:.1f} s")
+    return {"value": ev * its / el, "unit": "member·pixel evals/s", "cores": threads, "kind": kind, "sample": sample,
             "es_iters_per_s": its / el, "cpu": platform.processor() or platform.machine()}
+
+
+def run_gpu(w, steps, warmup, fd_steps=0, seconds=0.0):
+    """GPU ES iterations of workload w; with seconds > 0 the step count is chosen to time about that long."""
+    import numpy as np
+    z, p, tgt = inputs(w)
+    tr = make_trainer(w, z, p, tgt)
+    log(f"bench: {w.name}:", tr.banner())
+    it = 0
+    for _ in range(warmup):
+        it += 1
+        es_iter(tr, w, it)
+    tr.synchronize()
+    if seconds > 0:
+        t0 = time.perf_counter()
+        for _ in range(2):
+            it += 1
+            es_iter(tr, w, it)
+        tr.synchronize()
+        per = (time.perf_counter() - t0) / 2
+        steps = int(min(2000, max(3, math.ceil(seconds / per))))
+    # the timed region, every launch bracketed by HIP events on the trainer's stream
+    tr.set_profiling(True)
+    tr.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        it += 1
+        es_iter(tr, w, it)
+    tr.synchronize()
+    el = time.perf_counter() - t0
+    kernels = {}
+    for name in KERNELS:
+        ms, n = tr.kernel_time(name)
+        if n:
+            kernels[name] = {"ms_total": round(ms, 3), "launches": n, "ms_mean": round(ms / n, 4)}
+    tr.set_profiling(False)
+    fd = None
+    if fd_steps > 0:
+        tr.reset_mlp_adam()
+        tr.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(fd_steps):
+            it += 1
+            tr.mlp_step_fd(it, np.float32(w.fd_h), w.mlp_lr, w.mlp_batch)
+            tr.lat_step(it, w.lat_sigma, w.lat_lr, w.lat_pairs)
+            if w.qat_bits:
+                tr.qat_search()
+        tr.synchronize()
+        fd_el = time.perf_counter() - t1
+        fd = {"iters_per_s": fd_steps / fd_el, "ms_per_iter": 1e3 * fd_el / fd_steps,
+              "evals_per_s": (2 * (w.layout.nparams + 1) * w.mlp_batch) * fd_steps / fd_el}
+    loss, _ = tr.mlp_stats()
+    img = tr.decode_full()
+    assert np.isfinite(img).all() and np.isfinite(loss)
+    name = "k_pop_mfma" if tr.on_matrix_cores("pop_eval") else "k_pop_eval"
+    tr.close()
+    return {"z": z, "p": p, "tgt": tgt, "steps": steps, "el": el, "kernels": kernels, "fd": fd, "loss": loss, "pop_kernel": name}
+
+
+def roofline_of(w, r):
+    ev = evals_per_iter(w)
+    pe = r["kernels"]["pop_eval"]
+    pop_flop = ev["population"] * 2 * macs(w.layout)
+    achieved = pop_flop / (pe["ms_mean"] * 1e-3) / 1e12
+    roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": None, "kernel": r["pop_kernel"],
+            "flop_per_launch": pop_flop, "ms_per_launch": pe["ms_mean"]}
+    # HBM bytes per launch from the committed counter runs (FETCH_SIZE and WRITE_SIZE, each scaled by the
+    # same counter's reading for a plain copy of known size): profiles/traffic_<workload>.json
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{w.name}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            t = json.load(f)
+        roof["traffic"] = t.get("pop_eval_bytes_per_launch")
+        roof["traffic_source"] = os.path.relpath(tpath, ROOT)
+    return roof
+
+
+def all_configs(out_path: str, cpu_seconds: float):
+    from neural_block_textures_amd.configs import workloads
+    rows = []
+    for name, w in workloads().items():
+        r = run_gpu(w, 0, 3, seconds=2.0)
+        gpu_its = r["steps"] / r["el"]
+        ev = evals_per_iter(w)
+        # a population too large for a bounded CPU sample (over about 4 TFLOP per iteration) is sampled with 64 pairs
+        pairs = w.mlp_pairs if ev["total"] * 2 * macs(w.layout) < 4e12 else 64
+        log(f"bench: {name}: GPU {gpu_its:.2f} it/s; CPU sample ...")
+        cpu = cpu_baseline(w, r["z"], r["p"], r["tgt"], cpu_seconds, pairs=pairs) if cpu_seconds > 0 else None
+        cpu_its = cpu["value"] / ev["total"] if cpu else None   # full-size iterations per second at the sampled rate
+        row = {"workload": name, "gpu_es_iters_per_s": gpu_its, "gpu_ms_per_iter": 1e3 / gpu_its, "gpu_steps": r["steps"],
+               "gpu_evals_per_s": ev["total"] * gpu_its, "evals_per_iter": ev, "roofline": roofline_of(w, r),
+               "kernels": r["kernels"], "cpu": cpu, "cpu_es_iters_per_s": cpu_its,
+               "speedup": gpu_its / cpu_its if cpu_its else None}
+        print(json.dumps(row), flush=True)
+        rows.append(row)
+    with open(out_path, "w") as f:
+        f.write("# ES iterations per second, all five workloads (one MI355X vs the reference's CPU loop)\n\n")
+        f.write("Command (from the repository root on the MI355X box):\n\n```\n" + " ".join(["python3"] + sys.argv) + "\n```\n\n")
+        f.write("| workload | GPU ES it/s | GPU ms/iter | member-pixel evals/iter | population kernel | TFLOP/s | % of 157.3 "
+                "| CPU ES it/s | CPU threads | speedup | CPU sample |\n|---|---|---|---|---|---|---|---|---|---|---|\n")
+        for row in rows:
+            c = row["cpu"] or {}
+            rf = row["roofline"]
+            f.write(f"| {row['workload']} | {row['gpu_es_iters_per_s']:.2f} | {row['gpu_ms_per_iter']:.3f} | "
+                    f"{row['evals_per_iter']['total']:,} | `{rf['kernel']}` {rf['ms_per_launch']:.4f} ms | {rf['achieved']:.1f} | "
+                    f"{100 * rf['frac']:.1f}% | {row['cpu_es_iters_per_s'] or 0:.3g} | {c.get('cores', '-')} | "
+                    f"{row['speedup'] or 0:.0f}x | {c.get('sample', '-')} |\n")
+    log(f"bench: wrote {out_path}")
 
 
 def main():
@@ -107,6 +297,7 @@ def main():
     ap.add_argument("--workload", default="material512")
     ap.add_argument("--fd-steps", type=int, default=5, help="extra timed --mlp-fd iterations, reported apart")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bounded CPU-baseline sample (0 = skip)")
+    ap.add_argument("--all-configs", metavar="OUT_MD", help="run the five workloads and write a table")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="FLOATS",
                     help="only run a plain device copy of FLOATS floats three times (the reference for memory counters)")
     args = ap.parse_args()
@@ -120,12 +311,9 @@ def main():
 
     from neural_block_textures_amd import synth
     from neural_block_textures_amd.configs import workloads
-    from neural_block_textures_amd.trainer import Trainer
+    from neural_block_textures_amd.trainer import Layout, Trainer
 
-    w = workloads()[args.workload]
-    lay = w.layout
     if args.copy_calibration:
-        from neural_block_textures_amd.trainer import Layout
         small = Layout(8, 8, [(8, 8, 4, False)], [16, 16])
         zc, pc = synth.init_model(small, 1)
         tc = Trainer()
@@ -135,99 +323,38 @@ def main():
         tc.close()
         print(json.dumps({"copy_calibration": {"floats": n, "bytes_read": 4 * n, "bytes_written": 4 * n, "reps": 3}}))
         return
+    if args.all_configs:
+        all_configs(args.all_configs, args.cpu_seconds)
+        return
+
+    w = workloads()[args.workload]
+    lay = w.layout
     log(f"bench: {w.name} {lay.W}x{lay.H}x{lay.T} levels {lay.levels} mlp {lay.nin}->{lay.hidden}->{lay.nout} "
         f"pairs {w.mlp_pairs} batch {w.mlp_batch}")
-    maps = synth.material(w.seed, lay.W, lay.H) if lay.T == 4 else [synth.rgb_texture(w.seed, lay.W, lay.H)]
-    tgt = synth.target_from_maps(maps)
-    z, p = synth.init_model(lay, w.seed, qat_bits=w.qat_bits)
-    tr = Trainer()
-    tr.init(Trainer.model_desc(lay, max_pairs=w.mlp_pairs, max_batch=w.mlp_batch, seed=w.seed, qat_bits=w.qat_bits,
-                               qat_grid=synth.qat_grid() if w.qat_bits else None), z, p, tgt, lay)
-    log("bench:", tr.banner())
-
-    def es_iter(it):
-        tr.mlp_step(it, w.mlp_sigma, w.mlp_lr, w.mlp_pairs, w.mlp_batch)
-        tr.lat_step(it, w.lat_sigma, w.lat_lr, w.lat_pairs)
-        if w.qat_bits:
-            tr.qat_search()
-
-    it = 0
-    for _ in range(args.warmup):
-        it += 1
-        es_iter(it)
-    tr.synchronize()
-    tr.set_profiling(True)
-    tr.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        it += 1
-        es_iter(it)
-    tr.synchronize()
-    el = time.perf_counter() - t0
-    kernels = {}
-    for name in ("batch", "perturb", "pop_eval", "es_grad", "adam", "lat_eps", "lat_pair", "lat_gather", "qat_search",
-                 "decode", "fd_sets", "qes_snap", "dct_snap", "dct_rate"):
-        ms, n = tr.kernel_time(name)
-        if n:
-            kernels[name] = {"ms_total": round(ms, 3), "launches": n, "ms_mean": round(ms / n, 4)}
-    tr.set_profiling(False)
-    fd = None
-    if args.fd_steps > 0:
-        tr.reset_mlp_adam()
-        tr.synchronize()
-        t1 = time.perf_counter()
-        for _ in range(args.fd_steps):
-            it += 1
-            tr.mlp_step_fd(it, np.float32(w.fd_h), w.mlp_lr, w.mlp_batch)
-            tr.lat_step(it, w.lat_sigma, w.lat_lr, w.lat_pairs)
-            if w.qat_bits:
-                tr.qat_search()
-        tr.synchronize()
-        fd_el = time.perf_counter() - t1
-        fd = {"iters_per_s": args.fd_steps / fd_el, "ms_per_iter": 1e3 * fd_el / args.fd_steps,
-              "evals_per_s": (2 * (lay.nparams + 1) * w.mlp_batch) * args.fd_steps / fd_el}
-    loss, dstd = tr.mlp_stats()
-    img = tr.decode_full()
-    assert np.isfinite(img).all() and np.isfinite(loss)
-    tr.close()
-
-    ev = evals_per_iter(w)
-    flop_per_eval = 2 * macs(lay)
-    pe = kernels["pop_eval"]
-    pop_flop = ev["population"] * flop_per_eval
-    achieved = pop_flop / (pe["ms_mean"] * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": None,
-                "kernel": "k_pop_eval", "flop_per_launch": pop_flop, "ms_per_launch": pe["ms_mean"]}
-    # HBM bytes per launch from the committed counter runs (FETCH_SIZE and WRITE_SIZE, each scaled by the
-    # same counter's reading for a plain copy of known size): profiles/traffic_<workload>.json
-    tpath = os.path.join(ROOT, "profiles", f"traffic_{w.name}.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            t = json.load(f)
-        roofline["traffic"] = t.get("pop_eval_bytes_per_launch")
-        roofline["traffic_source"] = os.path.relpath(tpath, ROOT)
+    r = run_gpu(w, args.steps, args.warmup, fd_steps=args.fd_steps)
     cpu = None
     if args.cpu_seconds > 0:
         log(f"bench: CPU baseline for {args.cpu_seconds:.0f} s ...")
-        cpu = cpu_baseline(w, z, p, tgt, args.cpu_seconds)
-    value = ev["total"] * args.steps / el
+        cpu = cpu_baseline(w, r["z"], r["p"], r["tgt"], args.cpu_seconds)
+    ev = evals_per_iter(w)
+    el = r["el"]
+    pe = r["kernels"]["pop_eval"]
     out = {
-        "metric": "member·pixel evals/sec + ES iterations/sec (512² 4-tex, pop 8192), % roofline",
-        "value": value, "unit": "member·pixel evals/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": 1e3 * el / args.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32", "data": "synthetic",
+        "metric": METRIC,
+        "value": ev["total"] * args.steps / el, "unit": "member·pixel evals/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": 1e3 * el / args.steps, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": w.name, "image": [lay.W, lay.H, lay.T], "levels": [list(l) for l in lay.levels],
                    "mlp": [lay.nin] + list(lay.hidden) + [lay.nout], "population": w.population,
-                   "minibatch": w.mlp_batch, "lat_pairs": w.lat_pairs, "qat": w.qat_bits},
+                   "minibatch": w.mlp_batch, "lat_pairs": w.lat_pairs, "qat": w.qat_bits, "dct_q": w.dct_q},
         "es_iters_per_s": args.steps / el,
         "evals_per_iter": ev,
         "population_evals_per_s": ev["population"] / (pe["ms_mean"] * 1e-3),
-        "roofline": roofline,
+        "roofline": roofline_of(w, r),
         "cpu_baseline": cpu,
-        "fd_phase": fd,
-        "kernels": kernels,
-        "batch_loss": loss,
+        "fd_phase": r["fd"],
+        "kernels": r["kernels"],
+        "batch_loss": r["loss"],
     }
     print(json.dumps(out), flush=True)
 

@@ -128,6 +128,8 @@ void ntc_trainer_synchronize(ntc_trainer* t);
  * of the named kernel family ("pop_eval", "lat_pair", "qat_search", ...). */
 void ntc_trainer_set_profiling(ntc_trainer* t, int on);
 int ntc_trainer_kernel_time(ntc_trainer* t, const char* name, double* total_ms, long long* launches);
+// 1 if the stage ("pop_eval", "lat_pair", "qat_search") runs on the FP32 matrix cores for this model, else 0
+int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage);
 /* the device's Gaussian draws for indices index0 .. index0 + n - 1 of one (seed, stream, step, pair) */
 void ntc_trainer_debug_gauss(ntc_trainer* t, uint32_t stream, uint32_t step, uint32_t pair, uint64_t index0, size_t n,
                              float* out);

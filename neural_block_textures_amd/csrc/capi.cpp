@@ -152,6 +152,15 @@ void ntc_trainer_set_profiling(ntc_trainer* t, int on) {
     I.profiling = on != 0;
     if (on) I.times.clear();
 }
+int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage) {
+    const auto& I = *t->t.im;
+    const std::string s = stage ? stage : "";
+    if (s == "pop_eval") return ntc_hip::pop_on_matrix_cores(I) ? 1 : 0;
+    if (s == "lat_pair") return ntc_hip::lat_pair_on_matrix_cores(I) ? 1 : 0;
+    if (s == "qat_search") return ntc_hip::qat_on_matrix_cores(I) ? 1 : 0;
+    return 0;
+}
+
 int ntc_trainer_kernel_time(ntc_trainer* t, const char* name, double* total_ms, long long* launches) {
     auto& I = *t->t.im;
     ntc_hip::resolve_times(I);

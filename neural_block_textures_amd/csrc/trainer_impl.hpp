@@ -133,6 +133,10 @@ void launch_fill(Impl& I, float* p, size_t n, float v);
 void launch_batch(Impl& I, int it, int M);
 void launch_perturb(Impl& I, int it, float sigma, int N);
 void launch_fd_sets(Impl& I, float h);
+// which stages run on the matrix cores for this trainer's model
+bool pop_on_matrix_cores(const Impl& I);
+bool lat_pair_on_matrix_cores(const Impl& I);
+bool qat_on_matrix_cores(const Impl& I);
 // minibatch slots per population-evaluation block for a population of `pairs` pairs
 int pop_chunk(const Impl& I, int pairs, int M);
 void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks);

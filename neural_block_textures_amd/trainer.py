@@ -101,6 +101,7 @@ def library() -> C.CDLL:
             "ntc_trainer_synchronize": (None, [P]),
             "ntc_trainer_set_profiling": (None, [P, C.c_int]),
             "ntc_trainer_kernel_time": (C.c_int, [P, C.c_char_p, P, P]),
+            "ntc_trainer_on_matrix_cores": (C.c_int, [P, C.c_char_p]),
             "ntc_trainer_debug_gauss": (None, [P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, C.c_size_t, P]),
             "ntc_trainer_debug_noise_factors": (None, [P, C.c_uint32, C.c_size_t, P, P]),
             "ntc_trainer_debug_copy_calibration": (None, [P, C.c_size_t, C.c_int]),
@@ -377,6 +378,10 @@ class Trainer:
 
     def set_profiling(self, on: bool):
         self._lib.ntc_trainer_set_profiling(self._h, 1 if on else 0)
+
+    def on_matrix_cores(self, stage: str) -> bool:
+        """whether the stage ("pop_eval", "lat_pair", "qat_search") runs on the FP32 matrix cores"""
+        return bool(self._lib.ntc_trainer_on_matrix_cores(self._h, stage.encode()))
 
     def kernel_time(self, name):
         ms, n = C.c_double(), C.c_longlong()

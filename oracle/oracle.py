@@ -233,6 +233,8 @@ class Lib:
             L.ref_ntcb_selfcheck.restype = C.c_int
             L.ref_train_create.restype = C.c_void_p
             L.ref_train_create.argtypes = [_P, _P, _P, _P, _P]
+            L.ref_train_create_dct.restype = C.c_void_p
+            L.ref_train_create_dct.argtypes = [_P, _P, _P, _P, _P, _P, C.c_float, C.c_int, C.c_int]
             L.ref_train_iter.restype = C.c_double
             L.ref_train_iter.argtypes = [C.c_void_p, C.c_int, C.c_int]
             L.ref_train_get.argtypes = [C.c_void_p, _P, _P]

@@ -274,6 +274,18 @@ void* ref_train_create(const OrModel* m, const OrTrainCfg* c, const float* z, co
     T->lt.init(T->R.D.lat.size());
     return T;
 }
+// The same loop with a live DCT-coded level 0 (codes and steps given): every decode reads the snapped
+// plane, the latent step adds the rate pass with --dct-lambda part A and re-snaps (main.cpp:1638-1648, 1972).
+void* ref_train_create_dct(const OrModel* m, const OrTrainCfg* c, const float* z, const float* p, const float* tgt,
+                           const OrDct* d, float lambda, int rate_es, int rate_trunc) {
+    RefTrain* T = (RefTrain*)ref_train_create(m, c, z, p, tgt);
+    Decoder& D = T->R.D;
+    D.dct = dct_level_of(d);
+    D.dct.lambda = lambda; D.dct.rate_es = rate_es != 0; D.dct.rate_trunc = rate_trunc != 0;
+    D.zq.assign(D.lat.z.size(), 0.0f);
+    D.qes_refresh();
+    return T;
+}
 double ref_train_iter(void* h, int it, int iters) {
     RefTrain& T = *(RefTrain*)h;
     Decoder& D = T.R.D; const Options& o = T.R.o;
