@@ -6,8 +6,12 @@
 // SIMD (a 16x16x4 f32 step costs 32 cycles, a VALU instruction 4, and their mixes take the sum),
 // so everything around the matrix operations is counted in instructions: the activation is one
 // v_max_f32 (this file is compiled with relaxed NaN handling and the IEEE mode bit off, so the
-// maximum needs no canonicalising copies); the sigmoid is the hardware exp2 and reciprocal; tile
-// inputs are loaded with a wave-uniform SGPR base and loop-invariant 32-bit lane offsets.
+// maximum needs no canonicalising copies); a hidden layer's outputs feed the next layer in the order
+// the matrix instruction leaves them (no transpose; each unit's sum takes its inputs in another
+// order than the reference's ascending one); the sigmoid is the hardware exp2 and reciprocal; tile
+// inputs are loaded with a wave-uniform SGPR base and loop-invariant 32-bit lane offsets. Member
+// losses stay within 1e-5 relative of the reference's (they are not bit-identical here anyway:
+// the sigmoid differs in the last bits).
 //
 // Block (pair, chunk) has four waves: wave w evaluates member 2 pair + (w & 1) on the 16-slot
 // tiles 2 j + (w >> 1) of the chunk, two tiles at a time, the next two tiles' inputs loading
@@ -63,7 +67,7 @@ __global__ void __launch_bounds__(64 * kPopWaves) k_pop_mfma(DevModel m, const f
     const int pair = blockIdx.x, ch = blockIdx.y, sgn = wave & 1, half = wave >> 1;
     const int i16 = lane & 15, g = lane >> 4;
     MfmaWeights<S> W;
-    mfma_load<S>(W, wsets + (size_t)(2 * pair + sgn) * m.P, lane);
+    mfma_load<S, false>(W, wsets + (size_t)(2 * pair + sgn) * m.P, lane);
     float cw[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -96,7 +100,7 @@ __global__ void __launch_bounds__(64 * kPopWaves) k_pop_mfma(DevModel m, const f
                 if (4 * (Q::kKs1 - 1) + g >= Q::kIn) cur.b1[u][Q::kKs1 - 1] = 0.0f;
         }
         f4v o[kPopU];
-        mfma_forward<S, kPopU, LeakUnit>(W, cur.b1, m.leak, o);
+        mfma_forward<S, kPopU, LeakUnit, false>(W, cur.b1, m.leak, o);
 #pragma unroll
         for (int u = 0; u < kPopU; u++) {
             const int st = s0 + 16 * (2 * (j + u) + half);   // first slot of the tile (uniform)
@@ -165,7 +169,7 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
     MfmaWeights<S> W;
-    mfma_load<S>(W, w, lane);
+    mfma_load<S, false>(W, w, lane);
     float cw[4];
     lane_cw<NO>(m.cw, g, cw);
     float* out = dpix + (size_t)k * m.npix;
@@ -186,7 +190,7 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
 #pragma unroll
         for (int r = 0; r < 4; r++) t[r] = tgt[(size_t)pr * NO + min(4 * g + r, NO - 1)];
         f4v o[2];
-        mfma_forward<S, 2, LeakUnit>(W, b1, m.leak, o);
+        mfma_forward<S, 2, LeakUnit, false>(W, b1, m.leak, o);
         float dd[2][4];
 #pragma unroll
         for (int s2 = 0; s2 < 2; s2++)

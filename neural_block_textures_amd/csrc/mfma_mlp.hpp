@@ -34,6 +34,10 @@ struct MfmaShape<S, true> {
     static constexpr int kDeep = kNL > 1 ? kNL - 1 : 1;
 };
 
+// The hidden-layer input that lane group g feeds at k-step ks (see mfma_load).
+template <bool Exact>
+__device__ __forceinline__ int hidden_input(int ks, int g) { return Exact ? 4 * ks + g : 16 * (ks >> 2) + 4 * g + (ks & 3); }
+
 // One member's parameters in operand layout.
 template <class S>
 struct MfmaWeights {
@@ -47,8 +51,12 @@ struct MfmaWeights {
 };
 
 // Gathers a member's flat parameter vector (per layer W[out][in] row-major, then b[out]) into
-// operand layout; lane = threadIdx.x % 64.
-template <class S>
+// operand layout; lane = threadIdx.x % 64. Exact: the k-steps of a layer fed by a hidden layer take
+// the inputs in ascending order (k-step ks = inputs 4 ks .. 4 ks + 3; the activations are transposed
+// to match). Otherwise k-step 4 t + r takes inputs 16 t + 4 q + r (q = 0..3), the order in which a
+// 16-unit tile's D registers hold them, and the activations feed the next layer untransposed: the
+// same products, summed in another order.
+template <class S, bool Exact = true>
 __device__ __forceinline__ void mfma_load(MfmaWeights<S>& W, const float* __restrict__ w, int lane) {
     using Q = MfmaShape<S>;
     constexpr int NIN = Q::kIn, H = Q::kH, NO = Q::kNout;
@@ -69,14 +77,14 @@ __device__ __forceinline__ void mfma_load(MfmaWeights<S>& W, const float* __rest
 #pragma unroll
         for (int ot = 0; ot < Q::kHt; ot++) {
 #pragma unroll
-            for (int ks = 0; ks < Q::kKsH; ks++) W.ah[l][ot][ks] = p[(16 * ot + i16) * H + 4 * ks + g];
+            for (int ks = 0; ks < Q::kKsH; ks++) W.ah[l][ot][ks] = p[(16 * ot + i16) * H + hidden_input<Exact>(ks, g)];
 #pragma unroll
             for (int r = 0; r < 4; r++) W.ch[l][ot][r] = p[H * H + 16 * ot + 4 * g + r];
         }
         p += H * H + H;
     }
 #pragma unroll
-    for (int ks = 0; ks < Q::kKsH; ks++) W.ao[ks] = i16 < NO ? p[i16 * H + 4 * ks + g] : 0.0f;
+    for (int ks = 0; ks < Q::kKsH; ks++) W.ao[ks] = i16 < NO ? p[i16 * H + hidden_input<Exact>(ks, g)] : 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; r++) W.co[r] = 4 * g + r < NO ? p[NO * H + 4 * g + r] : 0.0f;
 }
@@ -105,7 +113,8 @@ __device__ __forceinline__ float act(float x, float leak) {
 // the other's matrix operations): b1[u] = the first layer's B operands of tile u (input 4 ks + l / 16
 // of pixel l % 16, zero past nin); returns the output layer's pre-activations of each tile in D layout
 // (lane l, register r = output 4 (l / 16) + r of pixel l % 16). Every lane of the wave must be active.
-template <class S, int U, bool LeakUnit>
+// Exact must match the weights' mfma_load.
+template <class S, int U, bool LeakUnit, bool Exact = true>
 __device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const float (&b1)[U][MfmaShape<S>::kKs1], float leak,
                                              f4v (&o)[U]) {
     using Q = MfmaShape<S>;
@@ -128,7 +137,11 @@ __device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const floa
             for (int ot = 0; ot < Q::kHt; ot++) {
 #pragma unroll
                 for (int r = 0; r < 4; r++) acc[u][ot][r] = act<LeakUnit>(acc[u][ot][r], leak);
-                transpose4(acc[u][ot], x[u] + 4 * ot);
+                if constexpr (Exact) transpose4(acc[u][ot], x[u] + 4 * ot);
+                else {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) x[u][4 * ot + r] = acc[u][ot][r];
+                }
             }
     }
 #pragma unroll
@@ -150,7 +163,11 @@ __device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const floa
             for (int ot = 0; ot < Q::kHt; ot++) {
 #pragma unroll
                 for (int r = 0; r < 4; r++) acc[u][ot][r] = act<LeakUnit>(acc[u][ot][r], leak);
-                transpose4(acc[u][ot], x[u] + 4 * ot);
+                if constexpr (Exact) transpose4(acc[u][ot], x[u] + 4 * ot);
+                else {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) x[u][4 * ot + r] = acc[u][ot][r];
+                }
             }
     }
 #pragma unroll
