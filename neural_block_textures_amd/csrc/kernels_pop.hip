@@ -1,6 +1,7 @@
 // The population evaluation (MlpTrainer::step's member losses, main.cpp:1848-1861) on the FP32
 // matrix cores of gfx950, for the fixed shapes whose hidden width is a multiple of 16; other
-// shapes use the VALU kernel of kernels_mlp.hip.
+// shapes use the VALU kernel of kernels_mlp.hip. In an ES step the kernel draws the pair's
+// perturbation itself (no member weight sets in memory).
 //
 // On this chip an FP32 matrix instruction and a VALU instruction do not run concurrently on a
 // SIMD (a 16x16x4 f32 step costs 32 cycles, a VALU instruction 4, and their mixes take the sum),
@@ -56,18 +57,41 @@ __device__ __forceinline__ float sigmoid_hw(float s) {
     return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(s * -1.44269504088896341f));
 }
 
-template <class S, bool LeakUnit, bool Clamp>
-__global__ void __launch_bounds__(64 * kPopWaves) k_pop_mfma(DevModel m, const float* __restrict__ wsets, int M, int Mcap,
+// Where a member's parameters come from: the weight sets of a central-difference step (wsets), or -
+// in an ES step - the block's own draw of the pair's Gaussians (NS_MLP, step, pair, k), written once
+// to LDS (and, by the chunk-0 block, to eps for the update), each weight w0 +- sigma eps as one fused
+// operation (main.cpp:1852-1856).
+struct PopSource {
+    const float* wsets;                    // central differences: 2 pairs x P
+    NoiseFix nt; uint64_t seed; uint32_t step; float sigma;
+    const float* w0; float* eps;           // ES: the current weights and the step's Gaussians [pair][P]
+};
+
+template <class S, bool LeakUnit, bool Clamp, bool Es>
+__global__ void __launch_bounds__(64 * kPopWaves) k_pop_mfma(DevModel m, PopSource src, int M, int Mcap,
                                                            int chunk, int chunks, const float* __restrict__ feat,
                                                            const float* __restrict__ btgt, double* __restrict__ part) {
     using Q = MfmaShape<S>;
     __shared__ double red[kPopWaves];
+    __shared__ float eps_s[Es ? Q::kP : 1];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int pair = blockIdx.x, ch = blockIdx.y, sgn = wave & 1, half = wave >> 1;
     const int i16 = lane & 15, g = lane >> 4;
     MfmaWeights<S> W;
-    mfma_load<S, false>(W, wsets + (size_t)(2 * pair + sgn) * m.P, lane);
+    if constexpr (Es) {
+        const uint64_t head = noise_head(src.seed, NS_MLP, src.step, (uint32_t)pair);
+        float* eg = src.eps + (size_t)pair * Q::kP;
+        for (int k = threadIdx.x; k < Q::kP; k += 64 * kPopWaves) {
+            const float e = gauss_at(src.nt, head, (uint64_t)k);
+            eps_s[k] = e;
+            if (ch == 0) eg[k] = e;
+        }
+        __syncthreads();
+        mfma_load_from<S, false>(W, PerturbedParams{ src.w0, eps_s, sgn ? -src.sigma : src.sigma }, lane);
+    } else {
+        mfma_load<S, false>(W, src.wsets + (size_t)(2 * pair + sgn) * Q::kP, lane);
+    }
     float cw[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -221,36 +245,61 @@ int pop_chunk(const Impl& I, int pairs, int M) {
     return std::min(M, 1024);
 }
 
-template <class S, bool LeakUnit>
-static void launch_pop_mfma(Impl& I, int pairs, int M, int chunk, int chunks) {
-    auto kern = I.dm.clamp_out ? k_pop_mfma<S, LeakUnit, true> : k_pop_mfma<S, LeakUnit, false>;
-    hipLaunchKernelGGL(kern, dim3(pairs, chunks), dim3(64 * kPopWaves), 0, I.stream, I.dm, I.wsets, M, I.Mcap, chunk, chunks, I.feat,
+template <class S, bool LeakUnit, bool Es>
+static void launch_pop_mfma(Impl& I, const PopSource& src, int pairs, int M, int chunk, int chunks) {
+    auto kern = I.dm.clamp_out ? k_pop_mfma<S, LeakUnit, true, Es> : k_pop_mfma<S, LeakUnit, false, Es>;
+    hipLaunchKernelGGL(kern, dim3(pairs, chunks), dim3(64 * kPopWaves), 0, I.stream, I.dm, src, M, I.Mcap, chunk, chunks, I.feat,
                        I.btgt, I.part);
 }
 
-void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks) {
-    ProfScope ps(I, "pop_eval");
+static void check_pop_launch(const Impl& I, int pairs, int chunk, int chunks) {
     if ((size_t)2 * pairs * chunks > I.part_cap) {
         fprintf(stderr, "ntc_hip backend: population evaluation needs %d partial sums, buffer holds %zu\n", 2 * pairs * chunks,
                 I.part_cap);
         exit(1);
     }
-    if (!pop_on_matrix_cores(I)) {
-        launch_pop_eval_valu(I, pairs, M, chunk, chunks);
-        return;
-    }
     if (chunk % 16 != 0) {
         fprintf(stderr, "ntc_hip backend: matrix-core population evaluation needs 16-slot chunks (got %d)\n", chunk);
         exit(1);
     }
+}
+
+template <bool Es>
+static void launch_pop_matrix(Impl& I, const PopSource& src, int pairs, int M, int chunk, int chunks) {
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         if constexpr (MfmaShape<S>::kOk) {
-            if (I.dm.leak >= 0.0f && I.dm.leak <= 1.0f) launch_pop_mfma<S, true>(I, pairs, M, chunk, chunks);
-            else launch_pop_mfma<S, false>(I, pairs, M, chunk, chunks);
+            if (I.dm.leak >= 0.0f && I.dm.leak <= 1.0f) launch_pop_mfma<S, true, Es>(I, src, pairs, M, chunk, chunks);
+            else launch_pop_mfma<S, false, Es>(I, src, pairs, M, chunk, chunks);
         }
     });
     NTC_CHECK(hipGetLastError());
+}
+
+void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks) {
+    ProfScope ps(I, "pop_eval");
+    if (!pop_on_matrix_cores(I)) {
+        if ((size_t)2 * pairs * chunks > I.part_cap) {
+            fprintf(stderr, "ntc_hip backend: population evaluation needs %d partial sums, buffer holds %zu\n", 2 * pairs * chunks,
+                    I.part_cap);
+            exit(1);
+        }
+        launch_pop_eval_valu(I, pairs, M, chunk, chunks);
+        return;
+    }
+    check_pop_launch(I, pairs, chunk, chunks);
+    PopSource src{};
+    src.wsets = I.wsets;
+    launch_pop_matrix<false>(I, src, pairs, M, chunk, chunks);
+}
+
+void launch_pop_eval_es(Impl& I, int it, float sigma, int N, int M, int chunk, int chunks) {
+    ProfScope ps(I, "pop_eval");
+    check_pop_launch(I, N, chunk, chunks);
+    PopSource src{};
+    src.nt = I.noise; src.seed = I.d.seed; src.step = (uint32_t)it; src.sigma = sigma;
+    src.w0 = I.w; src.eps = I.eps_mlp;
+    launch_pop_matrix<true>(I, src, N, M, chunk, chunks);
 }
 
 bool lat_pair_on_matrix_cores(const Impl& I) { return pop_on_matrix_cores(I); }

@@ -32,6 +32,7 @@ struct MfmaShape<S, true> {
     static constexpr int kHt = kH / 16;          // 16-unit tiles of a hidden layer
     static constexpr int kKsH = kH / 4;          // k-steps of a layer fed by a hidden layer
     static constexpr int kDeep = kNL > 1 ? kNL - 1 : 1;
+    static constexpr int kP = kH * kIn + kH + (kNL - 1) * (kH * kH + kH) + kNout * kH + kNout;   // parameters
 };
 
 // The hidden-layer input that lane group g feeds at k-step ks (see mfma_load).
@@ -56,8 +57,8 @@ struct MfmaWeights {
 // to match). Otherwise k-step 4 t + r takes inputs 16 t + 4 q + r (q = 0..3), the order in which a
 // 16-unit tile's D registers hold them, and the activations feed the next layer untransposed: the
 // same products, summed in another order.
-template <class S, bool Exact = true>
-__device__ __forceinline__ void mfma_load(MfmaWeights<S>& W, const float* __restrict__ w, int lane) {
+template <class S, bool Exact, class Get>
+__device__ __forceinline__ void mfma_load_from(MfmaWeights<S>& W, const Get& w, int lane) {
     using Q = MfmaShape<S>;
     constexpr int NIN = Q::kIn, H = Q::kH, NO = Q::kNout;
     const int i16 = lane & 15, g = lane >> 4;
@@ -66,27 +67,42 @@ __device__ __forceinline__ void mfma_load(MfmaWeights<S>& W, const float* __rest
 #pragma unroll
         for (int ks = 0; ks < Q::kKs1; ks++) {
             const int in = 4 * ks + g;
-            W.a1[ot][ks] = in < NIN ? w[(16 * ot + i16) * NIN + in] : 0.0f;
+            W.a1[ot][ks] = in < NIN ? w((16 * ot + i16) * NIN + in) : 0.0f;
         }
 #pragma unroll
-        for (int r = 0; r < 4; r++) W.c1[ot][r] = w[H * NIN + 16 * ot + 4 * g + r];
+        for (int r = 0; r < 4; r++) W.c1[ot][r] = w(H * NIN + 16 * ot + 4 * g + r);
     }
-    const float* p = w + H * NIN + H;
+    int p = H * NIN + H;
 #pragma unroll
     for (int l = 0; l < Q::kNL - 1; l++) {
 #pragma unroll
         for (int ot = 0; ot < Q::kHt; ot++) {
 #pragma unroll
-            for (int ks = 0; ks < Q::kKsH; ks++) W.ah[l][ot][ks] = p[(16 * ot + i16) * H + hidden_input<Exact>(ks, g)];
+            for (int ks = 0; ks < Q::kKsH; ks++) W.ah[l][ot][ks] = w(p + (16 * ot + i16) * H + hidden_input<Exact>(ks, g));
 #pragma unroll
-            for (int r = 0; r < 4; r++) W.ch[l][ot][r] = p[H * H + 16 * ot + 4 * g + r];
+            for (int r = 0; r < 4; r++) W.ch[l][ot][r] = w(p + H * H + 16 * ot + 4 * g + r);
         }
         p += H * H + H;
     }
 #pragma unroll
-    for (int ks = 0; ks < Q::kKsH; ks++) W.ao[ks] = i16 < NO ? p[i16 * H + hidden_input<Exact>(ks, g)] : 0.0f;
+    for (int ks = 0; ks < Q::kKsH; ks++) W.ao[ks] = i16 < NO ? w(p + i16 * H + hidden_input<Exact>(ks, g)) : 0.0f;
 #pragma unroll
-    for (int r = 0; r < 4; r++) W.co[r] = 4 * g + r < NO ? p[NO * H + 4 * g + r] : 0.0f;
+    for (int r = 0; r < 4; r++) W.co[r] = 4 * g + r < NO ? w(p + NO * H + 4 * g + r) : 0.0f;
+}
+
+// parameter k of a member: a flat vector, or w0 + sg eps as one fused operation (main.cpp:1856)
+struct ParamsAt {
+    const float* w;
+    __device__ __forceinline__ float operator()(int k) const { return w[k]; }
+};
+struct PerturbedParams {
+    const float* w0; const float* eps; float sg;
+    __device__ __forceinline__ float operator()(int k) const { return __builtin_fmaf(sg, eps[k], w0[k]); }
+};
+
+template <class S, bool Exact = true>
+__device__ __forceinline__ void mfma_load(MfmaWeights<S>& W, const float* __restrict__ w, int lane) {
+    mfma_load_from<S, Exact>(W, ParamsAt{ w }, lane);
 }
 
 __device__ __forceinline__ f4v mfma4(float a, float b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }

@@ -275,7 +275,7 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
     dev_alloc(&I.eps_mlp, (size_t)I.pairs_cap * I.P);
     I.gpart_cap = (size_t)((I.pairs_cap + 127) / 128) * I.P;
     dev_alloc(&I.gpart, I.gpart_cap);
-    ensure_wsets(I, (size_t)2 * I.pairs_cap * I.P);
+    if (!pop_on_matrix_cores(I)) ensure_wsets(I, (size_t)2 * I.pairs_cap * I.P);   // the matrix-core ES step needs none
     ensure_part(I, (size_t)2 * (std::max(I.pairs_cap, I.P + 1) * 4 + 2048));
     dev_alloc(&I.dl, (size_t)std::max(I.pairs_cap, I.P)); dev_alloc(&I.lsum, (size_t)I.pairs_cap); dev_alloc(&I.hh, (size_t)I.P);
     if (d.qat > 0) {
@@ -392,10 +392,15 @@ void Trainer::mlp_step(int it, float sigma, float lr, int N, int M) {
         exit(1);
     }
     launch_batch(I, it, M);
-    launch_perturb(I, it, sigma, N);
     const int chunk = pop_chunk(I, N, M), chunks = (M + chunk - 1) / chunk;
     ensure_part(I, (size_t)2 * N * chunks);
-    launch_pop_eval(I, N, M, chunk, chunks);
+    if (pop_on_matrix_cores(I)) {
+        launch_pop_eval_es(I, it, sigma, N, M, chunk, chunks);   // draws the perturbation itself
+    } else {
+        ensure_wsets(I, (size_t)2 * N * I.P);
+        launch_perturb(I, it, sigma, N);
+        launch_pop_eval(I, N, M, chunk, chunks);
+    }
     launch_es_finish(I, chunks, N, 3.0 * (double)I.d.wsum * (double)M);
     launch_es_grad(I, it, sigma, N);
     launch_adam(I, I.w, I.wgrad, I.wm, I.wv, I.P, lr, ++I.mlp_t);

@@ -140,6 +140,8 @@ bool qat_on_matrix_cores(const Impl& I);
 // minibatch slots per population-evaluation block for a population of `pairs` pairs
 int pop_chunk(const Impl& I, int pairs, int M);
 void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks);
+// the ES step's population evaluation with the perturbation drawn in the kernel (matrix-core shapes); fills eps_mlp
+void launch_pop_eval_es(Impl& I, int it, float sigma, int N, int M, int chunk, int chunks);
 void launch_pop_eval_valu(Impl& I, int pairs, int M, int chunk, int chunks);
 void launch_es_finish(Impl& I, int chunks, int N, double norm);
 void launch_es_grad(Impl& I, int it, float sigma, int N);
