@@ -311,6 +311,13 @@ __device__ __forceinline__ float pixel_err_f(const DevModel& m, const float (&o)
     return e;
 }
 
+// qat_index (main.cpp:2060-2064): lround of the grid coordinate, clamped
+__device__ __forceinline__ int qat_index(float v, int bits) {
+    const int levels = (1 << bits) - 1;
+    const int k = (int)roundf((v + 1.0f) * 0.5f * (float)levels);
+    return clampi(k, 0, levels);
+}
+
 // ---------------------------------------------------------------- reductions (wave64)
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll

@@ -5,7 +5,6 @@
 // Reference semantics (main.cpp): LatentTrainer::step_impl 1974-2044 (perturb texels, decode_err
 // twice, raster-order scatter into the distinct taps, grad += w * eps), dct_rate_pass 1935-1952,
 // qat_search 2088-2139.
-#include "mfma_mlp.hpp"
 #include "shapes.hpp"
 #include "trainer_impl.hpp"
 
@@ -87,12 +86,6 @@ __global__ void __launch_bounds__(kTPB) k_lat_gather(DevModel m, int level, int 
     }
 }
 
-// qat_index (main.cpp:2060-2064): lround of the grid coordinate, clamped
-__device__ __forceinline__ int qat_index(float v, int bits) {
-    const int levels = (1 << bits) - 1;
-    const int k = (int)roundf((v + 1.0f) * 0.5f * (float)levels);
-    return clampi(k, 0, levels);
-}
 
 // Exact per-texel search on the discrete nearest level 0 (qat_search): one thread per texel;
 // channels in order, the current grid value first, then every other value with strict <; the
@@ -149,84 +142,6 @@ void launch_lat_eps(Impl& I, int K, unsigned mask) {
     NTC_CHECK(hipGetLastError());
 }
 
-// The selector search on the matrix cores, for a nearest level 0 of the image's size (each texel's
-// cell is its own pixel): wave = 64 pixels in four 16-pixel tiles. Every lane builds its pixel's
-// features (features<S>); per channel, every candidate value is one MLP evaluation of the tile with
-// that feature replaced, the pixel's loss the reference's double sum over its channels in
-// ascending order (loss_subset's terms), broadcast to the pixel's four lanes. The choice is the
-// reference's: the current grid value first, then every other value with strict <, so the first
-// strictly smaller loss wins (main.cpp:2101-2132). The winner enters the features of the next channel
-// and is written to the decode buffer.
-template <class S>
-__global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __restrict__ w, float* __restrict__ zdec,
-                                                 const float* __restrict__ tgt, const int* __restrict__ qat_bits,
-                                                 const float* __restrict__ grid) {
-    using Q = MfmaShape<S>;
-    constexpr int NIN = Q::kIn, NO = Q::kNout, C0 = S::kC0, GL = (NO - 1) / 4;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
-    MfmaWeights<S> W;
-    mfma_load<S>(W, w, lane);
-    float cw[4];
-    lane_cw<NO>(m.cw, g, cw);
-    const int from_last = (GL * 16 + i16) << 2;   // the lane of this pixel that holds its loss
-    const bool unit_leak = m.leak >= 0.0f && m.leak <= 1.0f;
-    for (int u = 0; u < 4; u++) {
-        const int p = blockIdx.x * 256 + wave * 64 + u * 16 + i16;
-        const int pr = min(p, m.npix - 1);
-        float f[S::kMaxIn];
-        features<S>(m, PlainLatent{ zdec }, pr % m.W, pr / m.W, f);
-        float t[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) t[r] = tgt[(size_t)pr * NO + min(4 * g + r, NO - 1)];
-#pragma unroll
-        for (int c = 0; c < C0; c++) {
-            const int bits = qat_bits[c], levels = (1 << bits) - 1;
-            const float* gv = grid + bits * 257;
-            const int cur = qat_index(f[c], bits);
-            float b1[1][Q::kKs1];
-#pragma unroll
-            for (int ks = 0; ks < Q::kKs1; ks++) {
-                float v = 0.0f;
-#pragma unroll
-                for (int q = 0; q < 4; q++) if (4 * ks + q < NIN && g == q) v = f[4 * ks + q];
-                b1[0][ks] = v;
-            }
-            double cur_l = 0.0, best_l = 0.0;
-            int best_k = -1;
-            for (int kc = 0; kc <= levels; kc++) {
-                const float val = gv[kc];
-                if (g == c % 4) b1[0][c / 4] = val;
-                f4v o[1];
-                if (unit_leak) mfma_forward<S, 1, true>(W, b1, m.leak, o);
-                else mfma_forward<S, 1, false>(W, b1, m.leak, o);
-                float dd[4];
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float d = output_of(o[0][r], m.clamp_out) - t[r];
-                    dd[r] = __fmul_rn(d, d);
-                }
-                double l = chain_err_d<NO>(dd, cw, lane);
-                const long long b = __double_as_longlong(l);   // broadcast the pixel's loss to its four lanes
-                const int lo = __builtin_amdgcn_ds_bpermute(from_last, (int)(b & 0xFFFFFFFFll));
-                const int hi = __builtin_amdgcn_ds_bpermute(from_last, (int)(b >> 32));
-                l = __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
-                if (kc == cur) cur_l = l;
-                else if (best_k < 0 || l < best_l) { best_l = l; best_k = kc; }
-            }
-            const int win = (best_k >= 0 && best_l < cur_l) ? best_k : cur;
-            f[c] = gv[win];
-            if (g == 0 && p < m.npix) zdec[m.lv[0].off + (size_t)p * m.lv[0].C + c] = f[c];
-        }
-    }
-}
-
-bool qat_on_matrix_cores(const Impl& I) {
-    if (!I.lv0_unit_cells) return false;
-    bool ok = false;
-    dispatch_shape(I.dm, [&](auto s) { ok = MfmaShape<decltype(s)>::kOk; });
-    return ok;
-}
-
 void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask) {
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
@@ -247,16 +162,12 @@ void launch_lat_gather(Impl& I, int level, int K, float scale, bool rate) {
 void launch_qat_search(Impl& I) {
     const size_t ntx = (size_t)I.d.lv[0].W * I.d.lv[0].H;
     ProfScope ps(I, "qat_search");
-    const bool mfma = qat_on_matrix_cores(I);
+    if (qat_on_matrix_cores(I)) {
+        launch_qat_mfma(I);
+        return;
+    }
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
-        if constexpr (MfmaShape<S>::kOk) {
-            if (mfma) {
-                hipLaunchKernelGGL(k_qat_mfma<S>, dim3(blocks_for(I.npix, 256)), dim3(256), 0, I.stream, I.dm, I.w, I.zdec, I.tgt,
-                                   I.qat_bits, I.qat_grid);
-                return;
-            }
-        }
         hipLaunchKernelGGL(k_qat_search<S>, dim3(blocks_for(ntx, kTPB)), dim3(kTPB), 0, I.stream, I.dm, I.w, I.zdec, I.tgt, I.ranges,
                            I.qat_bits, I.qat_grid);
     });

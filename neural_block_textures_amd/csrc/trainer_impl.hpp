@@ -137,6 +137,7 @@ void launch_fd_sets(Impl& I, float h);
 bool pop_on_matrix_cores(const Impl& I);
 bool lat_pair_on_matrix_cores(const Impl& I);
 bool qat_on_matrix_cores(const Impl& I);
+void launch_qat_mfma(Impl& I);
 // minibatch slots per population-evaluation block for a population of `pairs` pairs
 int pop_chunk(const Impl& I, int pairs, int M);
 void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks);
