@@ -9,7 +9,8 @@
 // v_max_f32 (this file is compiled with relaxed NaN handling and the IEEE mode bit off, so the
 // maximum needs no canonicalising copies); a hidden layer's outputs feed the next layer in the order
 // the matrix instruction leaves them (no transpose; each unit's sum takes its inputs in another
-// order than the reference's ascending one); the sigmoid is the hardware exp2 and reciprocal; tile
+// order than the reference's ascending one); the sigmoid is the hardware exp2 and reciprocal, its
+// -log2(e) folded into the output layer; a lane's four channel terms are added in float per tile; tile
 // inputs are loaded with a wave-uniform SGPR base and loop-invariant 32-bit lane offsets. Member
 // losses stay within 1e-5 relative of the reference's (they are not bit-identical here anyway:
 // the sigmoid differs in the last bits).
@@ -24,7 +25,10 @@
 
 namespace ntc_hip {
 
-constexpr int kPopWaves = 4, kPopU = 2;
+constexpr int kPopWaves = 4;
+// 16-slot tiles a wave evaluates at once: two, one for the 64-wide hidden layers (registers)
+template <class S>
+constexpr int pop_u() { return MfmaShape<S>::kH > 32 ? 1 : 2; }
 
 // global-memory views: an SGPR base plus a 32-bit lane offset becomes one global_load
 typedef __attribute__((address_space(1))) const char GChar;
@@ -32,8 +36,8 @@ typedef __attribute__((address_space(1))) const float GFloat;
 
 template <class S>
 struct PopTileIn {
-    float b1[kPopU][MfmaShape<S>::kKs1];
-    float t[kPopU][4];
+    float b1[pop_u<S>()][MfmaShape<S>::kKs1];
+    float t[pop_u<S>()][4];
 };
 
 // Inputs of tiles (j, j + 1) of this wave: base = slot of tile j for lane 0 (uniform).
@@ -44,7 +48,7 @@ __device__ __forceinline__ void pop_load(PopTileIn<S>& in, const float* base_f, 
     const GChar* bf = (const GChar*)uniform_ptr(base_f);
     const GChar* bt = (const GChar*)uniform_ptr(base_t);
 #pragma unroll
-    for (int u = 0; u < kPopU; u++) {
+    for (int u = 0; u < pop_u<S>(); u++) {
 #pragma unroll
         for (int ks = 0; ks < Q::kKs1; ks++) in.b1[u][ks] = *(const GFloat*)(bf + fo[ks] + 128 * u);
 #pragma unroll
@@ -52,28 +56,40 @@ __device__ __forceinline__ void pop_load(PopTileIn<S>& in, const float* base_f, 
     }
 }
 
-// 1 / (1 + e^-s) from the hardware exp2 and reciprocal (each within about 1 ulp)
-__device__ __forceinline__ float sigmoid_hw(float s) {
-    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(s * -1.44269504088896341f));
+// 1 / (1 + e^-s) from the hardware exp2 and reciprocal (each within about 1 ulp), given
+// s2 = -log2(e) s: the kernels scale the output layer by kNegLog2e (scale_output), so the matrix
+// instruction delivers s2 directly
+constexpr float kNegLog2e = -1.44269504088896341f;
+__device__ __forceinline__ float sigmoid_hw2(float s2) { return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(s2)); }
+
+// the output of a pre-activation: clamp(s + 0.5) with --clamp, else the sigmoid of a pre-activation
+// delivered as -log2(e) s (the output layer is scaled when !clamp)
+template <class S>
+__device__ __forceinline__ float out_of(float s, bool clamp) {
+    return clamp ? __builtin_amdgcn_fmed3f(s + 0.5f, 0.0f, 1.0f) : sigmoid_hw2(s);
 }
 
 // Where a member's parameters come from: the weight sets of a central-difference step (wsets), or -
-// in an ES step - the block's own draw of the pair's Gaussians (NS_MLP, step, pair, k), written once
-// to LDS (and, by the chunk-0 block, to eps for the update), each weight w0 +- sigma eps as one fused
-// operation (main.cpp:1852-1856).
+// in an ES step - the block's own draw of the pair's Gaussians (NS_MLP, step, pair, k): both members'
+// weights w0 +- sigma eps (one fused operation each, main.cpp:1852-1856) go to LDS, and the chunk-0
+// block writes the Gaussians to eps for the update.
 struct PopSource {
     const float* wsets;                    // central differences: 2 pairs x P
     NoiseFix nt; uint64_t seed; uint32_t step; float sigma;
     const float* w0; float* eps;           // ES: the current weights and the step's Gaussians [pair][P]
 };
 
+// waves per SIMD the register allocation aims at (more would spill)
+template <class S>
+constexpr int pop_occupancy() { return MfmaShape<S>::kH > 32 ? 2 : (MfmaShape<S>::kIn <= 8 ? 4 : 3); }
+
 template <class S, bool LeakUnit, bool Clamp, bool Es>
-__global__ void __launch_bounds__(64 * kPopWaves) k_pop_mfma(DevModel m, PopSource src, int M, int Mcap,
+__global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_per_eu(pop_occupancy<S>()))) k_pop_mfma(DevModel m, PopSource src, int M, int Mcap,
                                                            int chunk, int chunks, const float* __restrict__ feat,
                                                            const float* __restrict__ btgt, double* __restrict__ part) {
     using Q = MfmaShape<S>;
     __shared__ double red[kPopWaves];
-    __shared__ float eps_s[Es ? Q::kP : 1];
+    __shared__ float wpm_s[Es ? 2 * Q::kP : 1];   // ES: the + member's weights, then the - member's
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int pair = blockIdx.x, ch = blockIdx.y, sgn = wave & 1, half = wave >> 1;
@@ -83,15 +99,17 @@ __global__ void __launch_bounds__(64 * kPopWaves) k_pop_mfma(DevModel m, PopSour
         const uint64_t head = noise_head(src.seed, NS_MLP, src.step, (uint32_t)pair);
         float* eg = src.eps + (size_t)pair * Q::kP;
         for (int k = threadIdx.x; k < Q::kP; k += 64 * kPopWaves) {
-            const float e = gauss_at(src.nt, head, (uint64_t)k);
-            eps_s[k] = e;
+            const float e = gauss_at(src.nt, head, (uint64_t)k), w0 = src.w0[k];
+            wpm_s[k] = __builtin_fmaf(src.sigma, e, w0);
+            wpm_s[Q::kP + k] = __builtin_fmaf(-src.sigma, e, w0);
             if (ch == 0) eg[k] = e;
         }
         __syncthreads();
-        mfma_load_from<S, false>(W, PerturbedParams{ src.w0, eps_s, sgn ? -src.sigma : src.sigma }, lane);
+        mfma_load<S, false>(W, wpm_s + sgn * Q::kP, lane);
     } else {
         mfma_load<S, false>(W, src.wsets + (size_t)(2 * pair + sgn) * Q::kP, lane);
     }
+    if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     float cw[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -112,37 +130,32 @@ __global__ void __launch_bounds__(64 * kPopWaves) k_pop_mfma(DevModel m, PopSour
     double e = 0.0;
     PopTileIn<S> cur;
     pop_load<S>(cur, feat + s0 + 16 * half, btgt + s0 + 16 * half, fo, to);
-    for (int j = 0; j < mine; j += kPopU) {
+    constexpr int U = pop_u<S>();
+    for (int j = 0; j < mine; j += U) {
         PopTileIn<S> nxt;
-        if (j + kPopU < mine) {
-            const int sn = s0 + 16 * (2 * (j + kPopU) + half);
+        if (j + U < mine) {
+            const int sn = s0 + 16 * (2 * (j + U) + half);
             pop_load<S>(nxt, feat + sn, btgt + sn, fo, to);
         }
         if constexpr (Q::kIn % 4 != 0) {   // inputs past nin are zero
 #pragma unroll
-            for (int u = 0; u < kPopU; u++)
+            for (int u = 0; u < U; u++)
                 if (4 * (Q::kKs1 - 1) + g >= Q::kIn) cur.b1[u][Q::kKs1 - 1] = 0.0f;
         }
-        f4v o[kPopU];
-        mfma_forward<S, kPopU, LeakUnit, false>(W, cur.b1, m.leak, o);
+        f4v o[U];
+        mfma_forward<S, U, LeakUnit, false>(W, cur.b1, m.leak, o);
 #pragma unroll
-        for (int u = 0; u < kPopU; u++) {
+        for (int u = 0; u < U; u++) {
             const int st = s0 + 16 * (2 * (j + u) + half);   // first slot of the tile (uniform)
-            float term[4];
+            float tsum = 0.0f;   // this lane's four channel terms cw (d d), added in float, then into the double
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float y = Clamp ? __builtin_amdgcn_fmed3f(o[u][r] + 0.5f, 0.0f, 1.0f) : sigmoid_hw(o[u][r]);
-                const float d = y - cur.t[u][r];
-                term[r] = __fmul_rn(cw[r], __fmul_rn(d, d));
+                const float d = out_of<S>(o[u][r], Clamp) - cur.t[u][r];
+                tsum += __fmul_rn(cw[r], __fmul_rn(d, d));
             }
             if (j + u < mine) {
-                if (st + 16 <= s1) {
-#pragma unroll
-                    for (int r = 0; r < 4; r++) e += (double)term[r];
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; r++) e += st + i16 < s1 ? (double)term[r] : 0.0;
-                }
+                if (st + 16 <= s1) e += (double)tsum;
+                else e += st + i16 < s1 ? (double)tsum : 0.0;
             }
         }
         cur = nxt;
@@ -166,10 +179,6 @@ __global__ void __launch_bounds__(64 * kPopWaves) k_pop_mfma(DevModel m, PopSour
 template <class S>
 constexpr int lat_pix() { return MfmaShape<S>::kIn <= 8 ? 512 : 256; }
 
-template <class S>
-__device__ __forceinline__ float out_of(float s, bool clamp) {
-    return clamp ? __builtin_amdgcn_fmed3f(s + 0.5f, 0.0f, 1.0f) : sigmoid_hw(s);
-}
 
 template <class S, bool LeakUnit, bool Clamp>
 __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* __restrict__ w, const float* __restrict__ zdec,
@@ -194,6 +203,7 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
     MfmaWeights<S> W;
     mfma_load<S, false>(W, w, lane);
+    if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     float cw[4];
     lane_cw<NO>(m.cw, g, cw);
     float* out = dpix + (size_t)k * m.npix;
@@ -246,6 +256,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
     MfmaWeights<S> W;
     mfma_load<S, false>(W, w, lane);
+    if (!m.clamp_out) scale_output<S>(W, kNegLog2e);
     float cw[4];
     lane_cw<NO>(m.cw, g, cw);
     const int from_last = (GL * 16 + i16) << 2;   // the lane of this pixel that holds its loss

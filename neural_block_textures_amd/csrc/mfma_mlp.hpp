@@ -105,6 +105,16 @@ __device__ __forceinline__ void mfma_load(MfmaWeights<S>& W, const float* __rest
     mfma_load_from<S, Exact>(W, ParamsAt{ w }, lane);
 }
 
+// Output weights and biases times sc (the evaluations with the hardware sigmoid fold its -log2(e)
+// into the output layer: the pre-activations come out as the exp2 argument).
+template <class S>
+__device__ __forceinline__ void scale_output(MfmaWeights<S>& W, float sc) {
+#pragma unroll
+    for (int ks = 0; ks < MfmaShape<S>::kKsH; ks++) W.ao[ks] *= sc;
+#pragma unroll
+    for (int r = 0; r < 4; r++) W.co[r] *= sc;
+}
+
 __device__ __forceinline__ f4v mfma4(float a, float b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
 // element (lane group g, register r) -> (lane group r, register g)
