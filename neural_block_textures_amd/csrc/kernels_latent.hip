@@ -53,39 +53,55 @@ __global__ void __launch_bounds__(kTPB) k_lat_pair(DevModel m, const float* __re
     dpix[(size_t)k * m.npix + p] = (ep - em) * m.inv_px;
 }
 
-// Footprint gather for one level (the gather form of the reference's raster-order scatter): one
-// thread per texel sums dpix over the pixel rectangle whose taps read the texel, in raster order,
-// then adds w * eps per channel, pair after pair. The rectangle comes from the host's range table
-// (built with the same tap arithmetic). With the --dct-lambda rate term, level 0 also receives
-// (rate_scale * dbits) * scale * eps right after each pair's mse term.
-__global__ void __launch_bounds__(kTPB) k_lat_gather(DevModel m, int level, int K, float scale, const float* __restrict__ dpix,
-                                                    const float* __restrict__ eps, const int* __restrict__ ranges,
-                                                    int rate, float rate_scale, int dct_bw, int dct_n,
-                                                    const int32_t* __restrict__ dbits, float* __restrict__ grad) {
+// Footprint gather for one level (the gather form of the reference's raster-order scatter,
+// main.cpp:2011-2037): the loss difference a texel's taps collect from pair k is the sum of dpix[k]
+// over the pixel rectangle that reads the texel, in raster order (the rectangle comes from the host's
+// range table, built with the same tap arithmetic); then grad += (d * scale) * eps per channel, pair
+// after pair. With the --dct-lambda rate term, level 0 also receives (rate_scale * dbits) * scale * eps
+// right after each pair's mse term. Block = 16 texels x 4 pairs: the 64 threads sum the footprints
+// of four pairs at once (each sum in raster order), then 16 threads apply the four pairs in order.
+constexpr int kGatherTex = 16, kGatherPairs = 4;
+__global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevModel m, int level, int K, float scale,
+                                                                         const float* __restrict__ dpix,
+                                                                         const float* __restrict__ eps, const int* __restrict__ ranges,
+                                                                         int rate, float rate_scale, int dct_bw, int dct_n,
+                                                                         const int32_t* __restrict__ dbits, float* __restrict__ grad) {
+    __shared__ float dsum[kGatherPairs][kGatherTex];
     const DevLevel& L = m.lv[level];
-    const int t = blockIdx.x * kTPB + threadIdx.x;
-    if (t >= L.W * L.H) return;
-    const int tx = t % L.W, ty = t / L.W;
+    const int j = threadIdx.x % kGatherTex, q = threadIdx.x / kGatherTex;
+    const int t = blockIdx.x * kGatherTex + j;
+    const bool live = t < L.W * L.H;
+    const int tt = live ? t : 0;
+    const int tx = tt % L.W, ty = tt / L.W;
     const int* R = ranges + L.rng;
     const int x0 = R[tx], x1 = R[L.W + tx], y0 = R[2 * L.W + ty], y1 = R[2 * L.W + L.H + ty];
-    const long long base = L.off + (long long)t * L.C;
+    const long long base = L.off + (long long)tt * L.C;
     const int blk = (ty / 8) * dct_bw + tx / 8;
-    for (int k = 0; k < K; k++) {
-        const float* dp = dpix + (size_t)k * m.npix;
-        float d = 0.0f;
-        for (int py = y0; py < y1; py++)
-            for (int px = x0; px < x1; px++) d += dp[(size_t)py * m.W + px];
-        const float wgt = d * scale;
-        const float* e = eps + (size_t)k * m.nz;
-        for (int c = 0; c < L.C; c++) grad[base + c] = __builtin_fmaf(wgt, e[base + c], grad[base + c]);
-        if (rate) {
-            const int32_t* db = dbits + (size_t)k * dct_n + (size_t)blk * L.C;
-            for (int c = 0; c < L.C; c++)
-                grad[base + c] = __builtin_fmaf(__fmul_rn(__fmul_rn(rate_scale, (float)db[c]), scale), e[base + c], grad[base + c]);
+    for (int k0 = 0; k0 < K; k0 += kGatherPairs) {
+        const int k = k0 + q;
+        if (live && k < K) {
+            const float* dp = dpix + (size_t)k * m.npix;
+            float d = 0.0f;
+            for (int py = y0; py < y1; py++)
+                for (int px = x0; px < x1; px++) d += dp[(size_t)py * m.W + px];
+            dsum[q][j] = d;
         }
+        __syncthreads();
+        if (live && q == 0) {
+            for (int kk = k0; kk < min(K, k0 + kGatherPairs); kk++) {
+                const float wgt = dsum[kk - k0][j] * scale;
+                const float* e = eps + (size_t)kk * m.nz;
+                for (int c = 0; c < L.C; c++) grad[base + c] = __builtin_fmaf(wgt, e[base + c], grad[base + c]);
+                if (rate) {
+                    const int32_t* db = dbits + (size_t)kk * dct_n + (size_t)blk * L.C;
+                    for (int c = 0; c < L.C; c++)
+                        grad[base + c] = __builtin_fmaf(__fmul_rn(__fmul_rn(rate_scale, (float)db[c]), scale), e[base + c], grad[base + c]);
+                }
+            }
+        }
+        __syncthreads();
     }
 }
-
 
 // Exact per-texel search on the discrete nearest level 0 (qat_search): one thread per texel;
 // channels in order, the current grid value first, then every other value with strict <; the
@@ -154,7 +170,8 @@ void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask) {
 void launch_lat_gather(Impl& I, int level, int K, float scale, bool rate) {
     const size_t ntx = (size_t)I.d.lv[level].W * I.d.lv[level].H;
     ProfScope ps(I, "lat_gather");
-    hipLaunchKernelGGL(k_lat_gather, dim3(blocks_for(ntx, kTPB)), dim3(kTPB), 0, I.stream, I.dm, level, K, scale, I.dpix, I.eps_lat,
+    hipLaunchKernelGGL(k_lat_gather, dim3(blocks_for(ntx, kGatherTex)), dim3(kGatherTex * kGatherPairs), 0, I.stream, I.dm, level, K,
+                       scale, I.dpix, I.eps_lat,
                        I.ranges, rate ? 1 : 0, I.ddct.rate_scale, I.ddct.BW, I.ddct.n, I.dct_dbits, I.zgrad);
     NTC_CHECK(hipGetLastError());
 }

@@ -131,8 +131,17 @@ __global__ void __launch_bounds__(kTPB) k_es_grad_part(int N, int P, float scale
     const int k = blockIdx.x * 64 + lane;
     const int i0 = (blockIdx.y * (kTPB / 64) + wave) * kChain, i1 = min(N, i0 + kChain);
     float g = 0.0f;
-    if (k < P)
-        for (int i = i0; i < i1; i++) g = __builtin_fmaf(__fmul_rn((float)dl[i], scale), eps[(size_t)i * P + k], g);
+    if (k < P) {
+        if (i1 - i0 == kChain) {   // a full chain: loads issued ahead of the dependent fma chain
+            float w[kChain], e[kChain];
+#pragma unroll
+            for (int q = 0; q < kChain; q++) { w[q] = __fmul_rn((float)dl[i0 + q], scale); e[q] = eps[(size_t)(i0 + q) * P + k]; }
+#pragma unroll
+            for (int q = 0; q < kChain; q++) g = __builtin_fmaf(w[q], e[q], g);
+        } else {
+            for (int i = i0; i < i1; i++) g = __builtin_fmaf(__fmul_rn((float)dl[i], scale), eps[(size_t)i * P + k], g);
+        }
+    }
     lds[wave][lane] = g;
     __syncthreads();
     if (wave == 0 && k < P) {
@@ -146,6 +155,7 @@ __global__ void __launch_bounds__(kTPB) k_es_grad_final(int P, int segs, const f
     const int k = blockIdx.x * kTPB + threadIdx.x;
     if (k >= P) return;
     float g = part[k];
+#pragma unroll 8
     for (int s = 1; s < segs; s++) g += part[(size_t)s * P + k];
     grad[k] = g;
 }
