@@ -171,7 +171,8 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
 
 // The latent pair evaluation (LatentTrainer::step_impl, main.cpp:1990-2007) on the matrix cores:
 // block (512 or 256 pixels, pair k). Phase 1: the threads build the features of each pixel with the
-// pair's texels perturbed by +sg eps and by -sg eps (features<S>, as the VALU kernel) into LDS.
+// pair's texels perturbed by +sg eps and by -sg eps (features_pm: both members from one set of
+// taps and texel loads) into LDS.
 // Phase 2: each wave evaluates a quarter of the pixels in 16-pixel tiles, the + and - members of
 // a tile together; each pixel's error is the reference's float fma chain over its channels in
 // ascending order (decode_err), and dpix = (e+ - e-) * inv_px.
@@ -191,13 +192,10 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     const float* e = eps + (size_t)k * m.nz;
     for (int q = threadIdx.x; q < kLatPix; q += 256) {
         const int p = min(p0 + q, m.npix - 1);
-        float f[S::kMaxIn];
-        features<S>(m, PerturbedLatent{ zdec, e, sg, mask }, p % m.W, p / m.W, f);
+        float fp[S::kMaxIn], fm[S::kMaxIn];
+        features_pm<S>(m, zdec, e, sg, mask, p % m.W, p / m.W, fp, fm);
 #pragma unroll
-        for (int i = 0; i < NIN; i++) F[0][i][q] = f[i];
-        features<S>(m, PerturbedLatent{ zdec, e, -sg, mask }, p % m.W, p / m.W, f);
-#pragma unroll
-        for (int i = 0; i < NIN; i++) F[1][i][q] = f[i];
+        for (int i = 0; i < NIN; i++) { F[0][i][q] = fp[i]; F[1][i][q] = fm[i]; }
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
