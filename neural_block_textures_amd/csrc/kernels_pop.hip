@@ -11,7 +11,7 @@
 // the matrix instruction leaves them (no transpose; each unit's sum takes its inputs in another
 // order than the reference's ascending one); the sigmoid is the hardware exp2 and reciprocal, its
 // -log2(e) folded into the output layer; a lane's four channel terms are added in float per tile; tile
-// inputs are loaded with a wave-uniform SGPR base and loop-invariant 32-bit lane offsets. Member
+// inputs are buffer loads with a loop-invariant lane offset and the tile's offset in an SGPR. Member
 // losses stay within 1e-5 relative of the reference's (they are not bit-identical here anyway:
 // the sigmoid differs in the last bits).
 //
@@ -30,9 +30,15 @@ constexpr int kPopWaves = 4;
 template <class S>
 constexpr int pop_u() { return MfmaShape<S>::kH > 32 ? 1 : 2; }
 
-// global-memory views: an SGPR base plus a 32-bit lane offset becomes one global_load
-typedef __attribute__((address_space(1))) const char GChar;
-typedef __attribute__((address_space(1))) const float GFloat;
+// A raw buffer over the minibatch arrays: loads take a loop-invariant 32-bit lane offset (VGPR) and
+// the tile's byte offset (SGPR), so no address arithmetic per load. num_records = the allocation
+// (every read stays inside it: the arrays carry 64 floats of slack past nin x Mcap / nout x Mcap).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const float* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float buffer_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
 
 template <class S>
 struct PopTileIn {
@@ -40,19 +46,19 @@ struct PopTileIn {
     float t[pop_u<S>()][4];
 };
 
-// Inputs of tiles (j, j + 1) of this wave: base = slot of tile j for lane 0 (uniform).
+// Inputs of tiles j .. j + U - 1 of this wave: soff = byte offset of tile j's first slot (uniform);
+// tile u sits 32 slots further per u.
 template <class S>
-__device__ __forceinline__ void pop_load(PopTileIn<S>& in, const float* base_f, const float* base_t, const uint32_t (&fo)[MfmaShape<S>::kKs1],
-                                         const uint32_t (&to)[4]) {
+__device__ __forceinline__ void pop_load(PopTileIn<S>& in, __amdgpu_buffer_rsrc_t rf, __amdgpu_buffer_rsrc_t rt, uint32_t soff,
+                                         const uint32_t (&fo)[MfmaShape<S>::kKs1], const uint32_t (&to)[4]) {
     using Q = MfmaShape<S>;
-    const GChar* bf = (const GChar*)uniform_ptr(base_f);
-    const GChar* bt = (const GChar*)uniform_ptr(base_t);
 #pragma unroll
     for (int u = 0; u < pop_u<S>(); u++) {
+        const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane((int)(soff + 128u * u));   // uniform: an SGPR
 #pragma unroll
-        for (int ks = 0; ks < Q::kKs1; ks++) in.b1[u][ks] = *(const GFloat*)(bf + fo[ks] + 128 * u);
+        for (int ks = 0; ks < Q::kKs1; ks++) in.b1[u][ks] = buffer_f32(rf, fo[ks], so);
 #pragma unroll
-        for (int r = 0; r < 4; r++) in.t[u][r] = *(const GFloat*)(bt + to[r] + 128 * u);
+        for (int r = 0; r < 4; r++) in.t[u][r] = buffer_f32(rt, to[r], so);
     }
 }
 
@@ -128,15 +134,14 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     const int tiles = (s1 - s0 + 15) >> 4;
     const int mine = (tiles - half + 1) >> 1;   // this wave's tiles: 2 j + half, j < mine
     double e = 0.0;
+    const __amdgpu_buffer_rsrc_t rf = buffer_of(feat, 4u * ((uint32_t)Q::kIn * (uint32_t)Mcap + 64u));
+    const __amdgpu_buffer_rsrc_t rt = buffer_of(btgt, 4u * ((uint32_t)Q::kNout * (uint32_t)Mcap + 64u));
     PopTileIn<S> cur;
-    pop_load<S>(cur, feat + s0 + 16 * half, btgt + s0 + 16 * half, fo, to);
+    pop_load<S>(cur, rf, rt, 4u * (uint32_t)(s0 + 16 * half), fo, to);
     constexpr int U = pop_u<S>();
     for (int j = 0; j < mine; j += U) {
         PopTileIn<S> nxt;
-        if (j + U < mine) {
-            const int sn = s0 + 16 * (2 * (j + U) + half);
-            pop_load<S>(nxt, feat + sn, btgt + sn, fo, to);
-        }
+        if (j + U < mine) pop_load<S>(nxt, rf, rt, 4u * (uint32_t)(s0 + 16 * (2 * (j + U) + half)), fo, to);
         if constexpr (Q::kIn % 4 != 0) {   // inputs past nin are zero
 #pragma unroll
             for (int u = 0; u < U; u++)
