@@ -35,7 +35,7 @@ FP32_PEAK_TFLOPS = 157.3
 METRIC = "member·pixel evals/sec + ES iterations/sec (512² 4-tex, pop 8192), % roofline"
 KERNELS = ("batch", "perturb", "pop_eval", "es_grad", "adam", "lat_eps", "lat_pair", "lat_gather", "qat_search", "decode",
            "fd_sets", "qes_snap", "dct_snap", "dct_rate")
-DCT_CODE = 8          # the benchmark's constant scale code (the reference fits them from probes every 500 iterations)
+DCT_CODE = 8          # the scale code set before the first device refit replaces it with the probe's
 DCT_LAMBDA = 0.5      # the reference's default --dct-lambda at q 50: min(0.5, 7.5 S(q)^2)
 DCT_LO16 = 4          # the default --dct-lambda-lo 0.25 as round(16 W)
 
@@ -68,15 +68,16 @@ def inputs(w):
     return z, p, tgt
 
 
-def dct_host_state(w):
-    """codes, symbols, steps, lambda weights of the workload's DCT-coded level 0 (host side)"""
+def dct_host_state(w, codes=None):
+    """codes (default: the constant DCT_CODE), symbols, steps, lambda weights of the workload's DCT-coded level 0"""
     import numpy as np
 
     from neural_block_textures_amd import dct_host
     W0, H0, C0, _ = w.layout.levels[0]
     n = (W0 // 8) * (H0 // 8) * C0
     t16, scale = dct_host.lambda_weights(DCT_LAMBDA, w.layout.W, w.layout.H, True, True)
-    return {"C": C0, "BW": W0 // 8, "BH": H0 // 8, "n": n, "code": np.full(n, DCT_CODE, np.uint8),
+    code = np.full(n, DCT_CODE, np.uint8) if codes is None else np.ascontiguousarray(codes, np.uint8).copy()
+    return {"C": C0, "BW": W0 // 8, "BH": H0 // 8, "n": n, "code": code,
             "sym": np.zeros(n * 64, np.int16), "steps": np.concatenate([dct_host.steps(q, 4).reshape(-1) for q in w.dct_q]),
             "lam_t16": t16, "rate_scale": scale}
 
@@ -102,6 +103,8 @@ def make_trainer(w, z, p, tgt):
             d.lam_t16[k] = h["lam_t16"][k]
         d.lo_w16, d.deadzone = DCT_LO16, 0
         tr.set_dct(d, h["code"], h["sym"], h["steps"])
+        tr.dct_codes = tr.dct_refit()   # the scale codes from the decoder sensitivity probe, as at the reference's DCT switch
+        tr.dct_desc = d
     return tr
 
 
@@ -112,7 +115,7 @@ def es_iter(tr, w, it):
         tr.qat_search()
 
 
-def cpu_baseline(w, z, p, tgt, seconds: float, pairs=None):
+def cpu_baseline(w, z, p, tgt, seconds: float, pairs=None, dct_codes=None):
     """The reference's CPU training loop (main.cpp compiled with its own -O3 -ffast-math flags and
     OpenMP, oracle/_ref/libntc_ref_fast.so) on the same inputs for a bounded number of iterations
     (with `pairs` < the workload's population for a sample of a very large one); the oracle's
@@ -134,7 +137,7 @@ def cpu_baseline(w, z, p, tgt, seconds: float, pairs=None):
     if O.have_reference(fast=True):
         L = O.reference(fast=True).lib
         if w.dct_q:
-            h = dct_host_state(w)
+            h = dct_host_state(w, dct_codes)
             d = O.OrDct()
             d.C, d.BW, d.BH, d.dc_step, d.deadzone, d.lo_w16 = h["C"], h["BW"], h["BH"], 4, 0, DCT_LO16
             for k in range(16):
@@ -178,6 +181,35 @@ def cpu_baseline(w, z, p, tgt, seconds: float, pairs=None):
                   f"down, everything else at full size), {el:.1f} s")
     return {"value": ev * its / el, "unit": "member·pixel evals/s", "cores": threads, "kind": kind, "sample": sample,
             "es_iters_per_s": its / el, "cpu": platform.processor() or platform.machine()}
+
+
+def cpu_refit_ms(w, r):
+    """The reference's host refit of the same state (main.cpp:4110-4120 with --cuda: the model downloaded,
+    dct_probe_codes and the level-0 snap on the host's cores; the set_dct upload not included)."""
+    import numpy as np
+
+    from oracle import oracle as O
+    if not O.have_reference(fast=True):
+        return None
+    L = O.reference(fast=True).lib
+    (z, p), zq = r["host_state"]
+    h = dct_host_state(w, r["dct_codes"])
+    d = O.OrDct()
+    d.C, d.BW, d.BH, d.dc_step, d.deadzone, d.lo_w16 = h["C"], h["BW"], h["BH"], 4, 0, DCT_LO16
+    for k in range(16):
+        d.lam_t16[k] = h["lam_t16"][k]
+    d.step = h["steps"].ctypes.data_as(C.POINTER(C.c_int))
+    d.code = h["code"].ctypes.data_as(C.POINTER(C.c_uint8))
+    d.sym = h["sym"].ctypes.data_as(C.POINTER(C.c_int16))
+    mc = O.model_of(w.layout)
+    W0, H0, C0, _ = w.layout.levels[0]
+    lv0 = O.OrLevel(W0, H0, C0, 1, 0)
+    n0 = W0 * H0 * C0
+    zs, zqo = z[:n0].copy(), np.zeros(n0, np.float32)
+    t0 = time.perf_counter()
+    L.ref_dct_probe_codes(C.byref(mc), p.ctypes.data, zq.ctypes.data, C.byref(d), h["code"].ctypes.data)
+    L.ref_dct_snap_level0(C.byref(d), C.byref(lv0), zs.ctypes.data, zqo.ctypes.data, None, None)
+    return 1e3 * (time.perf_counter() - t0)
 
 
 def run_gpu(w, steps, warmup, fd_steps=0, seconds=0.0):
@@ -229,12 +261,23 @@ def run_gpu(w, steps, warmup, fd_steps=0, seconds=0.0):
         fd_el = time.perf_counter() - t1
         fd = {"iters_per_s": fd_steps / fd_el, "ms_per_iter": 1e3 * fd_el / fd_steps,
               "evals_per_s": (2 * (w.layout.nparams + 1) * w.mlp_batch) * fd_steps / fd_el}
+    refit = None
+    if w.dct_q:   # the device refit (probe + re-snap) against the reference's host path for the same step
+        tr.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(5):
+            tr.dct_refit()
+        refit = {"device_ms": 1e3 * (time.perf_counter() - t1) / 5}
     loss, _ = tr.mlp_stats()
     img = tr.decode_full()
     assert np.isfinite(img).all() and np.isfinite(loss)
     name = "k_pop_mfma" if tr.on_matrix_cores("pop_eval") else "k_pop_eval"
+    out = {"z": z, "p": p, "tgt": tgt, "steps": steps, "el": el, "kernels": kernels, "fd": fd, "loss": loss, "pop_kernel": name,
+           "refit": refit, "dct_codes": getattr(tr, "dct_codes", None)}
+    if w.dct_q:
+        out["host_state"] = (tr.download_model(), tr.download_zq())
     tr.close()
-    return {"z": z, "p": p, "tgt": tgt, "steps": steps, "el": el, "kernels": kernels, "fd": fd, "loss": loss, "pop_kernel": name}
+    return out
 
 
 def roofline_of(w, r):
@@ -266,12 +309,14 @@ def all_configs(out_path: str, cpu_seconds: float):
         # a population too large for a bounded CPU sample (over about 4 TFLOP per iteration) is sampled with 64 pairs
         pairs = w.mlp_pairs if ev["total"] * 2 * macs(w.layout) < 4e12 else 64
         log(f"bench: {name}: GPU {gpu_its:.2f} it/s; CPU sample ...")
-        cpu = cpu_baseline(w, r["z"], r["p"], r["tgt"], cpu_seconds, pairs=pairs) if cpu_seconds > 0 else None
+        cpu = cpu_baseline(w, r["z"], r["p"], r["tgt"], cpu_seconds, pairs=pairs, dct_codes=r["dct_codes"]) if cpu_seconds > 0 else None
+        if r["refit"] is not None and cpu_seconds > 0:
+            r["refit"]["host_ms"] = cpu_refit_ms(w, r)
         cpu_its = cpu["value"] / ev["total"] if cpu else None   # full-size iterations per second at the sampled rate
         row = {"workload": name, "gpu_es_iters_per_s": gpu_its, "gpu_ms_per_iter": 1e3 / gpu_its, "gpu_steps": r["steps"],
                "gpu_evals_per_s": ev["total"] * gpu_its, "evals_per_iter": ev, "roofline": roofline_of(w, r),
                "kernels": r["kernels"], "cpu": cpu, "cpu_es_iters_per_s": cpu_its,
-               "speedup": gpu_its / cpu_its if cpu_its else None}
+               "speedup": gpu_its / cpu_its if cpu_its else None, "dct_refit": r["refit"]}
         print(json.dumps(row), flush=True)
         rows.append(row)
     with open(out_path, "w") as f:
@@ -286,6 +331,13 @@ def all_configs(out_path: str, cpu_seconds: float):
                     f"{row['evals_per_iter']['total']:,} | `{rf['kernel']}` {rf['ms_per_launch']:.4f} ms | {rf['achieved']:.1f} | "
                     f"{100 * rf['frac']:.1f}% | {row['cpu_es_iters_per_s'] or 0:.3g} | {c.get('cores', '-')} | "
                     f"{row['speedup'] or 0:.0f}x | {c.get('sample', '-')} |\n")
+        for row in rows:
+            rf = row.get("dct_refit")
+            if rf:
+                f.write(f"\n{row['workload']}: a --dct-q refit (decoder sensitivity probe + level-0 re-snap) takes "
+                        f"{rf['device_ms']:.3f} ms on the device (`ntc_trainer_dct_refit`); the reference's host probe and snap "
+                        f"of the same state take {rf.get('host_ms') or 0:.1f} ms on the host's cores (plus the model download "
+                        f"and the set_dct upload).\n")
     log(f"bench: wrote {out_path}")
 
 

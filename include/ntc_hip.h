@@ -92,6 +92,15 @@ void ntc_trainer_set_dct(ntc_trainer* t, const ntc_dct_desc* d, const uint8_t* c
 void ntc_trainer_download_dct(ntc_trainer* t, int16_t* sym, uint8_t* code);
 void ntc_trainer_download_dct_rate(ntc_trainer* t, int32_t* bits, int32_t* dbits_last_pair, int* ntrunc, int* nz_before,
                                    int* hits, int* evals);
+/* The decoder sensitivity probe of a --dct-q level 0 on the device. No counterpart in the reference's
+ * backend: it replaces the host's dct_probe_codes (main.cpp:1001-1032), which needs the model downloaded
+ * first. Codes (BW*BH*C, [block][channel]) and, if gain is not null, the block gains of the current decode
+ * buffer and weights. Requires --dct-q in the model description. */
+void ntc_trainer_dct_probe(ntc_trainer* t, uint8_t* code, float* gain);
+/* Decoder::dct_refit (main.cpp:1672-1680) on the device: probe, replace the codes, re-snap level 0 from the
+ * shadow; the new codes are returned if code is not null (download_dct gives the symbols). Replaces the
+ * reference's download + host refit + set_dct (main.cpp:4110-4120). Requires a prior set_dct. */
+void ntc_trainer_dct_refit(ntc_trainer* t, uint8_t* code);
 
 /* Trainer::mlp_step / mlp_step_fd / reset_mlp_adam / mlp_stats (cuda/ntc_cuda.h:110-115) */
 void ntc_trainer_mlp_step(ntc_trainer* t, int it, float sigma, float lr, int N, int M);

@@ -81,6 +81,9 @@ void ntc_trainer_download_dct_rate(ntc_trainer* t, int32_t* bits, int32_t* dbits
     t->t.download_dct_rate(bits, dbits_last_pair, ntrunc, nz_before, hits, evals);
 }
 
+void ntc_trainer_dct_probe(ntc_trainer* t, uint8_t* code, float* gain) { ntc_hip::dct_probe_impl(*t->t.im, code, gain); }
+void ntc_trainer_dct_refit(ntc_trainer* t, uint8_t* code) { ntc_hip::dct_refit_impl(*t->t.im, code); }
+
 void ntc_trainer_mlp_step(ntc_trainer* t, int it, float sigma, float lr, int N, int M) { t->t.mlp_step(it, sigma, lr, N, M); }
 void ntc_trainer_mlp_step_fd(ntc_trainer* t, int it, float h, float lr, int M) { t->t.mlp_step_fd(it, h, lr, M); }
 void ntc_trainer_reset_mlp_adam(ntc_trainer* t) { t->t.reset_mlp_adam(); }

@@ -87,6 +87,23 @@ void sync(Impl& I) { NTC_CHECK(hipStreamSynchronize(I.stream)); }
 }   // namespace
 
 namespace ntc_hip {
+// The decoder sensitivity probe on the device (the host's dct_probe_codes, main.cpp:1001-1032).
+void dct_probe_impl(Impl& I, uint8_t* code, float* gain) {
+    if (!I.dct) die("dct_probe without --dct-q in the model description");
+    launch_dct_probe(I, I.dct_probe_code, I.dct_gain);
+    if (code) NTC_CHECK(hipMemcpyAsync(code, I.dct_probe_code, (size_t)I.ddct.n, hipMemcpyDeviceToHost, I.stream));
+    if (gain) NTC_CHECK(hipMemcpyAsync(gain, I.dct_gain, (size_t)I.ddct.n * sizeof(float), hipMemcpyDeviceToHost, I.stream));
+    sync(I);
+}
+// Decoder::dct_refit (main.cpp:1672-1680) on the device: probe, replace the codes, re-snap (qes_refresh).
+void dct_refit_impl(Impl& I, uint8_t* code) {
+    if (!I.dct || !I.dct_live) die("dct_refit before set_dct");
+    launch_dct_probe(I, I.dct_code, nullptr);
+    snap_latent_impl(I);
+    if (code) NTC_CHECK(hipMemcpyAsync(code, I.dct_code, (size_t)I.ddct.n, hipMemcpyDeviceToHost, I.stream));
+    sync(I);
+}
+
 void resolve_times(Impl& I) {
     bool any = false;
     for (auto& kv : I.times) if (!kv.second.pending.empty()) any = true;
@@ -121,7 +138,7 @@ Trainer::~Trainer() {
         dev_free(I.wsets); dev_free(I.eps_mlp); dev_free(I.gpart); dev_free(I.part); dev_free(I.dl); dev_free(I.lsum); dev_free(I.hh);
         dev_free(I.eps_lat); dev_free(I.dpix); dev_free(I.ranges); dev_free(I.qat_grid); dev_free(I.qat_bits);
         dev_free(I.qes_dev); dev_free(I.qgrid);
-        dev_free(I.dct_sym); dev_free(I.dct_code); dev_free(I.dct_step); dev_free(I.dct_bits); dev_free(I.dct_dbits); dev_free(I.dct_cnt);
+        dev_free(I.dct_sym); dev_free(I.dct_code); dev_free(I.dct_step); dev_free(I.dct_bits); dev_free(I.dct_dbits); dev_free(I.dct_cnt); dev_free(I.dct_probe_code); dev_free(I.dct_gain);
         (void)hipStreamDestroy(I.stream);
     }
     delete im;
@@ -260,6 +277,7 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
         memcpy(D.zigzag, d.dct_zigzag, sizeof(D.zigzag));
         dev_alloc(&I.dct_sym, (size_t)D.n * 64); dev_alloc(&I.dct_code, (size_t)D.n); dev_alloc(&I.dct_step, (size_t)D.C * 16 * 64);
         dev_alloc(&I.dct_bits, (size_t)D.n); dev_alloc(&I.dct_cnt, 3);
+        dev_alloc(&I.dct_probe_code, (size_t)D.n); dev_alloc(&I.dct_gain, (size_t)D.n);
         NTC_CHECK(hipMemset(I.dct_sym, 0, (size_t)D.n * 64 * sizeof(int16_t)));
         NTC_CHECK(hipMemset(I.dct_code, 0, (size_t)D.n));
         NTC_CHECK(hipMemset(I.dct_step, 0, (size_t)D.C * 16 * 64 * sizeof(int)));

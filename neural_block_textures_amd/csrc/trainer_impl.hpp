@@ -92,6 +92,8 @@ struct ntc_cuda::Trainer::Impl {
     int* dct_step = nullptr;
     int32_t *dct_bits = nullptr, *dct_dbits = nullptr;   // dbits: Kcap x n (pair k's bit differences)
     int* dct_cnt = nullptr;    // ntrunc, nz_before (last snap), hits (last lat_step)
+    uint8_t* dct_probe_code = nullptr;   // the device probe's codes (n)
+    float* dct_gain = nullptr;           // and block gains (n)
     int dct_evals = 0, dct_last_K = 0;
 
     int mlp_t = 0, lat_t = 0, lat_step_no = 0;
@@ -166,6 +168,10 @@ void launch_qes_snap(Impl& I);
 void launch_dct_clamp0(Impl& I);
 void launch_dct_snap(Impl& I);
 void launch_dct_recon(Impl& I);
+// the decoder sensitivity probe over the decode buffer: codes (and block gains, when gain != null) into device buffers
+void launch_dct_probe(Impl& I, uint8_t* code, float* gain);
+void dct_probe_impl(Impl& I, uint8_t* code, float* gain);
+void dct_refit_impl(Impl& I, uint8_t* code);
 void launch_dct_rate_pairs(Impl& I, int K, float sigma);
 void launch_shadow_pull(Impl& I, size_t off, size_t n, float f);
 

@@ -102,6 +102,8 @@ def library() -> C.CDLL:
             "ntc_trainer_set_profiling": (None, [P, C.c_int]),
             "ntc_trainer_kernel_time": (C.c_int, [P, C.c_char_p, P, P]),
             "ntc_trainer_on_matrix_cores": (C.c_int, [P, C.c_char_p]),
+            "ntc_trainer_dct_probe": (None, [P, P, P]),
+            "ntc_trainer_dct_refit": (None, [P, P]),
             "ntc_trainer_debug_gauss": (None, [P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, C.c_size_t, P]),
             "ntc_trainer_debug_noise_factors": (None, [P, C.c_uint32, C.c_size_t, P, P]),
             "ntc_trainer_debug_copy_calibration": (None, [P, C.c_size_t, C.c_int]),
@@ -300,6 +302,19 @@ class Trainer:
         self._lib.ntc_trainer_download_dct_rate(self._h, bits.ctypes.data, dbits.ctypes.data,
                                                 *[C.addressof(x) for x in v])
         return bits, dbits, v[0].value, v[1].value, v[2].value, v[3].value
+
+    def dct_probe(self):
+        """the device's decoder sensitivity probe: (codes uint8 [block][channel], block gains float32)"""
+        code = np.empty(self.dct_n, np.uint8)
+        gain = np.empty(self.dct_n, np.float32)
+        self._lib.ntc_trainer_dct_probe(self._h, code.ctypes.data, gain.ctypes.data)
+        return code, gain
+
+    def dct_refit(self):
+        """probe on the device, replace the codes, re-snap level 0; returns the new codes"""
+        code = np.empty(self.dct_n, np.uint8)
+        self._lib.ntc_trainer_dct_refit(self._h, code.ctypes.data)
+        return code
 
     # ---- steps
     def mlp_step(self, it, sigma, lr, N, M):

@@ -193,3 +193,40 @@ def test_dct_plane(orc, C0, q, deadzone, lam, rate):
     zs5, zq5, _, _ = H.snap(np.concatenate([zp, zd3[n0:]]))
     zd5, _ = tr.download_model()
     assert np.array_equal(zd5[:n0], zs5) and np.array_equal(tr.download_zq()[:n0], zq5)
+
+
+@pytest.mark.parametrize("C0,q", [(1, [50]), (2, [75, 30])])
+def test_dct_device_probe_and_refit(orc, C0, q):
+    """The decoder sensitivity probe on the device (an extension: the reference probes on the host)
+    against the oracle's dct_probe_codes on the same decode buffer and weights: codes equal except on a
+    code boundary (the reference calls the probe an estimate); the device refit re-snaps exactly like
+    the host snap with the device's codes."""
+    lay = Layout(64, 48, [(64, 48, C0, True), (16, 12, 4, False)], [32, 32] if C0 == 1 else [20, 12], leak=0.01)
+    say("dct probe", C0, q)
+    z, p, tgt = data(lay, 40 + C0, zscale=0.7)
+    basis, zz = dct_tables(orc)
+    tr = trainer(lay, z, p, tgt, dct={"C": C0, "dc_step": 4, "q": q}, dct_basis=basis, dct_zigzag=zz)
+    n0 = 64 * 48 * C0
+    H = HostDct(orc, lay, q, lam=0.3)
+    zd, _ = tr.download_model()
+    H.probe(lay, p, tr.download_zq())
+    H.snap(zd)
+    tr.set_dct(H.desc(), H.code, H.sym, H.steps)
+    tr.lat_step(1, 0.05, 0.02, 2)                        # move the shadow and the plane
+    zd, pd = tr.download_model()
+    code_d, gain_d = tr.dct_probe()
+    H.probe(lay, pd, tr.download_zq())
+    diff = np.nonzero(code_d != H.code)[0]
+    say("probe codes differing", diff.size, "of", H.n)
+    x = np.log2(np.maximum(gain_d.astype(np.float64), 14 / 64) / (14 / 64)) / 0.6
+    assert diff.size <= max(2, H.n // 100)
+    assert np.all(np.abs(code_d[diff].astype(int) - H.code[diff].astype(int)) == 1)
+    assert np.all(np.abs(x[diff] - np.floor(x[diff]) - 0.5) < 1e-4)   # each one sits on a code boundary
+    assert np.array_equal(np.clip(np.round(x), 0, 15).astype(np.uint8)[x < 15.5], code_d[x < 15.5])
+    code_r = tr.dct_refit()
+    assert np.array_equal(code_r, code_d)                 # same decoder: same probe
+    H.code[:] = code_r
+    zs, zq, _, _ = H.snap(zd)
+    sym_d, code_dl = tr.download_dct()
+    assert np.array_equal(code_dl, code_r) and np.array_equal(sym_d, H.sym)
+    assert np.array_equal(tr.download_zq()[:n0], zq)
