@@ -101,6 +101,12 @@ void ntc_trainer_dct_probe(ntc_trainer* t, uint8_t* code, float* gain);
  * shadow; the new codes are returned if code is not null (download_dct gives the symbols). Replaces the
  * reference's download + host refit + set_dct (main.cpp:4110-4120). Requires a prior set_dct. */
 void ntc_trainer_dct_refit(ntc_trainer* t, uint8_t* code);
+/* The printed error of the current model (mse_of, main.cpp:1764-1788) without a download: the decode
+ * buffer decoded on the device, both images rounded to 8 bits as save_png does, squared differences
+ * summed exactly per texture over the extent ew x eh (0 = the whole image). tex_mse[T] = SSE_t / (3 ew eh),
+ * *weighted = sum_t w_t SSE_t / (3 wsum ew eh), with w_t = cw[3 t]. No counterpart in the reference's
+ * backend (its print path downloads the model and decodes on the host, main.cpp:4155-4160). */
+void ntc_trainer_decode_error(ntc_trainer* t, int ew, int eh, double* tex_mse, double* weighted);
 
 /* Trainer::mlp_step / mlp_step_fd / reset_mlp_adam / mlp_stats (cuda/ntc_cuda.h:110-115) */
 void ntc_trainer_mlp_step(ntc_trainer* t, int it, float sigma, float lr, int N, int M);

@@ -218,6 +218,41 @@ void launch_copy_calibration(Impl& I, const float* src, float* dst, size_t n) {
     NTC_CHECK(hipGetLastError());
 }
 
+// The printed error of a decode (mse_of, main.cpp:1764-1788): both images rounded to 8 bits as save_png
+// does (lround of the [0, 1]-clamped value times 255), the squared integer differences summed per
+// texture over the evaluation extent ew x eh. Integer sums: exact and independent of order; one
+// 64-bit partial per block and texture.
+__global__ void __launch_bounds__(kTPB) k_u8_sse(const float* __restrict__ img, const float* __restrict__ tgt, int W, int ew, int eh,
+                                                int nout, unsigned long long* __restrict__ part) {
+    __shared__ unsigned long long red[kTPB / 64][4];
+    const int T = nout / 3;
+    const int i = blockIdx.x * kTPB + threadIdx.x;
+    unsigned long long s[4] = { 0, 0, 0, 0 };
+    if (i < ew * eh) {
+        const size_t p = (size_t)(i / ew) * W + (i % ew);
+        for (int t = 0; t < T; t++)
+            for (int c = 0; c < 3; c++) {
+                const float x = img[p * nout + 3 * t + c], y = tgt[p * nout + 3 * t + c];
+                const int xi = (int)roundf(__fmul_rn(fminf(1.0f, fmaxf(0.0f, x)), 255.0f));
+                const int yi = (int)roundf(__fmul_rn(fminf(1.0f, fmaxf(0.0f, y)), 255.0f));
+                s[t] += (unsigned long long)((xi - yi) * (xi - yi));
+            }
+    }
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        unsigned long long v = s[t];
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        if (lane == 0) red[wid][t] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < 4) {
+        unsigned long long v = 0;
+        for (int q = 0; q < kTPB / 64; q++) v += red[q][threadIdx.x];
+        part[(size_t)blockIdx.x * 4 + threadIdx.x] = v;
+    }
+}
+
 __global__ void __launch_bounds__(kTPB) k_debug_factors(NoiseFix nt, uint32_t k0, size_t n, float* __restrict__ rad,
                                                        float* __restrict__ cosv) {
     const size_t i = (size_t)blockIdx.x * kTPB + threadIdx.x;
@@ -326,6 +361,12 @@ void launch_debug_gauss(Impl& I, uint32_t stream, uint32_t step, uint32_t pair, 
 
 void launch_debug_factors(Impl& I, uint32_t k0, size_t n, float* rad, float* cosv) {
     hipLaunchKernelGGL(k_debug_factors, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, I.noise, k0, n, rad, cosv);
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_u8_sse(Impl& I, int ew, int eh, unsigned long long* part) {
+    hipLaunchKernelGGL(k_u8_sse, dim3(blocks_for((size_t)ew * eh, kTPB)), dim3(kTPB), 0, I.stream, I.img, I.tgt, I.d.W, ew, eh, I.d.nout,
+                       part);
     NTC_CHECK(hipGetLastError());
 }
 

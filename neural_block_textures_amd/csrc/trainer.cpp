@@ -104,6 +104,33 @@ void dct_refit_impl(Impl& I, uint8_t* code) {
     sync(I);
 }
 
+// The print path's error figures without a download (mse_of, main.cpp:1764-1788): decode the decode
+// buffer on the device, then the exact per-texture sums of squared 8-bit differences.
+void decode_error_impl(Impl& I, int ew, int eh, double* tex_mse, double* weighted) {
+    if (I.d.nout % 3 != 0) die("decode_error needs RGB textures (nout a multiple of 3)");
+    if (ew <= 0 || ew > I.d.W) ew = I.d.W;
+    if (eh <= 0 || eh > I.d.H) eh = I.d.H;
+    const size_t blocks = ((size_t)ew * eh + 255) / 256;
+    unsigned long long* part = nullptr;
+    NTC_CHECK(hipMalloc(&part, blocks * 4 * sizeof(unsigned long long)));
+    launch_decode(I, I.zdec);
+    launch_u8_sse(I, ew, eh, part);
+    std::vector<unsigned long long> h(blocks * 4);
+    NTC_CHECK(hipMemcpyAsync(h.data(), part, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost, I.stream));
+    sync(I);
+    NTC_CHECK(hipFree(part));
+    const int T = I.d.nout / 3;
+    const double npix = (double)ew * eh;
+    double ws = 0.0;
+    for (int t = 0; t < T; t++) {
+        unsigned long long sse = 0;
+        for (size_t b = 0; b < blocks; b++) sse += h[b * 4 + t];
+        if (tex_mse) tex_mse[t] = (double)sse / (3.0 * npix);
+        ws += (double)I.d.cw[3 * t] * (double)sse;
+    }
+    if (weighted) *weighted = ws / (3.0 * (double)I.d.wsum * npix);
+}
+
 void resolve_times(Impl& I) {
     bool any = false;
     for (auto& kv : I.times) if (!kv.second.pending.empty()) any = true;

@@ -170,6 +170,10 @@ void launch_dct_snap(Impl& I);
 void launch_dct_recon(Impl& I);
 // the decoder sensitivity probe over the decode buffer: codes (and block gains, when gain != null) into device buffers
 void launch_dct_probe(Impl& I, uint8_t* code, float* gain);
+// per-block, per-texture 8-bit squared-error sums of the decode in img against the target (ceil(ew eh / 256) x 4)
+void launch_u8_sse(Impl& I, int ew, int eh, unsigned long long* part);
+// decode the decode buffer on the device and return mse_of's per-texture and weighted figures
+void decode_error_impl(Impl& I, int ew, int eh, double* tex_mse, double* weighted);
 void dct_probe_impl(Impl& I, uint8_t* code, float* gain);
 void dct_refit_impl(Impl& I, uint8_t* code);
 void launch_dct_rate_pairs(Impl& I, int K, float sigma);

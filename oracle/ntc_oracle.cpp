@@ -877,3 +877,28 @@ double or_train_iter(const OrModel* mp, const OrTrainCfg* c, OrTrainState* s, co
 }
 
 }   // extern "C"
+
+// mse_of, main.cpp:1764-1788: both images rounded to 8 bits as save_png does, squared differences per texture
+extern "C" void or_mse_of(const float* a, const float* b, int W, int H, int nc, const float* w, float wsum, int ew, int eh,
+                          double* tex, double* weighted) {
+    const int T = nc / 3;
+    if (ew <= 0 || ew > W) ew = W;
+    if (eh <= 0 || eh > H) eh = H;
+    double sse[4] = { 0, 0, 0, 0 };
+    for (int yy = 0; yy < eh; yy++)
+        for (int xx = 0; xx < ew; xx++) {
+            const size_t p = (size_t)yy * W + xx;
+            for (int t = 0; t < T; t++)
+                for (int c = 0; c < 3; c++) {
+                    const int xi = (int)std::lround(std::min(1.0f, std::max(0.0f, a[p * nc + 3 * t + c])) * 255.0f);
+                    const int yi = (int)std::lround(std::min(1.0f, std::max(0.0f, b[p * nc + 3 * t + c])) * 255.0f);
+                    const double d = (double)(xi - yi);
+                    sse[t] += d * d;
+                }
+        }
+    const double npix = (double)ew * eh;
+    double ws = 0.0;
+    for (int t = 0; t < T; t++) { tex[t] = sse[t] / (3.0 * npix); ws += (double)w[t] * sse[t]; }
+    *weighted = ws / (3.0 * wsum * npix);
+}
+

@@ -144,6 +144,11 @@ int or_round_fp16(float* p, long long n, long long* changed);
 int or_q8_index(float z, float lo, float range, int levels);
 float or_q8_value(int k, float lo, float range, int levels);
 
+/* ---- the printed error (mse_of, main.cpp:1764-1788): a and b are W*H*nc (nc = 3 T), w[T], extent ew x eh
+ * (0 = whole); tex[T] = SSE_t / (3 ew eh), *weighted = sum_t w_t SSE_t / (3 wsum ew eh), 8-bit rounding ---- */
+void or_mse_of(const float* a, const float* b, int W, int H, int nc, const float* w, float wsum, int ew, int eh, double* tex,
+               double* weighted);
+
 /* ---- full training driver (main.cpp:4063-4148, --rng hash), for trajectory parity and timing ---- */
 typedef struct OrTrainCfg {
     uint64_t seed;

@@ -145,6 +145,7 @@ def _load(path):
 
 _P = C.c_void_p
 _SIGS = {
+    "mse_of": (None, [_P, _P, C.c_int, C.c_int, C.c_int, _P, C.c_float, C.c_int, C.c_int, _P, _P]),
     "gauss": (C.c_float, [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64]),
     "noise_u32": (C.c_uint32, [C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64]),
     "noise_uniform": (C.c_uint32, [C.c_uint32, C.c_uint32]),

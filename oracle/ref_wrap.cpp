@@ -245,6 +245,17 @@ void ref_dct_rate_pair(const OrDct* d, const OrLevel* L0, const float* z, const 
             dbits[(size_t)b * Q.C + c] = dct_rate_block(Q, L, (size_t)b, c, z, eps0, sg, 1.0f) - dct_rate_block(Q, L, (size_t)b, c, z, eps0, sg, -1.0f);
 }
 
+// ---- the printed error
+void ref_mse_of(const float* a, const float* b, int W, int H, int nc, const float* w, float wsum, int ew, int eh, double* tex,
+                double* weighted) {
+    Image A, B;
+    A.w = B.w = W; A.h = B.h = H; A.nc = B.nc = nc;
+    A.rgb.assign(a, a + (size_t)W * H * nc); B.rgb.assign(b, b + (size_t)W * H * nc);
+    const Mse m = mse_of(A, B, std::vector<float>(w, w + nc / 3), wsum, ew, eh);
+    for (int t = 0; t < nc / 3; t++) tex[t] = m.tex[t];
+    *weighted = m.weighted;
+}
+
 // ---- fp16 and post-hoc quantization
 int ref_ntcb_selfcheck() { return ntcb_selfcheck() ? 1 : 0; }
 uint16_t ref_f32_to_f16(float f, int* overflow) { bool ov = false; const uint16_t h = ntcb_f32_to_f16(f, &ov); *overflow = ov ? 1 : 0; return h; }

@@ -200,6 +200,20 @@ def main():
     h = np.array([L.ref_f32_to_f16(C.c_float(x), C.byref(ov)) for x in xs], np.uint16)
     back = np.array([L.ref_f16_to_f32(int(v)) for v in range(65536)], np.float32)
     np.savez_compressed(os.path.join(OUT, "fp16.npz"), x=xs, half=h, all_back=back)
+    # ---- the printed error (mse_of): two textures, values outside [0, 1] and on 8-bit rounding boundaries,
+    # the whole image and a partial extent
+    rng = np.random.default_rng(8)
+    W, H, nc = 37, 29, 6
+    a = rng.normal(0.5, 0.4, W * H * nc).astype(np.float32)
+    b = rng.random(W * H * nc).astype(np.float32)
+    a[:300] = (np.arange(300) % 256 + 0.5).astype(np.float32) / np.float32(255.0)   # k + 1/2 LSB: lround's half cases
+    wts = np.array([1.0, 2.5], np.float32)
+    mse = dict(a=a, b=b, shape=np.array([W, H, nc]), w=wts, wsum=np.float32(3.5))
+    for tag, (ew, eh) in {"full": (0, 0), "part": (30, 20)}.items():
+        tex, wt = np.zeros(2), C.c_double()
+        L.ref_mse_of(P(a), P(b), W, H, nc, P(wts), C.c_float(3.5), ew, eh, P(tex), C.byref(wt))
+        mse[f"tex_{tag}"], mse[f"weighted_{tag}"], mse[f"extent_{tag}"] = tex, np.float64(wt.value), np.array([ew, eh])
+    np.savez_compressed(os.path.join(OUT, "mse.npz"), **mse)
     print("golden vectors written to", OUT)
 
 

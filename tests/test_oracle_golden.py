@@ -188,3 +188,15 @@ def test_fp16(orc):
     assert np.array_equal(h, fx["half"])
     back = np.array([orc._f16_to_f32(v) for v in range(65536)], np.float32)
     assert np.array_equal(back.view(np.uint32), fx["all_back"].view(np.uint32))
+
+
+def test_mse_of(orc):
+    """the printed error (mse_of) against the reference's, whole image and a partial extent"""
+    fx = golden("mse.npz")
+    W, H, nc = (int(v) for v in fx["shape"])
+    a, b, w = fx["a"], fx["b"], fx["w"]
+    for tag in ("full", "part"):
+        ew, eh = (int(v) for v in fx[f"extent_{tag}"])
+        tex, wt = np.zeros(2), C.c_double()
+        orc._mse_of(a.ctypes.data, b.ctypes.data, W, H, nc, w.ctypes.data, float(fx["wsum"]), ew, eh, tex.ctypes.data, C.byref(wt))
+        assert np.array_equal(tex, fx[f"tex_{tag}"]) and wt.value == float(fx[f"weighted_{tag}"])
