@@ -107,6 +107,10 @@ void ntc_trainer_dct_refit(ntc_trainer* t, uint8_t* code);
  * *weighted = sum_t w_t SSE_t / (3 wsum ew eh), with w_t = cw[3 t]. No counterpart in the reference's
  * backend (its print path downloads the model and decodes on the host, main.cpp:4155-4160). */
 void ntc_trainer_decode_error(ntc_trainer* t, int ew, int eh, double* tex_mse, double* weighted);
+/* The decode of the current model rounded to 8 bits as the reference's save_png and ntc_decode write it
+ * (lround of the [0, 1]-clamped value times 255): W*H*nout bytes, interleaved per pixel. No counterpart in
+ * the reference's backend (its decoder is the host program ntc_decode.cpp). */
+void ntc_trainer_decode_rgb8(ntc_trainer* t, uint8_t* out);
 
 /* Trainer::mlp_step / mlp_step_fd / reset_mlp_adam / mlp_stats (cuda/ntc_cuda.h:110-115) */
 void ntc_trainer_mlp_step(ntc_trainer* t, int it, float sigma, float lr, int N, int M);

@@ -218,6 +218,12 @@ void launch_copy_calibration(Impl& I, const float* src, float* dst, size_t n) {
     NTC_CHECK(hipGetLastError());
 }
 
+// A decode rounded to 8 bits as save_png writes it (lround of the [0, 1]-clamped value times 255).
+__global__ void __launch_bounds__(kTPB) k_pack_u8(const float* __restrict__ img, size_t n, uint8_t* __restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * kTPB + threadIdx.x;
+    if (i < n) out[i] = (uint8_t)(int)roundf(__fmul_rn(fminf(1.0f, fmaxf(0.0f, img[i])), 255.0f));
+}
+
 // The printed error of a decode (mse_of, main.cpp:1764-1788): both images rounded to 8 bits as save_png
 // does (lround of the [0, 1]-clamped value times 255), the squared integer differences summed per
 // texture over the evaluation extent ew x eh. Integer sums: exact and independent of order; one
@@ -367,6 +373,13 @@ void launch_debug_factors(Impl& I, uint32_t k0, size_t n, float* rad, float* cos
 void launch_u8_sse(Impl& I, int ew, int eh, unsigned long long* part) {
     hipLaunchKernelGGL(k_u8_sse, dim3(blocks_for((size_t)ew * eh, kTPB)), dim3(kTPB), 0, I.stream, I.img, I.tgt, I.d.W, ew, eh, I.d.nout,
                        part);
+    NTC_CHECK(hipGetLastError());
+}
+
+void launch_pack_u8(Impl& I, uint8_t* out) {
+    ProfScope ps(I, "pack_u8");
+    const size_t n = (size_t)I.npix * I.d.nout;
+    hipLaunchKernelGGL(k_pack_u8, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, I.img, n, out);
     NTC_CHECK(hipGetLastError());
 }
 

@@ -12,6 +12,12 @@ using ShapeTwoLevel = FixedShape<8, 4, 0, 1, 32, 2, 3>;   // 512x512 RGB, 128x12
 using ShapeMaterial = FixedShape<2, 4, 0, 1, 32, 2, 12>;  // 4 x 512x512 maps, --qat 2 512x512x2 + 128x128x4, 32,32
 using ShapeDct = FixedShape<1, 4, 0, 1, 32, 2, 3>;        // 512x512 RGB, --dct-q 512x512x1 + 128x128x4, 32,32
 using ShapeLarge = FixedShape<4, 8, 0, 1, 64, 2, 12>;     // 4 x 2048x2048 maps, 1024x1024x4 + 256x256x8, 64,64
+// the shapes of the reference's published runs (README.md:690-712; out_m1234/model.bin)
+using ShapeM1234 = FixedShape<4, 4, 0, 1, 36, 2, 12>;     // 4 maps, 128x128x4 + 64x64x4, 36,36 (10-36-36-12)
+using ShapeDct17 = FixedShape<1, 4, 0, 1, 17, 2, 3>;      // 1-channel DCT plane + 4 channels, 17,17 (7-17-17-3)
+using ShapeDct2x17 = FixedShape<2, 4, 0, 1, 17, 2, 3>;    // 2-channel DCT plane + 4 channels, 17,17 (8-17-17-3)
+using ShapeDct11 = FixedShape<1, 4, 0, 1, 11, 2, 3>;      // 7-11-11-3
+using ShapeDct7 = FixedShape<1, 4, 0, 1, 7, 2, 3>;        // 7-7-7-3
 
 template <class F>
 inline const char* dispatch_shape(const DevModel& m, F&& f) {
@@ -21,6 +27,11 @@ inline const char* dispatch_shape(const DevModel& m, F&& f) {
     if (ShapeLarge::matches(m)) { f(ShapeLarge{}); return "4+8|uv|64x2|12"; }
     if (Shape256::matches(m)) { f(Shape256{}); return "4|uv|16x2|3"; }
     if (ShapeDefault::matches(m)) { f(ShapeDefault{}); return "4|uv|24x2|3"; }
+    if (ShapeM1234::matches(m)) { f(ShapeM1234{}); return "4+4|uv|36x2|12"; }
+    if (ShapeDct17::matches(m)) { f(ShapeDct17{}); return "1+4|uv|17x2|3"; }
+    if (ShapeDct2x17::matches(m)) { f(ShapeDct2x17{}); return "2+4|uv|17x2|3"; }
+    if (ShapeDct11::matches(m)) { f(ShapeDct11{}); return "1+4|uv|11x2|3"; }
+    if (ShapeDct7::matches(m)) { f(ShapeDct7{}); return "1+4|uv|7x2|3"; }
     f(RuntimeShape{});
     return "runtime";
 }

@@ -131,6 +131,19 @@ void decode_error_impl(Impl& I, int ew, int eh, double* tex_mse, double* weighte
     if (weighted) *weighted = ws / (3.0 * (double)I.d.wsum * npix);
 }
 
+// The decoder's product (ntc_decode.cpp's RGB8 output, save_png's rounding) without the float image
+// crossing PCIe: decode on the device, round to 8 bits there, download W x H x nout bytes.
+void decode_rgb8_impl(Impl& I, uint8_t* out) {
+    const size_t n = (size_t)I.npix * I.d.nout;
+    uint8_t* d = nullptr;
+    NTC_CHECK(hipMalloc(&d, n));
+    launch_decode(I, I.zdec);
+    launch_pack_u8(I, d);
+    NTC_CHECK(hipMemcpyAsync(out, d, n, hipMemcpyDeviceToHost, I.stream));
+    sync(I);
+    NTC_CHECK(hipFree(d));
+}
+
 void resolve_times(Impl& I) {
     bool any = false;
     for (auto& kv : I.times) if (!kv.second.pending.empty()) any = true;

@@ -172,6 +172,10 @@ void launch_dct_recon(Impl& I);
 void launch_dct_probe(Impl& I, uint8_t* code, float* gain);
 // per-block, per-texture 8-bit squared-error sums of the decode in img against the target (ceil(ew eh / 256) x 4)
 void launch_u8_sse(Impl& I, int ew, int eh, unsigned long long* part);
+// img rounded to 8 bits (save_png) into out (device, npix x nout)
+void launch_pack_u8(Impl& I, uint8_t* out);
+// decode the decode buffer and download it as 8-bit values
+void decode_rgb8_impl(Impl& I, uint8_t* out);
 // decode the decode buffer on the device and return mse_of's per-texture and weighted figures
 void decode_error_impl(Impl& I, int ew, int eh, double* tex_mse, double* weighted);
 void dct_probe_impl(Impl& I, uint8_t* code, float* gain);

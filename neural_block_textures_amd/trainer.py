@@ -105,6 +105,7 @@ def library() -> C.CDLL:
             "ntc_trainer_dct_probe": (None, [P, P, P]),
             "ntc_trainer_dct_refit": (None, [P, P]),
             "ntc_trainer_decode_error": (None, [P, C.c_int, C.c_int, P, P]),
+            "ntc_trainer_decode_rgb8": (None, [P, P]),
             "ntc_trainer_debug_gauss": (None, [P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, C.c_size_t, P]),
             "ntc_trainer_debug_noise_factors": (None, [P, C.c_uint32, C.c_size_t, P, P]),
             "ntc_trainer_debug_copy_calibration": (None, [P, C.c_size_t, C.c_int]),
@@ -316,6 +317,12 @@ class Trainer:
         code = np.empty(self.dct_n, np.uint8)
         self._lib.ntc_trainer_dct_refit(self._h, code.ctypes.data)
         return code
+
+    def decode_rgb8(self):
+        """the decode rounded to 8 bits (save_png's rounding): uint8 [H*W*nout]"""
+        out = np.empty(self.layout.W * self.layout.H * self.layout.nout, np.uint8)
+        self._lib.ntc_trainer_decode_rgb8(self._h, out.ctypes.data)
+        return out
 
     def decode_error(self, ew=0, eh=0):
         """mse_of of the device's decode: (per-texture 8-bit MSE, weighted MSE)"""
