@@ -106,6 +106,16 @@ public:
     void debug_last_dl(std::vector<double>& dl) const;
     void debug_last_zgrad(std::vector<float>& g) const;
 
+    // Extensions with no counterpart in the reference's Trainer; each replaces a host stall of main.cpp.
+    // The decoder sensitivity probe of a --dct-q level 0 on the device (dct_probe_codes, main.cpp:1001-1032).
+    void dct_probe(uint8_t* code, float* gain);
+    // Decoder::dct_refit on the device (main.cpp:1672-1680): probe, replace the codes, re-snap level 0.
+    void dct_refit(uint8_t* code);
+    // mse_of (main.cpp:1764-1788) of the device's decode: per-texture and weighted 8-bit MSE over ew x eh.
+    void decode_error(int ew, int eh, double* tex_mse, double* weighted);
+    // The decode rounded to 8 bits as save_png writes it: W * H * nout bytes.
+    void decode_rgb8(uint8_t* out);
+
     struct Impl;
     Impl* im;
 };

@@ -81,11 +81,11 @@ void ntc_trainer_download_dct_rate(ntc_trainer* t, int32_t* bits, int32_t* dbits
     t->t.download_dct_rate(bits, dbits_last_pair, ntrunc, nz_before, hits, evals);
 }
 
-void ntc_trainer_dct_probe(ntc_trainer* t, uint8_t* code, float* gain) { ntc_hip::dct_probe_impl(*t->t.im, code, gain); }
-void ntc_trainer_dct_refit(ntc_trainer* t, uint8_t* code) { ntc_hip::dct_refit_impl(*t->t.im, code); }
-void ntc_trainer_decode_rgb8(ntc_trainer* t, uint8_t* out) { ntc_hip::decode_rgb8_impl(*t->t.im, out); }
+void ntc_trainer_dct_probe(ntc_trainer* t, uint8_t* code, float* gain) { t->t.dct_probe(code, gain); }
+void ntc_trainer_dct_refit(ntc_trainer* t, uint8_t* code) { t->t.dct_refit(code); }
+void ntc_trainer_decode_rgb8(ntc_trainer* t, uint8_t* out) { t->t.decode_rgb8(out); }
 void ntc_trainer_decode_error(ntc_trainer* t, int ew, int eh, double* tex_mse, double* weighted) {
-    ntc_hip::decode_error_impl(*t->t.im, ew, eh, tex_mse, weighted);
+    t->t.decode_error(ew, eh, tex_mse, weighted);
 }
 
 void ntc_trainer_mlp_step(ntc_trainer* t, int it, float sigma, float lr, int N, int M) { t->t.mlp_step(it, sigma, lr, N, M); }

@@ -560,6 +560,11 @@ void Trainer::decode_full(const float* z_host, float* img) {
     sync(I);
 }
 
+void Trainer::dct_probe(uint8_t* code, float* gain) { ntc_hip::dct_probe_impl(*im, code, gain); }
+void Trainer::dct_refit(uint8_t* code) { ntc_hip::dct_refit_impl(*im, code); }
+void Trainer::decode_error(int ew, int eh, double* tex_mse, double* weighted) { ntc_hip::decode_error_impl(*im, ew, eh, tex_mse, weighted); }
+void Trainer::decode_rgb8(uint8_t* out) { ntc_hip::decode_rgb8_impl(*im, out); }
+
 void Trainer::debug_last_batch(std::vector<int>& bidx) const {
     Impl& I = *im;
     bidx.resize(I.last_M);
