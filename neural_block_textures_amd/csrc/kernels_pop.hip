@@ -10,7 +10,8 @@
 // maximum needs no canonicalising copies); a hidden layer's outputs feed the next layer in the order
 // the matrix instruction leaves them (no transpose; each unit's sum takes its inputs in another
 // order than the reference's ascending one); the sigmoid is the hardware exp2 and reciprocal, its
-// -log2(e) folded into the output layer; a lane's four channel terms are added in float per tile; tile
+// -log2(e) folded into the output layer; a lane's channel terms cw d d are fused multiply-adds in float
+// over the tiles a wave evaluates at once, then added into a double; tile
 // inputs are buffer loads with a loop-invariant lane offset and the tile's offset in an SGPR. Member
 // losses stay within 1e-5 relative of the reference's (they are not bit-identical here anyway:
 // the sigmoid differs in the last bits).
@@ -136,34 +137,53 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     double e = 0.0;
     const __amdgpu_buffer_rsrc_t rf = buffer_of(feat, 4u * ((uint32_t)Q::kIn * (uint32_t)Mcap + 64u));
     const __amdgpu_buffer_rsrc_t rt = buffer_of(btgt, 4u * ((uint32_t)Q::kNout * (uint32_t)Mcap + 64u));
-    PopTileIn<S> cur;
-    pop_load<S>(cur, rf, rt, 4u * (uint32_t)(s0 + 16 * half), fo, to);
     constexpr int U = pop_u<S>();
-    for (int j = 0; j < mine; j += U) {
-        PopTileIn<S> nxt;
-        if (j + U < mine) pop_load<S>(nxt, rf, rt, 4u * (uint32_t)(s0 + 16 * (2 * (j + U) + half)), fo, to);
+    // One pass: tiles j .. j + U - 1 from c, while tiles j + U .. load into n. The loop alternates
+    // two input sets, so no registers are copied between passes. The loads are issued on every pass
+    // (the last one reloads its own tiles) so that the wait for them falls in the next pass.
+    auto pass = [&](PopTileIn<S>& c, PopTileIn<S>& n, int j) {
+        pop_load<S>(n, rf, rt, 4u * (uint32_t)(s0 + 16 * (2 * (j + U < mine ? j + U : j) + half)), fo, to);
         if constexpr (Q::kIn % 4 != 0) {   // inputs past nin are zero
 #pragma unroll
             for (int u = 0; u < U; u++)
-                if (4 * (Q::kKs1 - 1) + g >= Q::kIn) cur.b1[u][Q::kKs1 - 1] = 0.0f;
+                if (4 * (Q::kKs1 - 1) + g >= Q::kIn) c.b1[u][Q::kKs1 - 1] = 0.0f;
         }
         f4v o[U];
-        mfma_forward<S, U, LeakUnit, false>(W, cur.b1, m.leak, o);
+        mfma_forward<S, U, LeakUnit, false>(W, c.b1, m.leak, o);
+        // this lane's channel terms cw (d d): one multiply and one fused multiply-add each, summed in
+        // float over the pass's tiles, then into the double
+        float dq[U][4], dd[U][4];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int st = s0 + 16 * (2 * (j + u) + half);   // first slot of the tile (uniform)
-            float tsum = 0.0f;   // this lane's four channel terms cw (d d), added in float, then into the double
+        for (int u = 0; u < U; u++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float d = out_of<S>(o[u][r], Clamp) - cur.t[u][r];
-                tsum += __fmul_rn(cw[r], __fmul_rn(d, d));
+                dd[u][r] = out_of<S>(o[u][r], Clamp) - c.t[u][r];
+                dq[u][r] = __fmul_rn(cw[r], dd[u][r]);
             }
-            if (j + u < mine) {
-                if (st + 16 <= s1) e += (double)tsum;
-                else e += st + i16 < s1 ? (double)tsum : 0.0;
+        if (j + U <= mine && s0 + 16 * (2 * (j + U - 1) + half) + 16 <= s1) {   // all U tiles whole (uniform)
+            float tsum = 0.0f;
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) tsum = __builtin_fmaf(dq[u][r], dd[u][r], tsum);
+            e += (double)tsum;
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int st = s0 + 16 * (2 * (j + u) + half);   // first slot of the tile (uniform)
+                float tsum = 0.0f;
+#pragma unroll
+                for (int r = 0; r < 4; r++) tsum = __builtin_fmaf(dq[u][r], dd[u][r], tsum);
+                if (j + u < mine && st + i16 < s1) e += (double)tsum;
             }
         }
-        cur = nxt;
+    };
+    PopTileIn<S> in0, in1;
+    pop_load<S>(in0, rf, rt, 4u * (uint32_t)(s0 + 16 * half), fo, to);
+    for (int j = 0; j < mine; j += 2 * U) {
+        pass(in0, in1, j);
+        if (j + U >= mine) break;
+        pass(in1, in0, j + U);
     }
     e = wave_sum(e);
     if (lane == 0) red[wave] = e;
