@@ -199,8 +199,9 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
 // pair's texels perturbed by +sg eps and by -sg eps (features_pm: both members from one set of
 // taps and texel loads) into LDS.
 // Phase 2: each wave evaluates a quarter of the pixels in 16-pixel tiles, the + and - members of
-// a tile together; each pixel's error is the reference's float fma chain over its channels in
-// ascending order (decode_err), and dpix = (e+ - e-) * inv_px.
+// a tile together; each pixel's error is decode_err's float sum of cw (d d) over its channels (a
+// lane's four in ascending order, then the lane groups pairwise: the float sum is within a few ulp
+// of the reference's ascending chain), and dpix = (e+ - e-) * inv_px.
 // pixels per block: 512, or 256 for wide inputs (LDS)
 template <class S>
 constexpr int lat_pix() { return MfmaShape<S>::kIn <= 8 ? 512 : 256; }
@@ -230,10 +231,28 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     float cw[4];
     lane_cw<NO>(m.cw, g, cw);
     float* out = dpix + (size_t)k * m.npix;
+    // the targets of a tile: lane (g, j) reads channels 4 g .. 4 g + 3 of pixel j (one 16-byte load
+    // when a pixel's row is a whole number of float4; rows past the last channel are clamped)
+    auto load_t = [&](int u, float (&t)[4]) {
+        const int pr = min(p0 + (kLatPix / 4) * wave + 16 * u + i16, m.npix - 1);
+        if constexpr (NO % 4 == 0) {
+            const f4v v = *reinterpret_cast<const f4v*>(tgt + (size_t)pr * NO + min(4 * g, NO - 4));
+#pragma unroll
+            for (int r = 0; r < 4; r++) t[r] = v[r];
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; r++) t[r] = tgt[(size_t)pr * NO + min(4 * g + r, NO - 1)];
+        }
+    };
+    float tn[4];
+    load_t(0, tn);
     for (int u = 0; u < kLatPix / 64; u++) {   // kLatPix / 64 tiles of 16 pixels per wave
         const int col = (kLatPix / 4) * wave + 16 * u + i16;
         const int p = p0 + col;
-        const int pr = min(p, m.npix - 1);
+        float t[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) t[r] = tn[r];
+        if (u + 1 < kLatPix / 64) load_t(u + 1, tn);
         float b1[2][Q::kKs1];
 #pragma unroll
         for (int s2 = 0; s2 < 2; s2++)
@@ -243,30 +262,32 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
                 const float v = F[s2][min(kk, NIN - 1)][col];
                 b1[s2][ks] = kk < NIN ? v : 0.0f;
             }
-        float t[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) t[r] = tgt[(size_t)pr * NO + min(4 * g + r, NO - 1)];
         f4v o[2];
         mfma_forward<S, 2, LeakUnit, false>(W, b1, m.leak, o);
-        float dd[2][4];
+        // each lane's four channel terms cw (d d) in ascending order, then the four lane groups
+        // added pairwise (permlane swaps): e+ in lanes 0-31, e- in lanes 32-63, then e+ - e-
+        float ep = 0.0f, em = 0.0f;
 #pragma unroll
-        for (int s2 = 0; s2 < 2; s2++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float d = out_of<S>(o[s2][r], Clamp) - t[r];
-                dd[s2][r] = __fmul_rn(d, d);
-            }
-        const float ep = chain_err_f<NO>(dd[0], cw, lane);
-        const float em = chain_err_f<NO>(dd[1], cw, lane);
-        if (g == (NO - 1) / 4 && p < m.npix) out[p] = __fmul_rn(ep - em, m.inv_px);
+        for (int r = 0; r < 4; r++) {
+            const float dp = out_of<S>(o[0][r], Clamp) - t[r], dm = out_of<S>(o[1][r], Clamp) - t[r];
+            ep = __builtin_fmaf(cw[r], __fmul_rn(dp, dp), ep);
+            em = __builtin_fmaf(cw[r], __fmul_rn(dm, dm), em);
+        }
+        const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(ep), __float_as_uint(em), false, false);
+        const float s = __uint_as_float(h[0]) + __uint_as_float(h[1]);   // groups 0 + 2 and 1 + 3
+        const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+        const float c = __uint_as_float(q[0]) + __uint_as_float(q[1]);   // lanes 0-31: e+, 32-63: e-
+        const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+        if (g == 0 && p < m.npix) out[p] = __fmul_rn(__uint_as_float(x[0]) - __uint_as_float(x[1]), m.inv_px);
     }
 }
 
 // The selector search (qat_search, main.cpp:2088-2139) on the matrix cores, for a nearest level 0
 // of the image's size (each texel's cell is its own pixel): wave = 64 pixels in four 16-pixel tiles. Every lane builds its pixel's
 // features (features<S>); per channel, every candidate value is one MLP evaluation of the tile with
-// that feature replaced, the pixel's loss the reference's double sum over its channels in
-// ascending order (loss_subset's terms), broadcast to the pixel's four lanes. The choice is the
+// that feature replaced (two candidates at a time), the pixel's loss the double sum of the float
+// terms of loss_subset over its channels (a lane's four in ascending order, then the pixel's four
+// lanes pairwise, the same value in each of them). The choice is the
 // reference's: the current grid value first, then every other value with strict <, so the first
 // strictly smaller loss wins (main.cpp:2101-2132). The winner enters the features of the next channel
 // and is written to the decode buffer.
@@ -275,14 +296,13 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                                                  const float* __restrict__ tgt, const int* __restrict__ qat_bits,
                                                  const float* __restrict__ grid) {
     using Q = MfmaShape<S>;
-    constexpr int NIN = Q::kIn, NO = Q::kNout, C0 = S::kC0, GL = (NO - 1) / 4;
+    constexpr int NIN = Q::kIn, NO = Q::kNout, C0 = S::kC0;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
     MfmaWeights<S> W;
     mfma_load<S, false>(W, w, lane);
     if (!m.clamp_out) scale_output<S>(W, kNegLog2e);
     float cw[4];
     lane_cw<NO>(m.cw, g, cw);
-    const int from_last = (GL * 16 + i16) << 2;   // the lane of this pixel that holds its loss
     const bool unit_leak = m.leak >= 0.0f && m.leak <= 1.0f;
     for (int u = 0; u < 4; u++) {
         const int p = blockIdx.x * 256 + wave * 64 + u * 16 + i16;
@@ -307,25 +327,28 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
             }
             double cur_l = 0.0, best_l = 0.0;
             int best_k = -1;
-            for (int kc = 0; kc <= levels; kc++) {
-                const float val = gv[kc];
-                if (g == c % 4) b1[0][c / 4] = val;
-                f4v o[1];
-                if (unit_leak) mfma_forward<S, 1, true, false>(W, b1, m.leak, o);
-                else mfma_forward<S, 1, false, false>(W, b1, m.leak, o);
-                float dd[4];
+            for (int kc = 0; kc <= levels; kc += 2) {   // 2^bits candidates: two tiles at a time
+                float b2[2][Q::kKs1];
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float d = out_of<S>(o[0][r], m.clamp_out != 0) - t[r];
-                    dd[r] = __fmul_rn(d, d);
+                for (int v = 0; v < 2; v++)
+#pragma unroll
+                    for (int ks = 0; ks < Q::kKs1; ks++) b2[v][ks] = b1[0][ks];
+                if (g == c % 4) { b2[0][c / 4] = gv[kc]; b2[1][c / 4] = gv[kc + 1]; }
+                f4v o[2];
+                if (unit_leak) mfma_forward<S, 2, true, false>(W, b2, m.leak, o);
+                else mfma_forward<S, 2, false, false>(W, b2, m.leak, o);
+#pragma unroll
+                for (int v = 0; v < 2; v++) {
+                    double l = 0.0;   // this lane's channels in ascending order, then the pixel's lanes
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float d = out_of<S>(o[v][r], m.clamp_out != 0) - t[r];
+                        l += (double)__fmul_rn(cw[r], __fmul_rn(d, d));
+                    }
+                    l = group_sum_d(l);
+                    if (kc + v == cur) cur_l = l;
+                    else if (best_k < 0 || l < best_l) { best_l = l; best_k = kc + v; }
                 }
-                double l = chain_err_d<NO>(dd, cw, lane);
-                const long long b = __double_as_longlong(l);   // broadcast the pixel's loss to its four lanes
-                const int lo = __builtin_amdgcn_ds_bpermute(from_last, (int)(b & 0xFFFFFFFFll));
-                const int hi = __builtin_amdgcn_ds_bpermute(from_last, (int)(b >> 32));
-                l = __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
-                if (kc == cur) cur_l = l;
-                else if (best_k < 0 || l < best_l) { best_l = l; best_k = kc; }
             }
             const int win = (best_k >= 0 && best_l < cur_l) ? best_k : cur;
             f[c] = gv[win];

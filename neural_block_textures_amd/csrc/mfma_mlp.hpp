@@ -228,6 +228,21 @@ __device__ __forceinline__ float chain_err_f(const float (&dd)[4], const float (
     return e;
 }
 
+// The sum of v over the four lane groups of each pixel (lanes j, j + 16, j + 32, j + 48), in every
+// one of them: (g0 + g2) + (g1 + g3), from two permlane swaps of each half of the double (no LDS).
+__device__ __forceinline__ double group_sum_d(double v) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const unsigned lo = (unsigned)b, hi = (unsigned)(b >> 32);
+    auto join = [](unsigned l, unsigned h) { return __longlong_as_double((long long)(((unsigned long long)h << 32) | l)); };
+    const auto l32 = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto h32 = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    const double s = join(l32[0], h32[0]) + join(l32[1], h32[1]);   // rows: g0 + g2, g1 + g3, g0 + g2, g1 + g3
+    const unsigned long long sb = (unsigned long long)__double_as_longlong(s);
+    const auto l16 = __builtin_amdgcn_permlane16_swap((unsigned)sb, (unsigned)sb, false, false);
+    const auto h16 = __builtin_amdgcn_permlane16_swap((unsigned)(sb >> 32), (unsigned)(sb >> 32), false, false);
+    return join(l16[0], h16[0]) + join(l16[1], h16[1]);
+}
+
 // loss_subset's per-pixel terms (main.cpp:1747): s += (double)(cw (d d)), double
 template <int NO>
 __device__ __forceinline__ double chain_err_d(const float (&dd)[4], const float (&cw)[4], int lane) {
