@@ -1,10 +1,12 @@
-"""Decode a model file of the reference (v11 .. v14) on the GPU to 8-bit PNGs, one per texture.
+"""Decode a model file of the reference (model.bin v11 .. v14, or the bit-packed model.ntcb) on the GPU
+to 8-bit PNGs, one per texture, cropped to the source extent the file records (as ntc_decode writes).
 
-    python -m neural_block_textures_amd.decode model.bin out_prefix [--repeat 50]
+    python -m neural_block_textures_amd.decode model.bin|model.ntcb out_prefix [--repeat 50]
 
 The decode is the trainer's: the latent levels (a DCT-coded level 0 reconstructed from its symbols on
-the device), the MLP, and save_png's rounding, all on the device; W x H x 3T bytes cross PCIe. With
---repeat the decode is timed (HIP events around the decode and pack kernels) and reported in
+the device), the MLP, and save_png's rounding, all on the device; W x H x 3T bytes cross PCIe. A
+container's grid and palette levels are dequantized on the host as its readers do (strict float32).
+With --repeat the decode is timed (HIP events around the decode and pack kernels) and reported in
 Mtexel/s, the unit of the reference's ntc_decode timings.
 """
 from __future__ import annotations
@@ -18,7 +20,7 @@ import zlib
 
 import numpy as np
 
-from . import dct_host, model_file
+from . import dct_host, model_file, ntcb
 from .trainer import DctDesc, Trainer
 
 
@@ -59,19 +61,30 @@ def trainer_for(m: model_file.ModelFile) -> Trainer:
     return tr
 
 
+def load(path: str) -> model_file.ModelFile:
+    """a model file or a container (told apart by the magic), as the model the decode needs"""
+    with open(path, "rb") as f:
+        head = f.read(4)
+    if len(head) == 4 and struct.unpack("<I", head)[0] == ntcb.MAGIC:
+        return ntcb.read(path).to_model_file()
+    return model_file.read(path)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("model")
     ap.add_argument("out_prefix", nargs="?", default="")
     ap.add_argument("--repeat", type=int, default=0, help="time this many decodes and report Mtexel/s")
     a = ap.parse_args(argv)
-    m = model_file.read(a.model)
+    m = load(a.model)
     lay = m.layout
     tr = trainer_for(m)
     rgb = tr.decode_rgb8().reshape(lay.H, lay.W, lay.nout)
+    sw, sh = (m.size[2], m.size[3]) if m.size[2] > 0 else (lay.W, lay.H)
     if a.out_prefix:
         for t in range(lay.T):
-            write_png(f"{a.out_prefix}_t{t}.png", rgb[:, :, 3 * t:3 * t + 3])
+            name = f"{a.out_prefix}.png" if lay.T == 1 else f"{a.out_prefix}_t{t}.png"
+            write_png(name, np.ascontiguousarray(rgb[:sh, :sw, 3 * t:3 * t + 3]))
     if a.repeat > 0:
         tr.synchronize()
         tr.set_profiling(True)
