@@ -111,8 +111,9 @@ public:
     void dct_probe(uint8_t* code, float* gain);
     // Decoder::dct_refit on the device (main.cpp:1672-1680): probe, replace the codes, re-snap level 0.
     void dct_refit(uint8_t* code);
-    // mse_of (main.cpp:1764-1788) of the device's decode: per-texture and weighted 8-bit MSE over ew x eh.
-    void decode_error(int ew, int eh, double* tex_mse, double* weighted);
+    // mse_of (main.cpp:1764-1788) of the device's decode of its decode buffer, or of z_host (nz floats)
+    // as decode_full: per-texture and weighted 8-bit MSE over ew x eh.
+    void decode_error(const float* z_host, int ew, int eh, double* tex_mse, double* weighted);
     // The decode rounded to 8 bits as save_png writes it: W * H * nout bytes.
     void decode_rgb8(uint8_t* out);
 

@@ -102,11 +102,13 @@ void ntc_trainer_dct_probe(ntc_trainer* t, uint8_t* code, float* gain);
  * reference's download + host refit + set_dct (main.cpp:4110-4120). Requires a prior set_dct. */
 void ntc_trainer_dct_refit(ntc_trainer* t, uint8_t* code);
 /* The printed error of the current model (mse_of, main.cpp:1764-1788) without a download: the decode
- * buffer decoded on the device, both images rounded to 8 bits as save_png does, squared differences
- * summed exactly per texture over the extent ew x eh (0 = the whole image). tex_mse[T] = SSE_t / (3 ew eh),
- * *weighted = sum_t w_t SSE_t / (3 wsum ew eh), with w_t = cw[3 t]. No counterpart in the reference's
- * backend (its print path downloads the model and decodes on the host, main.cpp:4155-4160). */
-void ntc_trainer_decode_error(ntc_trainer* t, int ew, int eh, double* tex_mse, double* weighted);
+ * buffer - or z_host (nz floats, as decode_full; the post-hoc quantized latent of the print path's
+ * second figure, main.cpp:4172-4174) - decoded on the device, both images rounded to 8 bits as save_png
+ * does, squared differences summed exactly per texture over the extent ew x eh (0 = the whole image).
+ * tex_mse[T] = SSE_t / (3 ew eh), *weighted = sum_t w_t SSE_t / (3 wsum ew eh), with w_t = cw[3 t].
+ * No counterpart in the reference's backend (its print path downloads the model and decodes on the
+ * host, main.cpp:4155-4174). */
+void ntc_trainer_decode_error(ntc_trainer* t, const float* z_host, int ew, int eh, double* tex_mse, double* weighted);
 /* The decode of the current model rounded to 8 bits as the reference's save_png and ntc_decode write it
  * (lround of the [0, 1]-clamped value times 255): W*H*nout bytes, interleaved per pixel. No counterpart in
  * the reference's backend (its decoder is the host program ntc_decode.cpp). */

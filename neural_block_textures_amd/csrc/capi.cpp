@@ -84,8 +84,8 @@ void ntc_trainer_download_dct_rate(ntc_trainer* t, int32_t* bits, int32_t* dbits
 void ntc_trainer_dct_probe(ntc_trainer* t, uint8_t* code, float* gain) { t->t.dct_probe(code, gain); }
 void ntc_trainer_dct_refit(ntc_trainer* t, uint8_t* code) { t->t.dct_refit(code); }
 void ntc_trainer_decode_rgb8(ntc_trainer* t, uint8_t* out) { t->t.decode_rgb8(out); }
-void ntc_trainer_decode_error(ntc_trainer* t, int ew, int eh, double* tex_mse, double* weighted) {
-    t->t.decode_error(ew, eh, tex_mse, weighted);
+void ntc_trainer_decode_error(ntc_trainer* t, const float* z_host, int ew, int eh, double* tex_mse, double* weighted) {
+    t->t.decode_error(z_host, ew, eh, tex_mse, weighted);
 }
 
 void ntc_trainer_mlp_step(ntc_trainer* t, int it, float sigma, float lr, int N, int M) { t->t.mlp_step(it, sigma, lr, N, M); }

@@ -105,15 +105,21 @@ void dct_refit_impl(Impl& I, uint8_t* code) {
 }
 
 // The print path's error figures without a download (mse_of, main.cpp:1764-1788): decode the decode
-// buffer on the device, then the exact per-texture sums of squared 8-bit differences.
-void decode_error_impl(Impl& I, int ew, int eh, double* tex_mse, double* weighted) {
+// buffer - or, as decode_full, a latent the host passes (the post-hoc quantized one of bitrate_stats,
+// main.cpp:4172-4174) - on the device, then the exact per-texture sums of squared 8-bit differences.
+void decode_error_impl(Impl& I, const float* z_host, int ew, int eh, double* tex_mse, double* weighted) {
     if (I.d.nout % 3 != 0) die("decode_error needs RGB textures (nout a multiple of 3)");
     if (ew <= 0 || ew > I.d.W) ew = I.d.W;
     if (eh <= 0 || eh > I.d.H) eh = I.d.H;
     const size_t blocks = ((size_t)ew * eh + 255) / 256;
     unsigned long long* part = nullptr;
     NTC_CHECK(hipMalloc(&part, blocks * 4 * sizeof(unsigned long long)));
-    launch_decode(I, I.zdec);
+    const float* zsrc = I.zdec;
+    if (z_host) {
+        NTC_CHECK(hipMemcpyAsync(I.ztmp, z_host, I.nz * sizeof(float), hipMemcpyHostToDevice, I.stream));
+        zsrc = I.ztmp;
+    }
+    launch_decode(I, zsrc);
     launch_u8_sse(I, ew, eh, part);
     std::vector<unsigned long long> h(blocks * 4);
     NTC_CHECK(hipMemcpyAsync(h.data(), part, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost, I.stream));
@@ -562,7 +568,9 @@ void Trainer::decode_full(const float* z_host, float* img) {
 
 void Trainer::dct_probe(uint8_t* code, float* gain) { ntc_hip::dct_probe_impl(*im, code, gain); }
 void Trainer::dct_refit(uint8_t* code) { ntc_hip::dct_refit_impl(*im, code); }
-void Trainer::decode_error(int ew, int eh, double* tex_mse, double* weighted) { ntc_hip::decode_error_impl(*im, ew, eh, tex_mse, weighted); }
+void Trainer::decode_error(const float* z_host, int ew, int eh, double* tex_mse, double* weighted) {
+    ntc_hip::decode_error_impl(*im, z_host, ew, eh, tex_mse, weighted);
+}
 void Trainer::decode_rgb8(uint8_t* out) { ntc_hip::decode_rgb8_impl(*im, out); }
 
 void Trainer::debug_last_batch(std::vector<int>& bidx) const {

@@ -177,7 +177,7 @@ void launch_pack_u8(Impl& I, uint8_t* out);
 // decode the decode buffer and download it as 8-bit values
 void decode_rgb8_impl(Impl& I, uint8_t* out);
 // decode the decode buffer on the device and return mse_of's per-texture and weighted figures
-void decode_error_impl(Impl& I, int ew, int eh, double* tex_mse, double* weighted);
+void decode_error_impl(Impl& I, const float* z_host, int ew, int eh, double* tex_mse, double* weighted);
 void dct_probe_impl(Impl& I, uint8_t* code, float* gain);
 void dct_refit_impl(Impl& I, uint8_t* code);
 void launch_dct_rate_pairs(Impl& I, int K, float sigma);

@@ -104,7 +104,7 @@ def library() -> C.CDLL:
             "ntc_trainer_on_matrix_cores": (C.c_int, [P, C.c_char_p]),
             "ntc_trainer_dct_probe": (None, [P, P, P]),
             "ntc_trainer_dct_refit": (None, [P, P]),
-            "ntc_trainer_decode_error": (None, [P, C.c_int, C.c_int, P, P]),
+            "ntc_trainer_decode_error": (None, [P, P, C.c_int, C.c_int, P, P]),
             "ntc_trainer_decode_rgb8": (None, [P, P]),
             "ntc_trainer_debug_gauss": (None, [P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, C.c_size_t, P]),
             "ntc_trainer_debug_noise_factors": (None, [P, C.c_uint32, C.c_size_t, P, P]),
@@ -324,12 +324,14 @@ class Trainer:
         self._lib.ntc_trainer_decode_rgb8(self._h, out.ctypes.data)
         return out
 
-    def decode_error(self, ew=0, eh=0):
-        """mse_of of the device's decode: (per-texture 8-bit MSE, weighted MSE)"""
+    def decode_error(self, ew=0, eh=0, z=None):
+        """mse_of of the device's decode (of its decode buffer, or of the host latent z):
+        (per-texture 8-bit MSE, weighted MSE)"""
         T = max(1, self.layout.nout // 3) if self.layout else 4
         tex = np.zeros(4, np.float64)
         wt = C.c_double()
-        self._lib.ntc_trainer_decode_error(self._h, ew, eh, tex.ctypes.data, C.addressof(wt))
+        zh = None if z is None else _f32(z, self.nz)
+        self._lib.ntc_trainer_decode_error(self._h, _ptr(zh), ew, eh, tex.ctypes.data, C.addressof(wt))
         return tex[:T], wt.value
 
     # ---- steps
