@@ -1,5 +1,6 @@
 // The correction bits of the device's Gaussian draw, built on the host from its own C library and
-// copied to each device once per process (2 x 2 MiB, kept until the process ends).
+// copied to each device once per process (2 x 2 MiB and their 2 x 128 KiB summaries, one allocation
+// kept until the process ends).
 //
 // For every argument k of each Box-Muller factor the host compares its C library's logf / cosf
 // with the rounded double value of noise_math.hpp; where they differ it checks that the library's
@@ -22,6 +23,17 @@ namespace ntc_hip {
 namespace {
 std::mutex g_mutex;
 std::map<int, NoiseFix> g_fix;
+}
+
+// bit j of the summary = any of the arguments 16 j .. 16 j + 15 has its bit set (half a word of fix)
+std::vector<uint32_t> noise_fix_summary(const std::vector<uint32_t>& fix) {
+    std::vector<uint32_t> any((fix.size() * 2 + 31) / 32, 0u);
+    for (size_t w = 0; w < fix.size(); w++)
+        for (size_t h = 0; h < 2; h++) {
+            const size_t j = 2 * w + h;
+            if ((fix[w] >> (16 * h)) & 0xFFFFu) any[j >> 5] |= 1u << (j & 31);
+        }
+    return any;
 }
 
 bool noise_fix_for_device(int device, NoiseFix& out, std::string& why) {
@@ -65,12 +77,17 @@ bool noise_fix_for_device(int device, NoiseFix& out, std::string& why) {
         why = buf;
         return false;
     }
-    uint32_t *l = nullptr, *c = nullptr;
-    NTC_CHECK(hipMalloc(&l, (size_t)words * sizeof(uint32_t)));
-    NTC_CHECK(hipMalloc(&c, (size_t)words * sizeof(uint32_t)));
+    const std::vector<uint32_t> lany = noise_fix_summary(lfix), cany = noise_fix_summary(cfix);
+    const uint32_t swords = (uint32_t)lany.size();
+    uint32_t* buf = nullptr;
+    const size_t total = 2 * (size_t)words + 2 * (size_t)swords;
+    NTC_CHECK(hipMalloc(&buf, total * sizeof(uint32_t)));
+    uint32_t *l = buf, *c = buf + words, *la = buf + 2 * (size_t)words, *ca = la + swords;
     NTC_CHECK(hipMemcpy(l, lfix.data(), (size_t)words * sizeof(uint32_t), hipMemcpyHostToDevice));
     NTC_CHECK(hipMemcpy(c, cfix.data(), (size_t)words * sizeof(uint32_t), hipMemcpyHostToDevice));
-    out = NoiseFix{ l, c };
+    NTC_CHECK(hipMemcpy(la, lany.data(), (size_t)swords * sizeof(uint32_t), hipMemcpyHostToDevice));
+    NTC_CHECK(hipMemcpy(ca, cany.data(), (size_t)swords * sizeof(uint32_t), hipMemcpyHostToDevice));
+    out = NoiseFix{ l, c, la, ca };
     g_fix[device] = out;
     return true;
 }

@@ -129,6 +129,7 @@ inline int blocks_for(size_t n, int tpb) { return (int)((n + tpb - 1) / tpb); }
 // the device's noise correction bits (built once per device); false with a reason if the host's
 // C library cannot be reproduced
 bool noise_fix_for_device(int device, NoiseFix& out, std::string& why);
+std::vector<uint32_t> noise_fix_summary(const std::vector<uint32_t>& fix);
 
 // kernels_mlp.hip
 void launch_fill(Impl& I, float* p, size_t n, float v);
