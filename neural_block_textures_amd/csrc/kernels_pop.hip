@@ -195,14 +195,15 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
 }
 
 // The latent pair evaluation (LatentTrainer::step_impl, main.cpp:1990-2007) on the matrix cores:
-// block (512 or 256 pixels, pair k). Phase 1: the threads build the features of each pixel with the
-// pair's texels perturbed by +sg eps and by -sg eps (features_pm: both members from one set of
-// taps and texel loads) into LDS.
-// Phase 2: each wave evaluates a quarter of the pixels in 16-pixel tiles, the + and - members of
-// a tile together; each pixel's error is decode_err's float sum of cw (d d) over its channels (a
-// lane's four in ascending order, then the lane groups pairwise: the float sum is within a few ulp
-// of the reference's ascending chain), and dpix = (e+ - e-) * inv_px.
-// pixels per block: 512, or 256 for wide inputs (LDS)
+// block (512 or 256 pixels, pair k), each wave a quarter of them in rounds of 64. In a round every
+// lane builds the features of its own pixel with the pair's texels perturbed by +sg eps and by
+// -sg eps (features_pm: both members from one set of taps and texel loads), and four transposes
+// across the lane groups (tiles_of) turn the 64 pixels into the B operands of four 16-pixel tiles:
+// no shared memory and no barrier, so a wave's feature loads overlap other waves' matrix work. Each
+// tile's + and - members are evaluated together; a pixel's error is decode_err's float sum of
+// cw (d d) over its channels (a lane's four in ascending order, then the lane groups pairwise: within
+// a few ulp of the reference's ascending chain), and dpix = (e+ - e-) * inv_px.
+// pixels per block: 512, or 256 for wide inputs
 template <class S>
 constexpr int lat_pix() { return MfmaShape<S>::kIn <= 8 ? 512 : 256; }
 
@@ -212,29 +213,20 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
                                                       const float* __restrict__ eps, const float* __restrict__ tgt, float sg,
                                                       unsigned mask, float* __restrict__ dpix) {
     using Q = MfmaShape<S>;
-    constexpr int NIN = Q::kIn, NO = Q::kNout, kLatPix = lat_pix<S>(), LDW = kLatPix + 4;
-    __shared__ float F[2][NIN][LDW];
-    const int k = blockIdx.y, p0 = blockIdx.x * kLatPix;
-    const float* e = eps + (size_t)k * m.nz;
-    for (int q = threadIdx.x; q < kLatPix; q += 256) {
-        const int p = min(p0 + q, m.npix - 1);
-        float fp[S::kMaxIn], fm[S::kMaxIn];
-        features_pm<S>(m, zdec, e, sg, mask, p % m.W, p / m.W, fp, fm);
-#pragma unroll
-        for (int i = 0; i < NIN; i++) { F[0][i][q] = fp[i]; F[1][i][q] = fm[i]; }
-    }
-    __syncthreads();
+    constexpr int NO = Q::kNout, kLatPix = lat_pix<S>(), kRounds = kLatPix / 256;
+    const int k = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
+    const float* e = eps + (size_t)k * m.nz;
+    float* out = dpix + (size_t)k * m.npix;
     MfmaWeights<S> W;
     mfma_load<S, false>(W, w, lane);
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     float cw[4];
     lane_cw<NO>(m.cw, g, cw);
-    float* out = dpix + (size_t)k * m.npix;
-    // the targets of a tile: lane (g, j) reads channels 4 g .. 4 g + 3 of pixel j (one 16-byte load
-    // when a pixel's row is a whole number of float4; rows past the last channel are clamped)
-    auto load_t = [&](int u, float (&t)[4]) {
-        const int pr = min(p0 + (kLatPix / 4) * wave + 16 * u + i16, m.npix - 1);
+    // the targets of the tile at pixel t0: lane (g, j) reads channels 4 g .. 4 g + 3 of pixel t0 + j (one
+    // 16-byte load when a pixel's row is a whole number of float4; rows past the last are clamped)
+    auto load_t = [&](int t0, float (&t)[4]) {
+        const int pr = min(t0 + i16, m.npix - 1);
         if constexpr (NO % 4 == 0) {
             const f4v v = *reinterpret_cast<const f4v*>(tgt + (size_t)pr * NO + min(4 * g, NO - 4));
 #pragma unroll
@@ -244,59 +236,65 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
             for (int r = 0; r < 4; r++) t[r] = tgt[(size_t)pr * NO + min(4 * g + r, NO - 1)];
         }
     };
-    float tn[4];
-    load_t(0, tn);
-    for (int u = 0; u < kLatPix / 64; u++) {   // kLatPix / 64 tiles of 16 pixels per wave
-        const int col = (kLatPix / 4) * wave + 16 * u + i16;
-        const int p = p0 + col;
-        float t[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) t[r] = tn[r];
-        if (u + 1 < kLatPix / 64) load_t(u + 1, tn);
-        float b1[2][Q::kKs1];
-#pragma unroll
-        for (int s2 = 0; s2 < 2; s2++)
-#pragma unroll
-            for (int ks = 0; ks < Q::kKs1; ks++) {
-                const int kk = 4 * ks + g;
-                const float v = F[s2][min(kk, NIN - 1)][col];
-                b1[s2][ks] = kk < NIN ? v : 0.0f;
-            }
-        f4v o[2];
-        mfma_forward<S, 2, LeakUnit, false>(W, b1, m.leak, o);
-        // each lane's four channel terms cw (d d) in ascending order, then the four lane groups
-        // added pairwise (permlane swaps): e+ in lanes 0-31, e- in lanes 32-63, then e+ - e-
-        float ep = 0.0f, em = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float dp = out_of<S>(o[0][r], Clamp) - t[r], dm = out_of<S>(o[1][r], Clamp) - t[r];
-            ep = __builtin_fmaf(cw[r], __fmul_rn(dp, dp), ep);
-            em = __builtin_fmaf(cw[r], __fmul_rn(dm, dm), em);
+    for (int rd = 0; rd < kRounds; rd++) {
+        const int base = blockIdx.x * kLatPix + (kLatPix / 4) * wave + 64 * rd;   // tile t: pixels base + 16 t + j
+        float tn[4];
+        load_t(base, tn);
+        float bp[4][Q::kKs1], bm[4][Q::kKs1];
+        {
+            const int pr = min(base + lane, m.npix - 1);
+            float fp[S::kMaxIn], fm[S::kMaxIn];
+            features_pm<S>(m, zdec, e, sg, mask, pr % m.W, pr / m.W, fp, fm);
+            tiles_of<S>(fp, bp);
+            tiles_of<S>(fm, bm);
         }
-        const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(ep), __float_as_uint(em), false, false);
-        const float s = __uint_as_float(h[0]) + __uint_as_float(h[1]);   // groups 0 + 2 and 1 + 3
-        const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
-        const float c = __uint_as_float(q[0]) + __uint_as_float(q[1]);   // lanes 0-31: e+, 32-63: e-
-        const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);
-        if (g == 0 && p < m.npix) out[p] = __fmul_rn(__uint_as_float(x[0]) - __uint_as_float(x[1]), m.inv_px);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            float tt[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) tt[r] = tn[r];
+            if (t + 1 < 4) load_t(base + 16 * (t + 1), tn);
+            float b1[2][Q::kKs1];
+#pragma unroll
+            for (int ks = 0; ks < Q::kKs1; ks++) { b1[0][ks] = bp[t][ks]; b1[1][ks] = bm[t][ks]; }
+            f4v o[2];
+            mfma_forward<S, 2, LeakUnit, false>(W, b1, m.leak, o);
+            // each lane's four channel terms cw (d d) in ascending order, then the four lane groups
+            // added pairwise (permlane swaps): e+ in lanes 0-31, e- in lanes 32-63, then e+ - e-
+            float ep = 0.0f, em = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float dp = out_of<S>(o[0][r], Clamp) - tt[r], dm = out_of<S>(o[1][r], Clamp) - tt[r];
+                ep = __builtin_fmaf(cw[r], __fmul_rn(dp, dp), ep);
+                em = __builtin_fmaf(cw[r], __fmul_rn(dm, dm), em);
+            }
+            const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(ep), __float_as_uint(em), false, false);
+            const float s = __uint_as_float(h[0]) + __uint_as_float(h[1]);   // groups 0 + 2 and 1 + 3
+            const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+            const float c = __uint_as_float(q[0]) + __uint_as_float(q[1]);   // lanes 0-31: e+, 32-63: e-
+            const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+            const int p = base + 16 * t + i16;
+            if (g == 0 && p < m.npix) out[p] = __fmul_rn(__uint_as_float(x[0]) - __uint_as_float(x[1]), m.inv_px);
+        }
     }
 }
 
 // The selector search (qat_search, main.cpp:2088-2139) on the matrix cores, for a nearest level 0
-// of the image's size (each texel's cell is its own pixel): wave = 64 pixels in four 16-pixel tiles. Every lane builds its pixel's
-// features (features<S>); per channel, every candidate value is one MLP evaluation of the tile with
-// that feature replaced (two candidates at a time), the pixel's loss the double sum of the float
-// terms of loss_subset over its channels (a lane's four in ascending order, then the pixel's four
-// lanes pairwise, the same value in each of them). The choice is the
-// reference's: the current grid value first, then every other value with strict <, so the first
-// strictly smaller loss wins (main.cpp:2101-2132). The winner enters the features of the next channel
-// and is written to the decode buffer.
+// of the image's size (each texel's cell is its own pixel): wave = 64 pixels in four 16-pixel tiles.
+// Every lane builds the features of its own pixel (features<S>) and tiles_of turns them into the four
+// tiles' B operands. Per channel and tile, every candidate value is one MLP evaluation of the tile with
+// that feature replaced (two candidates at a time), the pixel's loss the double sum of the float terms
+// of loss_subset over its channels (a lane's four in ascending order, then the pixel's four lanes
+// pairwise, the same value in each of them). The choice is the reference's: the current grid value
+// first, then every other value with strict <, so the first strictly smaller loss wins
+// (main.cpp:2101-2132). The winner enters the features of the next channel and is written to the
+// decode buffer.
 template <class S>
 __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __restrict__ w, float* __restrict__ zdec,
                                                  const float* __restrict__ tgt, const int* __restrict__ qat_bits,
                                                  const float* __restrict__ grid) {
     using Q = MfmaShape<S>;
-    constexpr int NIN = Q::kIn, NO = Q::kNout, C0 = S::kC0;
+    constexpr int NO = Q::kNout, C0 = S::kC0;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
     MfmaWeights<S> W;
     mfma_load<S, false>(W, w, lane);
@@ -304,27 +302,30 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
     float cw[4];
     lane_cw<NO>(m.cw, g, cw);
     const bool unit_leak = m.leak >= 0.0f && m.leak <= 1.0f;
-    for (int u = 0; u < 4; u++) {
-        const int p = blockIdx.x * 256 + wave * 64 + u * 16 + i16;
-        const int pr = min(p, m.npix - 1);
-        float f[S::kMaxIn];
+    const int base = blockIdx.x * 256 + wave * 64;   // tile t: pixels base + 16 t + j
+    float f[S::kMaxIn];
+    {
+        const int pr = min(base + lane, m.npix - 1);
         features<S>(m, PlainLatent{ zdec }, pr % m.W, pr / m.W, f);
-        float t[4];
+    }
+    float b[4][Q::kKs1];
+    tiles_of<S>(f, b);
+    float t4[4][4];   // targets: lane (g, j) holds channels 4 g .. 4 g + 3 of pixel j of each tile
 #pragma unroll
-        for (int r = 0; r < 4; r++) t[r] = tgt[(size_t)pr * NO + min(4 * g + r, NO - 1)];
+    for (int t = 0; t < 4; t++) {
+        const int pr = min(base + 16 * t + i16, m.npix - 1);
 #pragma unroll
-        for (int c = 0; c < C0; c++) {
-            const int bits = qat_bits[c], levels = (1 << bits) - 1;
-            const float* gv = grid + bits * 257;
-            const int cur = qat_index(f[c], bits);
-            float b1[1][Q::kKs1];
+        for (int r = 0; r < 4; r++) t4[t][r] = tgt[(size_t)pr * NO + min(4 * g + r, NO - 1)];
+    }
 #pragma unroll
-            for (int ks = 0; ks < Q::kKs1; ks++) {
-                float v = 0.0f;
+    for (int c = 0; c < C0; c++) {
+        const int bits = qat_bits[c], levels = (1 << bits) - 1;
+        const float* gv = grid + bits * 257;
+        // this channel's current value of every pixel, from the lane that built the pixel's features
+        const int cur_own = qat_index(f[c], bits);
 #pragma unroll
-                for (int q = 0; q < 4; q++) if (4 * ks + q < NIN && g == q) v = f[4 * ks + q];
-                b1[0][ks] = v;
-            }
+        for (int t = 0; t < 4; t++) {
+            const int cur = __builtin_amdgcn_ds_bpermute((16 * t + i16) << 2, cur_own);
             double cur_l = 0.0, best_l = 0.0;
             int best_k = -1;
             for (int kc = 0; kc <= levels; kc += 2) {   // 2^bits candidates: two tiles at a time
@@ -332,7 +333,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
 #pragma unroll
                 for (int v = 0; v < 2; v++)
 #pragma unroll
-                    for (int ks = 0; ks < Q::kKs1; ks++) b2[v][ks] = b1[0][ks];
+                    for (int ks = 0; ks < Q::kKs1; ks++) b2[v][ks] = b[t][ks];
                 if (g == c % 4) { b2[0][c / 4] = gv[kc]; b2[1][c / 4] = gv[kc + 1]; }
                 f4v o[2];
                 if (unit_leak) mfma_forward<S, 2, true, false>(W, b2, m.leak, o);
@@ -342,7 +343,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                     double l = 0.0;   // this lane's channels in ascending order, then the pixel's lanes
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        const float d = out_of<S>(o[v][r], m.clamp_out != 0) - t[r];
+                        const float d = out_of<S>(o[v][r], m.clamp_out != 0) - t4[t][r];
                         l += (double)__fmul_rn(cw[r], __fmul_rn(d, d));
                     }
                     l = group_sum_d(l);
@@ -351,8 +352,9 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                 }
             }
             const int win = (best_k >= 0 && best_l < cur_l) ? best_k : cur;
-            f[c] = gv[win];
-            if (g == 0 && p < m.npix) zdec[m.lv[0].off + (size_t)p * m.lv[0].C + c] = f[c];
+            if (g == c % 4) b[t][c / 4] = gv[win];
+            const int p = base + 16 * t + i16;
+            if (g == 0 && p < m.npix) zdec[m.lv[0].off + (size_t)p * m.lv[0].C + c] = gv[win];
         }
     }
 }

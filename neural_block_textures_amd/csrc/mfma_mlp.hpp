@@ -127,6 +127,25 @@ __device__ __forceinline__ void transpose4(const f4v& v, float* y) {
     y[2] = __uint_as_float(t23[0]); y[3] = __uint_as_float(t23[1]);
 }
 
+// Lane (t, j) holds the features f of pixel j of tile t (t = its lane group: a wave's 64 lanes build
+// the features of 64 different pixels). The first layer's B operands of the four tiles: b[t][ks] in
+// lane (g, j) = feature 4 ks + g of pixel j of tile t (zero past nin), one 4 x 4 transpose across
+// the lane groups per k-step.
+template <class S>
+__device__ __forceinline__ void tiles_of(const float (&f)[S::kMaxIn], float (&b)[4][MfmaShape<S>::kKs1]) {
+    using Q = MfmaShape<S>;
+#pragma unroll
+    for (int ks = 0; ks < Q::kKs1; ks++) {
+        f4v v;
+#pragma unroll
+        for (int r = 0; r < 4; r++) v[r] = 4 * ks + r < Q::kIn ? f[4 * ks + r] : 0.0f;
+        float y[4];
+        transpose4(v, y);
+#pragma unroll
+        for (int t = 0; t < 4; t++) b[t][ks] = y[t];
+    }
+}
+
 // The activation of main.cpp:560, x > 0 ? x : leak x. For 0 <= leak <= 1 this is max(x, leak x)
 // bit for bit (also for signed zeros and NaN), one instruction fewer.
 template <bool LeakUnit>
