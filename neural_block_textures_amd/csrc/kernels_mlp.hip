@@ -107,15 +107,16 @@ __global__ void __launch_bounds__(kTPB) k_pop_eval(DevModel m, const float* __re
 }
 
 // Per pair: member losses = chunk sums in chunk order / norm; dl = l+ - l-, lsum = (l+ + l-) / 2.
-__global__ void __launch_bounds__(kTPB) k_es_finish(const double* __restrict__ part, int chunks, int N, double norm,
-                                                   double* __restrict__ dl, double* __restrict__ lsum) {
-    const int i = blockIdx.x * kTPB + threadIdx.x;
-    if (i >= N) return;
-    double lp = 0.0, lm = 0.0;
-    for (int j = 0; j < chunks; j++) { lp += part[(size_t)(2 * i) * chunks + j]; lm += part[(size_t)(2 * i + 1) * chunks + j]; }
-    lp /= norm; lm /= norm;
-    dl[i] = lp - lm;
-    lsum[i] = 0.5 * (lp + lm);
+// Adam::step (main.cpp:1793-1810) on parameter i given its gradient; c1, c2 from the host's powf
+__device__ __forceinline__ void adam_at(float* __restrict__ theta, float* __restrict__ m, float* __restrict__ v, size_t i, float gi,
+                                        float lr, float c1, float c2) {
+    const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+    const float ob1 = 1.0f - b1, ob2 = 1.0f - b2;
+    const float mi = __builtin_fmaf(b1, m[i], __fmul_rn(ob1, gi));
+    const float vi = __builtin_fmaf(b2, v[i], __fmul_rn(__fmul_rn(ob2, gi), gi));
+    m[i] = mi; v[i] = vi;
+    const float mh = mi / c1, vh = vi / c2;
+    theta[i] = theta[i] - (lr * mh) / (__builtin_sqrtf(vh) + eps);
 }
 
 // ES update direction (main.cpp:1868-1873): g[k] = sum over pairs of ((float)dl_i * scale) * eps_ik, one
@@ -123,23 +124,41 @@ __global__ void __launch_bounds__(kTPB) k_es_finish(const double* __restrict__ p
 // leaves only P threads for N * P reads; here block (weight tile, segment) runs four chains of kChain
 // pairs, one per wave, and the chains are added in a fixed order (waves, then segments), so the sum is
 // deterministic and differs from the single chain only in rounding.
+// Each wave first finishes its chain's pair losses from the population partials (lane q: pair i0 + q,
+// the member's chunk sums added in ascending order, divided by the loss norm): dl_i = l+ - l-, and the
+// blocks of weight tile 0 store dl and the pair means for the statistics.
 constexpr int kChain = 32;
-__global__ void __launch_bounds__(kTPB) k_es_grad_part(int N, int P, float scale, const double* __restrict__ dl,
+__global__ void __launch_bounds__(kTPB) k_es_grad_part(int N, int P, float scale, const double* __restrict__ lpart, int chunks,
+                                                      double norm, double* __restrict__ dl, double* __restrict__ lsum,
                                                       const float* __restrict__ eps, float* __restrict__ part) {
     __shared__ float lds[kTPB / 64][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int k = blockIdx.x * 64 + lane;
     const int i0 = (blockIdx.y * (kTPB / 64) + wave) * kChain, i1 = min(N, i0 + kChain);
+    float wl = 0.0f;   // lane q: ((float)dl_{i0 + q}) * scale
+    if (i0 + lane < i1) {
+        const int i = i0 + lane;
+        double lp = 0.0, lm = 0.0;
+        for (int j = 0; j < chunks; j++) { lp += lpart[(size_t)(2 * i) * chunks + j]; lm += lpart[(size_t)(2 * i + 1) * chunks + j]; }
+        lp /= norm; lm /= norm;
+        const double d = lp - lm;
+        if (blockIdx.x == 0) { dl[i] = d; lsum[i] = 0.5 * (lp + lm); }
+        wl = __fmul_rn((float)d, scale);
+    }
     float g = 0.0f;
     if (k < P) {
         if (i1 - i0 == kChain) {   // a full chain: loads issued ahead of the dependent fma chain
             float w[kChain], e[kChain];
 #pragma unroll
-            for (int q = 0; q < kChain; q++) { w[q] = __fmul_rn((float)dl[i0 + q], scale); e[q] = eps[(size_t)(i0 + q) * P + k]; }
+            for (int q = 0; q < kChain; q++) {
+                w[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), q));
+                e[q] = eps[(size_t)(i0 + q) * P + k];
+            }
 #pragma unroll
             for (int q = 0; q < kChain; q++) g = __builtin_fmaf(w[q], e[q], g);
         } else {
-            for (int i = i0; i < i1; i++) g = __builtin_fmaf(__fmul_rn((float)dl[i], scale), eps[(size_t)i * P + k], g);
+            for (int i = i0; i < i1; i++)
+                g = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), i - i0)), eps[(size_t)i * P + k], g);
         }
     }
     lds[wave][lane] = g;
@@ -151,13 +170,17 @@ __global__ void __launch_bounds__(kTPB) k_es_grad_part(int N, int P, float scale
         part[(size_t)blockIdx.y * P + k] = s;
     }
 }
-__global__ void __launch_bounds__(kTPB) k_es_grad_final(int P, int segs, const float* __restrict__ part, float* __restrict__ grad) {
+// the segments added in order, then Adam on the weight
+__global__ void __launch_bounds__(kTPB) k_es_grad_final(int P, int segs, const float* __restrict__ part, float* __restrict__ grad,
+                                                       float* __restrict__ theta, float* __restrict__ m, float* __restrict__ v, float lr,
+                                                       float c1, float c2) {
     const int k = blockIdx.x * kTPB + threadIdx.x;
     if (k >= P) return;
     float g = part[k];
 #pragma unroll 8
     for (int s = 1; s < segs; s++) g += part[(size_t)s * P + k];
     grad[k] = g;
+    adam_at(theta, m, v, (size_t)k, g, lr, c1, c2);
 }
 
 // Central differences: dl_j = L(w_j + h) - L(w_j - h), g_j = dl_j / hh_j; pair P gives L(w).
@@ -181,14 +204,7 @@ __global__ void __launch_bounds__(kTPB) k_adam(float* __restrict__ theta, const 
                                               float* __restrict__ v, size_t n, float lr, float c1, float c2) {
     const size_t i = (size_t)blockIdx.x * kTPB + threadIdx.x;
     if (i >= n) return;
-    const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
-    const float ob1 = 1.0f - b1, ob2 = 1.0f - b2;
-    const float gi = g[i];
-    const float mi = __builtin_fmaf(b1, m[i], __fmul_rn(ob1, gi));
-    const float vi = __builtin_fmaf(b2, v[i], __fmul_rn(__fmul_rn(ob2, gi), gi));
-    m[i] = mi; v[i] = vi;
-    const float mh = mi / c1, vh = vi / c2;
-    theta[i] = theta[i] - (lr * mh) / (__builtin_sqrtf(vh) + eps);
+    adam_at(theta, m, v, i, g[i], lr, c1, c2);
 }
 
 // Full decode (Decoder::decode_full): one pixel per thread.
@@ -314,13 +330,10 @@ void launch_pop_eval_valu(Impl& I, int pairs, int M, int chunk, int chunks) {
     NTC_CHECK(hipGetLastError());
 }
 
-void launch_es_finish(Impl& I, int chunks, int N, double norm) {
-    hipLaunchKernelGGL(k_es_finish, dim3(blocks_for(N, kTPB)), dim3(kTPB), 0, I.stream, I.part, chunks, N, norm, I.dl, I.lsum);
-    NTC_CHECK(hipGetLastError());
-}
-
-void launch_es_grad(Impl& I, int /*it*/, float sigma, int N) {
+// The pair losses, the update direction and the Adam step of an ES step (main.cpp:1862-1874)
+void launch_es_update(Impl& I, int chunks, double norm, float sigma, int N, float lr, int t) {
     const float scale = 1.0f / (2.0f * (float)N * sigma);
+    const float c1 = 1.0f - powf(0.9f, (float)t), c2 = 1.0f - powf(0.999f, (float)t);
     const int per_block = kChain * (kTPB / 64);
     const int segs = (N + per_block - 1) / per_block;
     if ((size_t)segs * I.P > I.gpart_cap) {   // sized at init for max_pairs; N never exceeds it
@@ -329,10 +342,11 @@ void launch_es_grad(Impl& I, int /*it*/, float sigma, int N) {
     }
     ProfScope ps(I, "es_grad");
     float* part = I.gpart;
-    hipLaunchKernelGGL(k_es_grad_part, dim3(blocks_for(I.P, 64), segs), dim3(kTPB), 0, I.stream, N, I.P, scale, I.dl, I.eps_mlp,
-                       part);
+    hipLaunchKernelGGL(k_es_grad_part, dim3(blocks_for(I.P, 64), segs), dim3(kTPB), 0, I.stream, N, I.P, scale, I.part, chunks, norm,
+                       I.dl, I.lsum, I.eps_mlp, part);
     NTC_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(k_es_grad_final, dim3(blocks_for(I.P, kTPB)), dim3(kTPB), 0, I.stream, I.P, segs, part, I.wgrad);
+    hipLaunchKernelGGL(k_es_grad_final, dim3(blocks_for(I.P, kTPB)), dim3(kTPB), 0, I.stream, I.P, segs, part, I.wgrad, I.w, I.wm,
+                       I.wv, lr, c1, c2);
     NTC_CHECK(hipGetLastError());
 }
 

@@ -465,9 +465,7 @@ void Trainer::mlp_step(int it, float sigma, float lr, int N, int M) {
         launch_perturb(I, it, sigma, N);
         launch_pop_eval(I, N, M, chunk, chunks);
     }
-    launch_es_finish(I, chunks, N, 3.0 * (double)I.d.wsum * (double)M);
-    launch_es_grad(I, it, sigma, N);
-    launch_adam(I, I.w, I.wgrad, I.wm, I.wv, I.P, lr, ++I.mlp_t);
+    launch_es_update(I, chunks, 3.0 * (double)I.d.wsum * (double)M, sigma, N, lr, ++I.mlp_t);
     I.last_N = N; I.last_fd = false; I.last_M = M; I.last_chunk = chunk;
 }
 
@@ -528,11 +526,11 @@ void Trainer::lat_step(int /*it*/, float sigma, float lr, int K) {
     unsigned mask = 0;
     for (int l = 0; l < I.d.nlev; l++) if (!(qat && l == 0)) mask |= 1u << l;
     ensure_lat(I, K);
-    launch_fill(I, I.zgrad, I.nz, 0.0f);
     const bool rate = I.dct_live && I.dct_rate_es;
     I.dct_evals = rate ? I.ddct.n * K : 0;
+    if (!mask) launch_fill(I, I.zgrad, I.nz, 0.0f);
     if (mask) {
-        launch_lat_eps(I, K, mask);
+        launch_lat_eps(I, K, mask);   // also clears zgrad
         launch_lat_pair(I, K, sigma, mask);
         if (rate) { launch_dct_rate_pairs(I, K, sigma); I.dct_last_K = K; }
         const float scale = 1.0f / (2.0f * (float)K * sigma);

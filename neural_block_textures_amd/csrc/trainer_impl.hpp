@@ -147,8 +147,7 @@ void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks);
 // the ES step's population evaluation with the perturbation drawn in the kernel (matrix-core shapes); fills eps_mlp
 void launch_pop_eval_es(Impl& I, int it, float sigma, int N, int M, int chunk, int chunks);
 void launch_pop_eval_valu(Impl& I, int pairs, int M, int chunk, int chunks);
-void launch_es_finish(Impl& I, int chunks, int N, double norm);
-void launch_es_grad(Impl& I, int it, float sigma, int N);
+void launch_es_update(Impl& I, int chunks, double norm, float sigma, int N, float lr, int t);
 void launch_fd_finish(Impl& I, int chunks, double norm);
 void launch_adam(Impl& I, float* theta, const float* g, float* m, float* v, size_t n, float lr, int t);
 void launch_decode(Impl& I, const float* z);
@@ -158,7 +157,7 @@ void launch_debug_factors(Impl& I, uint32_t k0, size_t n, float* rad, float* cos
 void launch_copy_calibration(Impl& I, const float* src, float* dst, size_t n);
 
 // kernels_latent.hip
-void launch_lat_eps(Impl& I, int K, unsigned mask);
+void launch_lat_eps(Impl& I, int K, unsigned mask);   // also clears the latent gradient
 void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask);
 void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask);
 void launch_lat_gather(Impl& I, int level, int K, float scale, bool rate);
