@@ -270,6 +270,18 @@ __device__ __forceinline__ const float* uniform_ptr(const float* p) {
     return (const float*)(((uint64_t)hi << 32) | lo);
 }
 
+// Adam::step (main.cpp:1793-1810) on parameter i given its gradient; c1, c2 from the host's powf
+__device__ __forceinline__ void adam_at(float* __restrict__ theta, float* __restrict__ m, float* __restrict__ v, size_t i, float gi,
+                                        float lr, float c1, float c2) {
+    const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+    const float ob1 = 1.0f - b1, ob2 = 1.0f - b2;
+    const float mi = __builtin_fmaf(b1, m[i], __fmul_rn(ob1, gi));
+    const float vi = __builtin_fmaf(b2, v[i], __fmul_rn(__fmul_rn(ob2, gi), gi));
+    m[i] = mi; v[i] = vi;
+    const float mh = mi / c1, vh = vi / c2;
+    theta[i] = theta[i] - (lr * mh) / (__builtin_sqrtf(vh) + eps);
+}
+
 __device__ __forceinline__ float activate(float x, float leak) { return x > 0.0f ? x : leak * x; }   // main.cpp:560
 __device__ __forceinline__ float output_of(float s, int clamp_out) {                                  // main.cpp:624-625
     return clamp_out ? fminf(1.0f, fmaxf(0.0f, s + 0.5f)) : 1.0f / (1.0f + expf(-s));

@@ -62,12 +62,16 @@ __global__ void __launch_bounds__(kTPB) k_lat_pair(DevModel m, const float* __re
 // after pair. With the --dct-lambda rate term, level 0 also receives (rate_scale * dbits) * scale * eps
 // right after each pair's mse term. Block = 16 texels x 4 pairs: the 64 threads sum the footprints
 // of four pairs at once (each sum in raster order), then 16 threads apply the four pairs in order.
+// A texel's gradient is then final (one block owns it), so with `adam` the block also takes the
+// texel's Adam step (the latent ES step's update, main.cpp:2036-2037).
 constexpr int kGatherTex = 16, kGatherPairs = 4;
 __global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevModel m, int level, int K, float scale,
                                                                          const float* __restrict__ dpix,
                                                                          const float* __restrict__ eps, const int* __restrict__ ranges,
                                                                          int rate, float rate_scale, int dct_bw, int dct_n,
-                                                                         const int32_t* __restrict__ dbits, float* __restrict__ grad) {
+                                                                         const int32_t* __restrict__ dbits, float* __restrict__ grad,
+                                                                         int adam, float* __restrict__ z, float* __restrict__ zm,
+                                                                         float* __restrict__ zv, float lr, float c1, float c2) {
     __shared__ float dsum[kGatherPairs][kGatherTex];
     const DevLevel& L = m.lv[level];
     const int j = threadIdx.x % kGatherTex, q = threadIdx.x / kGatherTex;
@@ -103,6 +107,8 @@ __global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevMod
         }
         __syncthreads();
     }
+    if (adam && live && q == 0)
+        for (int c = 0; c < L.C; c++) adam_at(z, zm, zv, (size_t)(base + c), grad[base + c], lr, c1, c2);
 }
 
 // Exact per-texel search on the discrete nearest level 0 (qat_search): one thread per texel;
@@ -169,12 +175,14 @@ void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask) {
     NTC_CHECK(hipGetLastError());
 }
 
-void launch_lat_gather(Impl& I, int level, int K, float scale, bool rate) {
+void launch_lat_gather(Impl& I, int level, int K, float scale, bool rate, float lr, int t) {
     const size_t ntx = (size_t)I.d.lv[level].W * I.d.lv[level].H;
+    const float c1 = t > 0 ? 1.0f - powf(0.9f, (float)t) : 1.0f, c2 = t > 0 ? 1.0f - powf(0.999f, (float)t) : 1.0f;
     ProfScope ps(I, "lat_gather");
     hipLaunchKernelGGL(k_lat_gather, dim3(blocks_for(ntx, kGatherTex)), dim3(kGatherTex * kGatherPairs), 0, I.stream, I.dm, level, K,
                        scale, I.dpix, I.eps_lat,
-                       I.ranges, rate ? 1 : 0, I.ddct.rate_scale, I.ddct.BW, I.ddct.n, I.dct_dbits, I.zgrad);
+                       I.ranges, rate ? 1 : 0, I.ddct.rate_scale, I.ddct.BW, I.ddct.n, I.dct_dbits, I.zgrad, t > 0 ? 1 : 0, I.z, I.zm,
+                       I.zv, lr, c1, c2);
     NTC_CHECK(hipGetLastError());
 }
 

@@ -1,5 +1,5 @@
 // MLP-side kernels of the gfx950 ES backend: minibatch draw, member weight sets, the population
-// evaluation, the ES and central-difference finishes, the ES weight update, Adam and the decode.
+// evaluation, the central-difference finish, the ES weight update with its Adam step, Adam and the decode.
 //
 // Reference semantics (main.cpp): MlpTrainer::draw_batch 1825-1833, MlpTrainer::step 1836-1876,
 // MlpTrainer::step_fd 1890-1920, Adam::step 1799-1809, Decoder::decode_full 1712-1718.
@@ -104,19 +104,6 @@ __global__ void __launch_bounds__(kTPB) k_pop_eval(DevModel m, const float* __re
         part[(size_t)(2 * pair) * chunks + ch] = ap;
         part[(size_t)(2 * pair + 1) * chunks + ch] = an;
     }
-}
-
-// Per pair: member losses = chunk sums in chunk order / norm; dl = l+ - l-, lsum = (l+ + l-) / 2.
-// Adam::step (main.cpp:1793-1810) on parameter i given its gradient; c1, c2 from the host's powf
-__device__ __forceinline__ void adam_at(float* __restrict__ theta, float* __restrict__ m, float* __restrict__ v, size_t i, float gi,
-                                        float lr, float c1, float c2) {
-    const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
-    const float ob1 = 1.0f - b1, ob2 = 1.0f - b2;
-    const float mi = __builtin_fmaf(b1, m[i], __fmul_rn(ob1, gi));
-    const float vi = __builtin_fmaf(b2, v[i], __fmul_rn(__fmul_rn(ob2, gi), gi));
-    m[i] = mi; v[i] = vi;
-    const float mh = mi / c1, vh = vi / c2;
-    theta[i] = theta[i] - (lr * mh) / (__builtin_sqrtf(vh) + eps);
 }
 
 // ES update direction (main.cpp:1868-1873): g[k] = sum over pairs of ((float)dl_i * scale) * eps_ik, one

@@ -534,10 +534,15 @@ void Trainer::lat_step(int /*it*/, float sigma, float lr, int K) {
         launch_lat_pair(I, K, sigma, mask);
         if (rate) { launch_dct_rate_pairs(I, K, sigma); I.dct_last_K = K; }
         const float scale = 1.0f / (2.0f * (float)K * sigma);
+        // Adam on the perturbed levels inside their gathers. The other levels' gradients are zero at
+        // every step of this trainer (the mask is fixed by --qat at init), so their Adam moments stay
+        // zero and the reference's step leaves them exactly as they are: it is skipped.
+        ++I.lat_t;
         for (int l = 0; l < I.d.nlev; l++)
-            if ((mask >> l) & 1u) launch_lat_gather(I, l, K, scale, rate && l == 0);
+            if ((mask >> l) & 1u) launch_lat_gather(I, l, K, scale, rate && l == 0, lr, I.lat_t);
+    } else {
+        launch_adam(I, I.z, I.zgrad, I.zm, I.zv, I.nz, lr, ++I.lat_t);
     }
-    launch_adam(I, I.z, I.zgrad, I.zm, I.zv, I.nz, lr, ++I.lat_t);
     snap_latent_impl(I);
     I.lat_step_no++;
 }

@@ -160,7 +160,8 @@ void launch_copy_calibration(Impl& I, const float* src, float* dst, size_t n);
 void launch_lat_eps(Impl& I, int K, unsigned mask);   // also clears the latent gradient
 void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask);
 void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask);
-void launch_lat_gather(Impl& I, int level, int K, float scale, bool rate);
+// the footprint gather of one level; with t > 0 also the Adam step t (learning rate lr) of its texels
+void launch_lat_gather(Impl& I, int level, int K, float scale, bool rate, float lr = 0.0f, int t = 0);
 void launch_qat_search(Impl& I);
 
 // kernels_quant.hip
