@@ -13,7 +13,7 @@
 namespace ntc_hip {
 
 constexpr int kTPB = 256;
-constexpr int kTPB_DCT = 64;   // one (block, channel) per thread, 3 x 64 floats of state each
+constexpr int kTPB_DCT = 64;   // the probe: one (block, channel) per thread
 
 // ---------------------------------------------------------------- --qes
 __device__ __forceinline__ int qes_index(float v, float lo, float range, int levels) {
@@ -43,10 +43,6 @@ __global__ void __launch_bounds__(kTPB) k_qes_snap(DevModel m, const ntc_cuda::Q
 // ---------------------------------------------------------------- --dct-q
 __device__ __forceinline__ float dct_clampf(float v, float lo, float hi) { if (!(v >= lo)) return lo; if (v > hi) return hi; return v; }
 __device__ __forceinline__ bool first_order(int u, int v) { return (u == 1 && v == 0) || (u == 0 && v == 1); }
-__device__ __forceinline__ int floor_log2(unsigned v) { int k = 0; while (v >>= 1) k++; return k; }
-__device__ __forceinline__ int c_run(int r) { return 16 * (2 * floor_log2((unsigned)(r + 1)) + 1); }
-__device__ __forceinline__ int c_mag(int q) { return 16 * (2 * floor_log2((unsigned)q) + 1); }
-__device__ __forceinline__ int lo_weight(int tok, int p, int lo16) { return p <= 2 ? (tok * lo16 + 8) >> 4 : tok; }
 
 __device__ __forceinline__ int quant_dc(float d, int S) { return (int)dct_clampf(rintf(d / (float)S), -1024.0f, 1024.0f); }
 __device__ __forceinline__ float dequant_dc(int q, int S) { return (float)q * (float)S; }
@@ -65,74 +61,129 @@ __device__ __forceinline__ float dequant_ac(int q, int L, int u, int v, bool dz)
     const float mag = tau + (float)abs(q) * (float)L;
     return q < 0 ? -mag : mag;
 }
-// 8x8 transforms with the basis folded in; w[x * 8 + y], C[u * 8 + v]; sums from 0, index ascending
-__device__ void fwd8(const DevDct& D, const float* w, float* C) {
-    float T[64];
-    for (int x = 0; x < 8; x++)
-        for (int v = 0; v < 8; v++) { float s = 0.0f; for (int y = 0; y < 8; y++) s = s + w[x * 8 + y] * D.basis[v * 8 + y]; T[x * 8 + v] = s; }
-    for (int u = 0; u < 8; u++)
-        for (int v = 0; v < 8; v++) { float s = 0.0f; for (int x = 0; x < 8; x++) s = s + T[x * 8 + v] * D.basis[u * 8 + x]; C[u * 8 + v] = s; }
-}
-__device__ void inv8(const DevDct& D, const float* C, float* w) {
-    float T[64];
-    for (int x = 0; x < 8; x++)
-        for (int v = 0; v < 8; v++) { float s = 0.0f; for (int u = 0; u < 8; u++) s = s + D.basis[u * 8 + x] * C[u * 8 + v]; T[x * 8 + v] = s; }
-    for (int x = 0; x < 8; x++)
-        for (int y = 0; y < 8; y++) { float s = 0.0f; for (int v = 0; v < 8; v++) s = s + D.basis[v * 8 + y] * T[x * 8 + v]; w[x * 8 + y] = s; }
-}
-// proxy bits of one (block, channel), 1/16 bit (dct_block_bits)
-__device__ int block_bits(const DevDct& D, const int16_t* sym) {
-    int bits = 0, run = 0, lnz = 0;
-    for (int p = 1; p < 64; p++) {
-        const int q = sym[D.zigzag[p]];
-        if (q == 0) { run++; continue; }
-        bits += lo_weight(c_run(run) + c_mag(min(256, abs(q))) + 16, p, D.lo_w16);
-        lnz = p; run = 0;
-    }
-    if (lnz < 63) bits += 32;
-    return bits;
-}
-// greedy truncation from zigzag 63 down (dct_truncate_block)
-__device__ int truncate_block(const DevDct& D, const float* Cf, const int* st, float lam16, int16_t* sym) {
-    int ntrunc = 0, next = 64;
-    for (int p = 63; p >= 1; p--) {
-        const int k = D.zigzag[p], q = sym[k];
-        if (q == 0) continue;
-        int prev = 0;
-        for (int j = p - 1; j >= 1; j--) if (sym[D.zigzag[j]] != 0) { prev = j; break; }
-        const int r1 = p - prev - 1;
-        const int token = lo_weight(c_run(r1) + c_mag(min(256, abs(q))) + 16, p, D.lo_w16);
-        const int saved = next == 64 ? token - (p == 63 ? 32 : 0) : token + c_run(next - p - 1) - c_run(next - p - 1 + r1 + 1);
-        const float v = dequant_ac(q, st[k], k / 8, k % 8, D.deadzone != 0), c = Cf[k];
-        const float dD = c * c - (c - v) * (c - v);
-        if (dD < lam16 * (float)saved) { sym[k] = 0; ntrunc++; }
-        else next = p;
-    }
-    return ntrunc;
-}
-// dct_quantize_block
-__device__ int quantize_block(const DevDct& D, const float* Cf, const int* st, float lam16, bool with_bits, int16_t* sym,
-                              int* ntrunc, int* nz_before) {
-    for (int k = 0; k < 64; k++) sym[k] = (int16_t)(k == 0 ? quant_dc(Cf[0], D.dc_step) : quant_ac(Cf[k], st[k], k / 8, k % 8, D.deadzone != 0));
-    int nt = 0, nz = 0;
-    if (lam16 > 0.0f) {
-        for (int k = 1; k < 64; k++) if (sym[k] != 0) nz++;
-        nt = truncate_block(D, Cf, st, lam16, sym);
-    }
-    *ntrunc = nt; *nz_before = nz;
-    return with_bits ? block_bits(D, sym) : 0;
-}
 __device__ __forceinline__ size_t lvl0_index(const DevLevel& L0, int bx, int by, int x, int y, int c) {
     return (size_t)L0.off + ((size_t)(by * 8 + y) * L0.W + (bx * 8 + x)) * L0.C + c;
 }
-// dequantize + inverse DCT + clamp into zq (dct_recon_block)
-__device__ void recon_block(const DevDct& D, const DevLevel& L0, int i, const int16_t* sy, const int* st, float* zq) {
-    const int b = i / D.C, c = i % D.C, bx = b % D.BW, by = b / D.BW;
-    float Cf[64], w[64];
-    for (int k = 0; k < 64; k++) Cf[k] = k == 0 ? dequant_dc(sy[0], D.dc_step) : dequant_ac(sy[k], st[k], k / 8, k % 8, D.deadzone != 0);
-    inv8(D, Cf, w);
-    for (int y = 0; y < 8; y++)
-        for (int x = 0; x < 8; x++) zq[lvl0_index(L0, bx, by, x, y, c)] = dct_clampf(w[y * 8 + x] / 32.0f - 1.0f, -1.0f, 1.0f);
+
+// ---- one wave per (block, channel): lane = 8 row + column of the block, or 8 u + v of its
+// coefficients, or a zigzag position. Every value is computed with the reference's operations in
+// the reference's order (dct_fwd8 / dct_inv8 sums from 0 in ascending index, the quantizers, the
+// greedy truncation walking the nonzero ACs from zigzag 63 down, the token costs); only the work is
+// spread over the lanes, and the integer totals are order-free.
+constexpr int kDctWaves = 4;   // (block, channel) items per 256-thread workgroup
+
+struct DctTables {
+    float basis[64];   // [u * 8 + x]
+    int zz[64];        // zigzag position -> natural index
+    int izz[64];       // natural index -> zigzag position
+};
+__device__ __forceinline__ void load_tables(const DevDct& D, DctTables& T) {
+    if (threadIdx.x < 64) {
+        const int t = threadIdx.x;
+        T.basis[t] = D.basis[t];
+        T.zz[t] = D.zigzag[t];
+        T.izz[D.zigzag[t]] = t;
+    }
+    __syncthreads();
+}
+__device__ __forceinline__ float lane_f(float v, int src) { return __shfl(v, src); }
+__device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ int ilog2(unsigned v) { return 31 - __clz((int)v); }   // v >= 1
+__device__ __forceinline__ int c_run(int r) { return 16 * (2 * ilog2((unsigned)(r + 1)) + 1); }
+__device__ __forceinline__ int c_mag(int q) { return 16 * (2 * ilog2((unsigned)q) + 1); }
+__device__ __forceinline__ int lo_weight(int tok, int p, int lo16) { return p <= 2 ? (tok * lo16 + 8) >> 4 : tok; }
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// dct_fwd8 (main.cpp:783-789): in lane 8 a + b the sample W[a][b]; out in lane 8 u + v the coefficient
+// C[u][v]. T[a][v] = sum_b W[a][b] B[v][b], then C[u][v] = sum_a T[a][v] B[u][a].
+__device__ __forceinline__ float wave_fwd8(const DctTables& T, float w, int lane) {
+    const int hi = lane >> 3, lo = lane & 7;
+    float t = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 8; b++) t = t + lane_f(w, 8 * hi + b) * T.basis[lo * 8 + b];
+    float c = 0.0f;
+#pragma unroll
+    for (int a = 0; a < 8; a++) c = c + lane_f(t, 8 * a + lo) * T.basis[hi * 8 + a];
+    return c;
+}
+// dct_inv8 (main.cpp:790-796): in lane 8 u + v the coefficient; out in lane 8 a + b the sample. T[a][v] = sum_u B[u][a] C[u][v],
+// then W[a][b] = sum_v B[v][b] T[a][v].
+__device__ __forceinline__ float wave_inv8(const DctTables& T, float c, int lane) {
+    const int hi = lane >> 3, lo = lane & 7;
+    float t = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; u++) t = t + T.basis[u * 8 + hi] * lane_f(c, 8 * u + lo);
+    float w = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 8; v++) w = w + T.basis[v * 8 + lo] * lane_f(t, 8 * hi + v);
+    return w;
+}
+
+// dct_block_bits (main.cpp:835-849) of the symbols whose nonzero ACs are the set bits of m (zigzag
+// positions), lane p holding the symbol at position p: each nonzero's token cost with its run since the
+// previous nonzero, plus the EOB unless position 63 is the last nonzero.
+__device__ __forceinline__ int wave_block_bits(uint64_t m, int qp, int lo16, int lane) {
+    int cost = 0;
+    if ((m >> lane) & 1ull) {
+        const uint64_t below = m & ((1ull << lane) - 1ull);
+        const int prev = below ? 63 - __clzll((long long)below) : 0;
+        cost = lo_weight(c_run(lane - prev - 1) + c_mag(min(256, abs(qp))) + 16, lane, lo16);
+    }
+    const int lnz = m ? 63 - __clzll((long long)m) : 0;
+    return wave_sum_i(cost) + (lnz < 63 ? 32 : 0);
+}
+
+struct WaveSyms { int q; int bits; int ntrunc; int nz; };   // q: this lane's symbol, natural order (lane = k)
+
+// dct_quantize_block (main.cpp:871-883): the symbols of coefficient C (lane = k), the greedy truncation
+// with lam16 > 0 (dct_truncate_block, main.cpp:850-870), and the proxy bits of the result when asked.
+__device__ WaveSyms wave_quantize(const DevDct& D, const DctTables& T, float Cf, const int* __restrict__ st, float lam16,
+                                  bool with_bits, int lane) {
+    const bool dz = D.deadzone != 0;
+    WaveSyms r;
+    r.q = lane == 0 ? quant_dc(Cf, D.dc_step) : quant_ac(Cf, st[lane], lane >> 3, lane & 7, dz);
+    // the zigzag view: lane p holds position p
+    const int kp = T.zz[lane];
+    const int qp = __shfl(r.q, kp);
+    uint64_t m = __ballot(lane >= 1 && qp != 0);
+    r.nz = lam16 > 0.0f ? __popcll(m) : 0;   // the nonzero ACs before truncation, counted where it runs
+    r.ntrunc = 0;
+    if (lam16 > 0.0f && m) {
+        const float cp = lane_f(Cf, kp);
+        const uint64_t below = m & ((1ull << lane) - 1ull);
+        const int prev = below ? 63 - __clzll((long long)below) : 0;
+        const int r1 = lane - prev - 1;
+        const int token = lo_weight(c_run(r1) + c_mag(min(256, abs(qp))) + 16, lane, D.lo_w16);
+        const float vq = dequant_ac(qp, st[kp], kp >> 3, kp & 7, dz);
+        const float dD = cp * cp - (cp - vq) * (cp - vq);
+        uint64_t mm = m, cut = 0;
+        int next = 64;
+        while (mm) {   // uniform: the wave walks the block's nonzero ACs from the top
+            const int p = 63 - __clzll((long long)mm);
+            mm &= ~(1ull << p);
+            const int tok = readlane_i(token, p), rr = readlane_i(r1, p);
+            const float dd = __int_as_float(readlane_i(__float_as_int(dD), p));
+            const int saved = next == 64 ? tok - (p == 63 ? 32 : 0) : tok + c_run(next - p - 1) - c_run(next - p - 1 + rr + 1);
+            if (dd < lam16 * (float)saved) { cut |= 1ull << p; r.ntrunc++; }
+            else next = p;
+        }
+        if ((cut >> T.izz[lane]) & 1ull) r.q = 0;
+        m &= ~cut;
+    }
+    r.bits = with_bits ? wave_block_bits(m, qp, D.lo_w16, lane) : 0;
+    return r;
+}
+
+// dct_recon_block (main.cpp:899-917) of one lane's symbol (natural order): dequantize, inverse DCT, and
+// the plane value of this lane's texel (row lane >> 3, column lane & 7)
+__device__ __forceinline__ float wave_recon(const DevDct& D, const DctTables& T, int q, const int* __restrict__ st, int lane) {
+    const float Cd = lane == 0 ? dequant_dc(q, D.dc_step) : dequant_ac(q, st[lane], lane >> 3, lane & 7, D.deadzone != 0);
+    const float w = wave_inv8(T, Cd, lane);
+    return dct_clampf(w / 32.0f - 1.0f, -1.0f, 1.0f);
 }
 
 __global__ void __launch_bounds__(kTPB) k_dct_clamp0(float* __restrict__ z, float* __restrict__ zq, size_t off, size_t n0) {
@@ -142,56 +193,66 @@ __global__ void __launch_bounds__(kTPB) k_dct_clamp0(float* __restrict__ z, floa
     z[off + i] = v; zq[off + i] = v;
 }
 
-// dct_snap_block per (block, channel): clamp the shadow in place, forward DCT of (s + 1) * 32,
-// quantize (+ truncation), symbols out, reconstruct zq; integer counters are order-independent.
-__global__ void __launch_bounds__(kTPB_DCT) k_dct_snap(DevDct D, DevLevel L0, float* __restrict__ z, float* __restrict__ zq,
-                                                      int16_t* __restrict__ sym, const uint8_t* __restrict__ code,
-                                                      const int* __restrict__ step, int32_t* __restrict__ bits, int* __restrict__ cnt) {
-    const int i = blockIdx.x * kTPB_DCT + threadIdx.x;
+// dct_snap_block (main.cpp:918-940) per (block, channel), one wave each: clamp the shadow in place, forward DCT of
+// (s + 1) * 32, quantize (+ truncation), symbols out, reconstruct zq; with the rate term on, the block's
+// proxy bits and its two counts (added up on the host when asked: no atomics).
+__global__ void __launch_bounds__(64 * kDctWaves) k_dct_snap(DevDct D, DevLevel L0, float* __restrict__ z, float* __restrict__ zq,
+                                                            int16_t* __restrict__ sym, const uint8_t* __restrict__ code,
+                                                            const int* __restrict__ step, int32_t* __restrict__ bits,
+                                                            int* __restrict__ tn) {
+    __shared__ DctTables T;
+    load_tables(D, T);
+    const int lane = threadIdx.x & 63;
+    const int i = blockIdx.x * kDctWaves + (threadIdx.x >> 6);
     if (i >= D.n) return;
     const int b = i / D.C, c = i % D.C, bx = b % D.BW, by = b / D.BW;
-    float w[64], Cf[64];
-    for (int y = 0; y < 8; y++)
-        for (int x = 0; x < 8; x++) {
-            const size_t idx = lvl0_index(L0, bx, by, x, y, c);
-            const float s = dct_clampf(z[idx], -1.0f, 1.0f);
-            z[idx] = s;
-            w[y * 8 + x] = (s + 1.0f) * 32.0f;
-        }
-    fwd8(D, w, Cf);
+    const size_t idx = lvl0_index(L0, bx, by, lane & 7, lane >> 3, c);
+    const float s = dct_clampf(z[idx], -1.0f, 1.0f);
+    z[idx] = s;
+    const float Cf = wave_fwd8(T, (s + 1.0f) * 32.0f, lane);
     const int cd = code[i];
     const int* st = step + ((size_t)c * 16 + cd) * 64;
-    int16_t sy[64];
-    int nt = 0, nz = 0;
-    quantize_block(D, Cf, st, D.lam_t16[cd], false, sy, &nt, &nz);
-    for (int k = 0; k < 64; k++) sym[(size_t)i * 64 + k] = sy[k];
-    if (D.rate_es || D.rate_trunc) {
-        bits[i] = block_bits(D, sy);
-        if (nt) atomicAdd(cnt, nt);
-        if (nz) atomicAdd(cnt + 1, nz);
+    const bool rate = D.rate_es || D.rate_trunc;
+    const WaveSyms q = wave_quantize(D, T, Cf, st, D.lam_t16[cd], rate, lane);
+    sym[(size_t)i * 64 + lane] = (int16_t)q.q;
+    if (rate && lane == 0) {
+        bits[i] = q.bits;
+        tn[i] = q.ntrunc;
+        tn[D.n + i] = q.nz;
     }
-    recon_block(D, L0, i, sy, st, zq);
+    zq[idx] = wave_recon(D, T, q.q, st, lane);
 }
 
 // level 0 of the decode copy from uploaded symbols (the shadow is not touched)
-__global__ void __launch_bounds__(kTPB_DCT) k_dct_recon(DevDct D, DevLevel L0, const int16_t* __restrict__ sym,
-                                                       const uint8_t* __restrict__ code, const int* __restrict__ step,
-                                                       float* __restrict__ zq, int32_t* __restrict__ bits) {
-    const int i = blockIdx.x * kTPB_DCT + threadIdx.x;
+__global__ void __launch_bounds__(64 * kDctWaves) k_dct_recon(DevDct D, DevLevel L0, const int16_t* __restrict__ sym,
+                                                             const uint8_t* __restrict__ code, const int* __restrict__ step,
+                                                             float* __restrict__ zq, int32_t* __restrict__ bits) {
+    __shared__ DctTables T;
+    load_tables(D, T);
+    const int lane = threadIdx.x & 63;
+    const int i = blockIdx.x * kDctWaves + (threadIdx.x >> 6);
     if (i >= D.n) return;
-    int16_t sy[64];
-    for (int k = 0; k < 64; k++) sy[k] = sym[(size_t)i * 64 + k];
-    if (D.rate_es || D.rate_trunc) bits[i] = block_bits(D, sy);
-    recon_block(D, L0, i, sy, step + ((size_t)(i % D.C) * 16 + code[i]) * 64, zq);
+    const int q = sym[(size_t)i * 64 + lane];
+    if (D.rate_es || D.rate_trunc) {
+        const int qp = __shfl(q, T.zz[lane]);
+        const int bb = wave_block_bits(__ballot(lane >= 1 && qp != 0), qp, D.lo_w16, lane);
+        if (lane == 0) bits[i] = bb;
+    }
+    const int b = i / D.C, c = i % D.C, bx = b % D.BW, by = b / D.BW;
+    zq[lvl0_index(L0, bx, by, lane & 7, lane >> 3, c)] = wave_recon(D, T, q, step + ((size_t)c * 16 + code[i]) * 64, lane);
 }
 
 // --dct-lambda part A for pair blockIdx.y: bits(snap(clamp(z + sg eps))) - bits(snap(clamp(z - sg eps)))
-// on the shadow, with the pair's level-0 Gaussians (the latent step's own draws).
-__global__ void __launch_bounds__(kTPB_DCT) k_dct_rate_pair(DevDct D, DevLevel L0, long long nz, float sg,
-                                                           const float* __restrict__ z, const float* __restrict__ eps,
-                                                           const uint8_t* __restrict__ code, const int* __restrict__ step,
-                                                           int32_t* __restrict__ dbits, int* __restrict__ hits) {
-    const int i = blockIdx.x * kTPB_DCT + threadIdx.x;
+// on the shadow, with the pair's level-0 Gaussians (the latent step's own draws); one wave per
+// (block, channel, pair). The hit count (pairs whose bits differ) is the number of nonzero dbits.
+__global__ void __launch_bounds__(64 * kDctWaves) k_dct_rate_pair(DevDct D, DevLevel L0, long long nz, float sg,
+                                                                 const float* __restrict__ z, const float* __restrict__ eps,
+                                                                 const uint8_t* __restrict__ code, const int* __restrict__ step,
+                                                                 int32_t* __restrict__ dbits) {
+    __shared__ DctTables T;
+    load_tables(D, T);
+    const int lane = threadIdx.x & 63;
+    const int i = blockIdx.x * kDctWaves + (threadIdx.x >> 6);
     if (i >= D.n) return;
     const int k = blockIdx.y;
     const float* e = eps + (size_t)k * nz;
@@ -199,23 +260,16 @@ __global__ void __launch_bounds__(kTPB_DCT) k_dct_rate_pair(DevDct D, DevLevel L
     const int cd = code[i];
     const int* st = step + ((size_t)c * 16 + cd) * 64;
     const float lam = D.lam_t16[cd];
+    const size_t idx = lvl0_index(L0, bx, by, lane & 7, lane >> 3, c);
+    const float zv = z[idx], pert = sg * e[idx];
     int bb[2];
+#pragma unroll
     for (int sgn = 0; sgn < 2; sgn++) {
-        float w[64], Cf[64];
-        int16_t sy[64];
-        for (int y = 0; y < 8; y++)
-            for (int x = 0; x < 8; x++) {
-                const size_t idx = lvl0_index(L0, bx, by, x, y, c);
-                const float pert = sg * e[idx];
-                const float s = dct_clampf(sgn == 0 ? z[idx] + pert : z[idx] - pert, -1.0f, 1.0f);
-                w[y * 8 + x] = (s + 1.0f) * 32.0f;
-            }
-        fwd8(D, w, Cf);
-        int nt, nzb;
-        bb[sgn] = quantize_block(D, Cf, st, lam, true, sy, &nt, &nzb);
+        const float s = dct_clampf(sgn == 0 ? zv + pert : zv - pert, -1.0f, 1.0f);
+        const float Cf = wave_fwd8(T, (s + 1.0f) * 32.0f, lane);
+        bb[sgn] = wave_quantize(D, T, Cf, st, lam, true, lane).bits;
     }
-    dbits[(size_t)k * D.n + i] = bb[0] - bb[1];
-    if (bb[0] != bb[1]) atomicAdd(hits, 1);
+    if (lane == 0) dbits[(size_t)k * D.n + i] = bb[0] - bb[1];
 }
 
 // z += f * (zq - z) on [off, off + n) (one fused operation, as the reference's build evaluates
@@ -223,11 +277,6 @@ __global__ void __launch_bounds__(kTPB_DCT) k_dct_rate_pair(DevDct D, DevLevel L
 __global__ void __launch_bounds__(kTPB) k_shadow_pull(float* __restrict__ z, const float* __restrict__ zq, size_t off, size_t n, float f) {
     const size_t i = (size_t)blockIdx.x * kTPB + threadIdx.x;
     if (i < n) z[off + i] = __builtin_fmaf(f, zq[off + i] - z[off + i], z[off + i]);
-}
-
-__global__ void k_zero_ints(int* __restrict__ p, int n) {
-    const int i = threadIdx.x;
-    if (i < n) p[i] = 0;
 }
 
 // ---------------------------------------------------------------- launchers
@@ -285,25 +334,19 @@ __global__ void __launch_bounds__(kTPB_DCT) k_dct_probe(DevModel m, const float*
 
 void launch_dct_snap(Impl& I) {
     ProfScope ps(I, "dct_snap");
-    if (I.dct_rate_es || I.dct_rate_trunc) {
-        hipLaunchKernelGGL(k_zero_ints, dim3(1), dim3(64), 0, I.stream, I.dct_cnt, 2);
-        NTC_CHECK(hipGetLastError());
-    }
-    hipLaunchKernelGGL(k_dct_snap, dim3(blocks_for(I.ddct.n, kTPB_DCT)), dim3(kTPB_DCT), 0, I.stream, I.ddct, I.dm.lv[0], I.z, I.zq,
-                       I.dct_sym, I.dct_code, I.dct_step, I.dct_bits, I.dct_cnt);
+    hipLaunchKernelGGL(k_dct_snap, dim3(blocks_for(I.ddct.n, kDctWaves)), dim3(64 * kDctWaves), 0, I.stream, I.ddct, I.dm.lv[0], I.z, I.zq,
+                       I.dct_sym, I.dct_code, I.dct_step, I.dct_bits, I.dct_tn);
     NTC_CHECK(hipGetLastError());
 }
 void launch_dct_recon(Impl& I) {
-    hipLaunchKernelGGL(k_dct_recon, dim3(blocks_for(I.ddct.n, kTPB_DCT)), dim3(kTPB_DCT), 0, I.stream, I.ddct, I.dm.lv[0], I.dct_sym,
+    hipLaunchKernelGGL(k_dct_recon, dim3(blocks_for(I.ddct.n, kDctWaves)), dim3(64 * kDctWaves), 0, I.stream, I.ddct, I.dm.lv[0], I.dct_sym,
                        I.dct_code, I.dct_step, I.zq, I.dct_bits);
     NTC_CHECK(hipGetLastError());
 }
 void launch_dct_rate_pairs(Impl& I, int K, float sigma) {
     ProfScope ps(I, "dct_rate");
-    hipLaunchKernelGGL(k_zero_ints, dim3(1), dim3(64), 0, I.stream, I.dct_cnt + 2, 1);
-    NTC_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(k_dct_rate_pair, dim3(blocks_for(I.ddct.n, kTPB_DCT), K), dim3(kTPB_DCT), 0, I.stream, I.ddct, I.dm.lv[0],
-                       (long long)I.nz, sigma, I.z, I.eps_lat, I.dct_code, I.dct_step, I.dct_dbits, I.dct_cnt + 2);
+    hipLaunchKernelGGL(k_dct_rate_pair, dim3(blocks_for(I.ddct.n, kDctWaves), K), dim3(64 * kDctWaves), 0, I.stream, I.ddct, I.dm.lv[0],
+                       (long long)I.nz, sigma, I.z, I.eps_lat, I.dct_code, I.dct_step, I.dct_dbits);
     NTC_CHECK(hipGetLastError());
 }
 void launch_shadow_pull(Impl& I, size_t off, size_t n, float f) {

@@ -184,7 +184,7 @@ Trainer::~Trainer() {
         dev_free(I.wsets); dev_free(I.eps_mlp); dev_free(I.gpart); dev_free(I.part); dev_free(I.dl); dev_free(I.lsum); dev_free(I.hh);
         dev_free(I.eps_lat); dev_free(I.dpix); dev_free(I.ranges); dev_free(I.qat_grid); dev_free(I.qat_bits);
         dev_free(I.qes_dev); dev_free(I.qgrid);
-        dev_free(I.dct_sym); dev_free(I.dct_code); dev_free(I.dct_step); dev_free(I.dct_bits); dev_free(I.dct_dbits); dev_free(I.dct_cnt); dev_free(I.dct_probe_code); dev_free(I.dct_gain);
+        dev_free(I.dct_sym); dev_free(I.dct_code); dev_free(I.dct_step); dev_free(I.dct_bits); dev_free(I.dct_dbits); dev_free(I.dct_tn); dev_free(I.dct_probe_code); dev_free(I.dct_gain);
         (void)hipStreamDestroy(I.stream);
     }
     delete im;
@@ -322,13 +322,13 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
         memcpy(D.basis, d.dct_basis, sizeof(D.basis));
         memcpy(D.zigzag, d.dct_zigzag, sizeof(D.zigzag));
         dev_alloc(&I.dct_sym, (size_t)D.n * 64); dev_alloc(&I.dct_code, (size_t)D.n); dev_alloc(&I.dct_step, (size_t)D.C * 16 * 64);
-        dev_alloc(&I.dct_bits, (size_t)D.n); dev_alloc(&I.dct_cnt, 3);
+        dev_alloc(&I.dct_bits, (size_t)D.n); dev_alloc(&I.dct_tn, 2 * (size_t)D.n);
         dev_alloc(&I.dct_probe_code, (size_t)D.n); dev_alloc(&I.dct_gain, (size_t)D.n);
         NTC_CHECK(hipMemset(I.dct_sym, 0, (size_t)D.n * 64 * sizeof(int16_t)));
         NTC_CHECK(hipMemset(I.dct_code, 0, (size_t)D.n));
         NTC_CHECK(hipMemset(I.dct_step, 0, (size_t)D.C * 16 * 64 * sizeof(int)));
         NTC_CHECK(hipMemset(I.dct_bits, 0, (size_t)D.n * sizeof(int32_t)));
-        NTC_CHECK(hipMemset(I.dct_cnt, 0, 3 * sizeof(int)));
+        NTC_CHECK(hipMemset(I.dct_tn, 0, 2 * (size_t)D.n * sizeof(int)));
     }
     dev_alloc(&I.w, I.P); dev_alloc(&I.wgrad, I.P); dev_alloc(&I.wm, I.P); dev_alloc(&I.wv, I.P);
     dev_alloc(&I.tgt, I.npix * d.nout); dev_alloc(&I.img, I.npix * d.nout);
@@ -439,12 +439,19 @@ void Trainer::download_dct_rate(int32_t* bits, int32_t* dbits_last_pair, int* nt
                                      (size_t)I.ddct.n * sizeof(int32_t), hipMemcpyDeviceToHost, I.stream));
         else memset(dbits_last_pair, 0, (size_t)I.ddct.n * sizeof(int32_t));
     }
-    int cnt[3];
-    NTC_CHECK(hipMemcpyAsync(cnt, I.dct_cnt, sizeof(cnt), hipMemcpyDeviceToHost, I.stream));
+    // the counts: sums of the last snap's per-block counts, and the pairs of the last rate pass whose
+    // bits differ between the two members (the nonzero dbits)
+    const size_t n = (size_t)I.ddct.n, nd = (I.dct_dbits && I.dct_last_K > 0) ? (size_t)I.dct_last_K * n : 0;
+    std::vector<int> tn(2 * n), db(nd);
+    NTC_CHECK(hipMemcpyAsync(tn.data(), I.dct_tn, 2 * n * sizeof(int), hipMemcpyDeviceToHost, I.stream));
+    if (nd) NTC_CHECK(hipMemcpyAsync(db.data(), I.dct_dbits, nd * sizeof(int), hipMemcpyDeviceToHost, I.stream));
     sync(I);
-    if (ntrunc) *ntrunc = cnt[0];
-    if (nz_before) *nz_before = cnt[1];
-    if (hits) *hits = cnt[2];
+    long long nt = 0, nzb = 0, h = 0;
+    for (size_t i = 0; i < n; i++) { nt += tn[i]; nzb += tn[n + i]; }
+    for (size_t i = 0; i < nd; i++) h += db[i] != 0;
+    if (ntrunc) *ntrunc = (int)nt;
+    if (nz_before) *nz_before = (int)nzb;
+    if (hits) *hits = (int)h;
     if (evals) *evals = I.dct_evals;
 }
 

@@ -91,7 +91,7 @@ struct ntc_cuda::Trainer::Impl {
     uint8_t* dct_code = nullptr;
     int* dct_step = nullptr;
     int32_t *dct_bits = nullptr, *dct_dbits = nullptr;   // dbits: Kcap x n (pair k's bit differences)
-    int* dct_cnt = nullptr;    // ntrunc, nz_before (last snap), hits (last lat_step)
+    int* dct_tn = nullptr;     // per (block, channel) of the last snap: truncated ACs [n], then nonzero ACs before truncation [n]
     uint8_t* dct_probe_code = nullptr;   // the device probe's codes (n)
     float* dct_gain = nullptr;           // and block gains (n)
     int dct_evals = 0, dct_last_K = 0;
