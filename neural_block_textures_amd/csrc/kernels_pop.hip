@@ -41,14 +41,20 @@ __device__ __forceinline__ float buffer_f32(__amdgpu_buffer_rsrc_t r, uint32_t v
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
 }
 
+// Models with at most 4 outputs keep all of them in lane group 0 of a tile's output registers: the
+// two tiles of a pass are packed into one register set (tile u in lane group u) before the sigmoid and
+// the error terms, which then run once for both tiles.
+template <class S>
+constexpr bool pop_pack() { return MfmaShape<S>::kNout <= 4 && pop_u<S>() == 2; }
+
 template <class S>
 struct PopTileIn {
     float b1[pop_u<S>()][MfmaShape<S>::kKs1];
-    float t[pop_u<S>()][4];
+    float t[pop_pack<S>() ? 1 : pop_u<S>()][4];   // packed: lane group u holds tile u's targets
 };
 
 // Inputs of tiles j .. j + U - 1 of this wave: soff = byte offset of tile j's first slot (uniform);
-// tile u sits 32 slots further per u.
+// tile u sits 32 slots further per u (packed: the target offsets of lane group 1 already include it).
 template <class S>
 __device__ __forceinline__ void pop_load(PopTileIn<S>& in, __amdgpu_buffer_rsrc_t rf, __amdgpu_buffer_rsrc_t rt, uint32_t soff,
                                          const uint32_t (&fo)[MfmaShape<S>::kKs1], const uint32_t (&to)[4]) {
@@ -58,8 +64,10 @@ __device__ __forceinline__ void pop_load(PopTileIn<S>& in, __amdgpu_buffer_rsrc_
         const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane((int)(soff + 128u * u));   // uniform: an SGPR
 #pragma unroll
         for (int ks = 0; ks < Q::kKs1; ks++) in.b1[u][ks] = buffer_f32(rf, fo[ks], so);
+        if (!pop_pack<S>() || u == 0) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) in.t[u][r] = buffer_f32(rt, to[r], so);
+            for (int r = 0; r < 4; r++) in.t[u][r] = buffer_f32(rt, to[r], so);
+        }
     }
 }
 
@@ -117,20 +125,27 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
         mfma_load<S, false>(W, src.wsets + (size_t)(2 * pair + sgn) * Q::kP, lane);
     }
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
+    constexpr bool kPack = pop_pack<S>();
+    // the channel weight of each of this lane's output registers (rows 4 g + r; packed: rows r of
+    // lane group g's tile, groups 2 and 3 unused), zero past the last output
     float cw[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         cw[r] = 0.0f;
 #pragma unroll
-        for (int c = 0; c < Q::kNout; c++) if (4 * g + r == c) cw[r] = m.cw[c];
+        for (int c = 0; c < Q::kNout; c++)
+            if ((kPack ? (g <= 1 && r == c) : 4 * g + r == c)) cw[r] = m.cw[c];
     }
     // lane byte offsets of the feature rows 4 ks + g and target rows 4 g + r (rows past the last
-    // one are clamped to it: their weights, or their channel weights cw, are zero)
+    // one are clamped to it: their weights, or their channel weights cw, are zero); packed: target
+    // row r of tile g (lane group 1 reads the pass's second tile)
     uint32_t fo[Q::kKs1], to[4];
 #pragma unroll
     for (int ks = 0; ks < Q::kKs1; ks++) fo[ks] = 4u * ((uint32_t)min(4 * ks + g, Q::kIn - 1) * (uint32_t)Mcap + (uint32_t)i16);
 #pragma unroll
-    for (int r = 0; r < 4; r++) to[r] = 4u * ((uint32_t)min(4 * g + r, Q::kNout - 1) * (uint32_t)Mcap + (uint32_t)i16);
+    for (int r = 0; r < 4; r++)
+        to[r] = kPack ? 4u * ((uint32_t)min(r, Q::kNout - 1) * (uint32_t)Mcap + (uint32_t)i16) + (g == 1 ? 128u : 0u)
+                      : 4u * ((uint32_t)min(4 * g + r, Q::kNout - 1) * (uint32_t)Mcap + (uint32_t)i16);
     const int s0 = ch * chunk, s1 = min(M, s0 + chunk);
     const int tiles = (s1 - s0 + 15) >> 4;
     const int mine = (tiles - half + 1) >> 1;   // this wave's tiles: 2 j + half, j < mine
@@ -150,31 +165,50 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
         }
         f4v o[U];
         mfma_forward<S, U, LeakUnit, false>(W, c.b1, m.leak, o);
-        // this lane's channel terms cw (d d): one multiply and one fused multiply-add each, summed in
-        // float over the pass's tiles, then into the double
-        float dq[U][4], dd[U][4];
+        if constexpr (kPack) {
+            // lane group 0 of each tile holds its outputs: tile 1's move to lane group 1
+            f4v op;
 #pragma unroll
-        for (int u = 0; u < U; u++)
+            for (int r = 0; r < 4; r++)
+                op[r] = __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(o[0][r]), __float_as_uint(o[1][r]), false, false)[0]);
+            float tsum = 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                dd[u][r] = out_of<S>(o[u][r], Clamp) - c.t[u][r];
-                dq[u][r] = __fmul_rn(cw[r], dd[u][r]);
+                const float d = out_of<S>(op[r], Clamp) - c.t[0][r];
+                tsum = __builtin_fmaf(__fmul_rn(cw[r], d), d, tsum);
             }
-        if (j + U <= mine && s0 + 16 * (2 * (j + U - 1) + half) + 16 <= s1) {   // all U tiles whole (uniform)
-            float tsum = 0.0f;
+            if (j + U <= mine && s0 + 16 * (2 * (j + U - 1) + half) + 16 <= s1) e += (double)tsum;   // both tiles whole (uniform)
+            else {
+                const int gu = g & 1;   // this lane's tile (groups 2, 3 carry zeros)
+                if (j + gu < mine && s0 + 16 * (2 * (j + gu) + half) + i16 < s1) e += (double)tsum;
+            }
+        } else {
+            // this lane's channel terms cw (d d): one multiply and one fused multiply-add each, summed in
+            // float over the pass's tiles, then into the double
+            float dq[U][4], dd[U][4];
 #pragma unroll
             for (int u = 0; u < U; u++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) tsum = __builtin_fmaf(dq[u][r], dd[u][r], tsum);
-            e += (double)tsum;
-        } else {
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int st = s0 + 16 * (2 * (j + u) + half);   // first slot of the tile (uniform)
+                for (int r = 0; r < 4; r++) {
+                    dd[u][r] = out_of<S>(o[u][r], Clamp) - c.t[u][r];
+                    dq[u][r] = __fmul_rn(cw[r], dd[u][r]);
+                }
+            if (j + U <= mine && s0 + 16 * (2 * (j + U - 1) + half) + 16 <= s1) {   // all U tiles whole (uniform)
                 float tsum = 0.0f;
 #pragma unroll
-                for (int r = 0; r < 4; r++) tsum = __builtin_fmaf(dq[u][r], dd[u][r], tsum);
-                if (j + u < mine && st + i16 < s1) e += (double)tsum;
+                for (int u = 0; u < U; u++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) tsum = __builtin_fmaf(dq[u][r], dd[u][r], tsum);
+                e += (double)tsum;
+            } else {
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const int st = s0 + 16 * (2 * (j + u) + half);   // first slot of the tile (uniform)
+                    float tsum = 0.0f;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) tsum = __builtin_fmaf(dq[u][r], dd[u][r], tsum);
+                    if (j + u < mine && st + i16 < s1) e += (double)tsum;
+                }
             }
         }
     };
@@ -214,6 +248,9 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
                                                       unsigned mask, float* __restrict__ dpix) {
     using Q = MfmaShape<S>;
     constexpr int NO = Q::kNout, kLatPix = lat_pix<S>(), kRounds = kLatPix / 256;
+    // at most 4 outputs: the + member's outputs stay in lane group 0, the - member's move to group 1,
+    // and each pixel's error is one lane's chain over its channels in ascending order
+    constexpr bool kPack = NO <= 4;
     const int k = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
     const float* e = eps + (size_t)k * m.nz;
@@ -222,12 +259,21 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     mfma_load<S, false>(W, w, lane);
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     float cw[4];
-    lane_cw<NO>(m.cw, g, cw);
+    if constexpr (kPack) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) cw[r] = (g <= 1 && r < NO) ? m.cw[r] : 0.0f;
+    } else {
+        lane_cw<NO>(m.cw, g, cw);
+    }
     // the targets of the tile at pixel t0: lane (g, j) reads channels 4 g .. 4 g + 3 of pixel t0 + j (one
-    // 16-byte load when a pixel's row is a whole number of float4; rows past the last are clamped)
+    // 16-byte load when a pixel's row is a whole number of float4; rows past the last are clamped);
+    // packed: channels 0 .. 3 in every lane group
     auto load_t = [&](int t0, float (&t)[4]) {
         const int pr = min(t0 + i16, m.npix - 1);
-        if constexpr (NO % 4 == 0) {
+        if constexpr (kPack) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) t[r] = tgt[(size_t)pr * NO + min(r, NO - 1)];
+        } else if constexpr (NO % 4 == 0) {
             const f4v v = *reinterpret_cast<const f4v*>(tgt + (size_t)pr * NO + min(4 * g, NO - 4));
 #pragma unroll
             for (int r = 0; r < 4; r++) t[r] = v[r];
@@ -259,6 +305,20 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
             for (int ks = 0; ks < Q::kKs1; ks++) { b1[0][ks] = bp[t][ks]; b1[1][ks] = bm[t][ks]; }
             f4v o[2];
             mfma_forward<S, 2, LeakUnit, false>(W, b1, m.leak, o);
+            const int p = base + 16 * t + i16;
+            if constexpr (kPack) {
+                float ev = 0.0f;   // group 0: e+, group 1: e-
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float op = __uint_as_float(
+                        __builtin_amdgcn_permlane16_swap(__float_as_uint(o[0][r]), __float_as_uint(o[1][r]), false, false)[0]);
+                    const float d = out_of<S>(op, Clamp) - tt[r];
+                    ev = __builtin_fmaf(cw[r], __fmul_rn(d, d), ev);
+                }
+                const auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(ev), __float_as_uint(ev), false, false);
+                if (g == 0 && p < m.npix) out[p] = __fmul_rn(__uint_as_float(x[0]) - __uint_as_float(x[1]), m.inv_px);
+                continue;
+            }
             // each lane's four channel terms cw (d d) in ascending order, then the four lane groups
             // added pairwise (permlane swaps): e+ in lanes 0-31, e- in lanes 32-63, then e+ - e-
             float ep = 0.0f, em = 0.0f;
@@ -273,7 +333,6 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
             const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
             const float c = __uint_as_float(q[0]) + __uint_as_float(q[1]);   // lanes 0-31: e+, 32-63: e-
             const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);
-            const int p = base + 16 * t + i16;
             if (g == 0 && p < m.npix) out[p] = __fmul_rn(__uint_as_float(x[0]) - __uint_as_float(x[1]), m.inv_px);
         }
     }
