@@ -231,8 +231,9 @@ def run_gpu(w, steps, warmup, fd_steps=0, seconds=0.0):
         tr.synchronize()
         per = (time.perf_counter() - t0) / 2
         steps = int(min(2000, max(3, math.ceil(seconds / per))))
-    # the timed region, every launch bracketed by HIP events on the trainer's stream
-    tr.set_profiling(True)
+    # the timed region: every launch of the population kernel bracketed by HIP events on the trainer's
+    # stream (an event pair costs the stream a few microseconds, so the other launches go unbracketed)
+    tr.set_profiling(True, only=["pop_eval"])
     tr.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -240,12 +241,22 @@ def run_gpu(w, steps, warmup, fd_steps=0, seconds=0.0):
         es_iter(tr, w, it)
     tr.synchronize()
     el = time.perf_counter() - t0
+    pop_ms, pop_n = tr.kernel_time("pop_eval")
+    tr.set_profiling(False)
+    # the per-kernel breakdown: a further profiled stretch with every launch bracketed
+    tr.set_profiling(True)
+    for _ in range(max(3, min(steps, 50))):
+        it += 1
+        es_iter(tr, w, it)
+    tr.synchronize()
     kernels = {}
     for name in KERNELS:
         ms, n = tr.kernel_time(name)
         if n:
             kernels[name] = {"ms_total": round(ms, 3), "launches": n, "ms_mean": round(ms / n, 4)}
     tr.set_profiling(False)
+    if pop_n:   # the roofline's launch time is the timed region's
+        kernels["pop_eval"] = {"ms_total": round(pop_ms, 3), "launches": pop_n, "ms_mean": round(pop_ms / pop_n, 4)}
     fd = None
     if fd_steps > 0:
         tr.reset_mlp_adam()

@@ -148,6 +148,9 @@ void ntc_trainer_synchronize(ntc_trainer* t);
 /* Per-kernel device time with HIP events recorded on the trainer's stream around each launch
  * of the named kernel family ("pop_eval", "lat_pair", "qat_search", ...). */
 void ntc_trainer_set_profiling(ntc_trainer* t, int on);
+/* restrict the events to the comma-separated kernel families in names (null or "" = every family): each
+ * event pair costs the stream a few microseconds */
+void ntc_trainer_set_profiling_only(ntc_trainer* t, const char* names);
 int ntc_trainer_kernel_time(ntc_trainer* t, const char* name, double* total_ms, long long* launches);
 // 1 if the stage ("pop_eval", "lat_pair", "qat_search") runs on the FP32 matrix cores for this model, else 0
 int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage);

@@ -159,6 +159,7 @@ void ntc_trainer_set_profiling(ntc_trainer* t, int on) {
     I.profiling = on != 0;
     if (on) I.times.clear();
 }
+void ntc_trainer_set_profiling_only(ntc_trainer* t, const char* names) { t->t.im->prof_only = names ? names : ""; }
 int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage) {
     const auto& I = *t->t.im;
     const std::string s = stage ? stage : "";

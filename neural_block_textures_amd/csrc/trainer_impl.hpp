@@ -105,6 +105,7 @@ struct ntc_cuda::Trainer::Impl {
     const char* shape_name = "runtime";
 
     bool profiling = false;
+    std::string prof_only;     // comma-separated kernel families to time; empty = all
     std::map<std::string, ntc_hip::KernelTimes> times;
 };
 
@@ -114,11 +115,17 @@ using Impl = ntc_cuda::Trainer::Impl;
 // profiling: events around one launch on the trainer's stream
 struct ProfScope {
     Impl& I; const char* name; hipEvent_t a = nullptr, b = nullptr;
-    ProfScope(Impl& I_, const char* n) : I(I_), name(n) {
-        if (I.profiling) { NTC_CHECK(hipEventCreate(&a)); NTC_CHECK(hipEventCreate(&b)); NTC_CHECK(hipEventRecord(a, I.stream)); }
+    bool on;
+    ProfScope(Impl& I_, const char* n) : I(I_), name(n), on(I_.profiling && selected(I_.prof_only, n)) {
+        if (on) { NTC_CHECK(hipEventCreate(&a)); NTC_CHECK(hipEventCreate(&b)); NTC_CHECK(hipEventRecord(a, I.stream)); }
     }
     ~ProfScope() {
-        if (I.profiling) { NTC_CHECK(hipEventRecord(b, I.stream)); I.times[name].pending.emplace_back(a, b); }
+        if (on) { NTC_CHECK(hipEventRecord(b, I.stream)); I.times[name].pending.emplace_back(a, b); }
+    }
+    static bool selected(const std::string& only, const char* n) {
+        if (only.empty()) return true;
+        const std::string key = "," + only + ",", item = "," + std::string(n) + ",";
+        return key.find(item) != std::string::npos;
     }
 };
 void resolve_times(Impl& I);

@@ -100,6 +100,7 @@ def library() -> C.CDLL:
             "ntc_trainer_stream": (P, [P]),
             "ntc_trainer_synchronize": (None, [P]),
             "ntc_trainer_set_profiling": (None, [P, C.c_int]),
+            "ntc_trainer_set_profiling_only": (None, [P, C.c_char_p]),
             "ntc_trainer_kernel_time": (C.c_int, [P, C.c_char_p, P, P]),
             "ntc_trainer_on_matrix_cores": (C.c_int, [P, C.c_char_p]),
             "ntc_trainer_dct_probe": (None, [P, P, P]),
@@ -409,7 +410,9 @@ class Trainer:
     def synchronize(self):
         self._lib.ntc_trainer_synchronize(self._h)
 
-    def set_profiling(self, on: bool):
+    def set_profiling(self, on: bool, only=None):
+        """HIP events around every launch (of the kernel families in `only`, if given)"""
+        self._lib.ntc_trainer_set_profiling_only(self._h, ",".join(only).encode() if only else b"")
         self._lib.ntc_trainer_set_profiling(self._h, 1 if on else 0)
 
     def on_matrix_cores(self, stage: str) -> bool:
