@@ -27,9 +27,10 @@
 namespace ntc_hip {
 
 constexpr int kPopWaves = 4;
-// 16-slot tiles a wave evaluates at once: two, one for the 64-wide hidden layers (registers)
+// 16-slot tiles a wave evaluates at once (two independent chains of matrix instructions; the 64-wide
+// models then hold 236 VGPRs at two waves per SIMD)
 template <class S>
-constexpr int pop_u() { return MfmaShape<S>::kH > 32 ? 1 : 2; }
+constexpr int pop_u() { return 2; }
 
 // A raw buffer over the minibatch arrays: loads take a loop-invariant 32-bit lane offset (VGPR) and
 // the tile's byte offset (SGPR), so no address arithmetic per load. num_records = the allocation
