@@ -60,3 +60,22 @@ def test_round_trip_v14(tmp_path):
     assert r.version == 14 and r.layout.levels == lay.levels and r.dct["q"] == [75, 30] and r.dct["deadzone"] == 0
     assert np.array_equal(r.dct["sym"], dct["sym"]) and np.array_equal(r.dct["code"], dct["code"])
     assert np.array_equal(r.z, z) and np.array_equal(r.p, m.p)
+
+
+def test_post_hoc_8bit_decode_matches_reference(orc):
+    """ntc_decode's default (--q8): the levels training left continuous on bitrate_stats' per-channel 8-bit
+    grid; the oracle's decode of those values against the reference's recon_q_final_t*.png"""
+    from neural_block_textures_amd import decode
+    m = decode.load(MODEL)            # q8 by default
+    raw = model_file.read(MODEL)
+    assert not np.array_equal(m.z, raw.z)
+    for (W, H, C, _), off in zip(m.layout.levels, m.layout.offsets):   # at most 256 values per channel
+        lv = m.z[off:off + W * H * C].reshape(-1, C)
+        assert max(np.unique(lv[:, c]).size for c in range(C)) <= 256
+    ref = golden("ref_m1234_recon.npz")
+    img = u8(orc.decode_full(m.layout, m.p, m.z)).reshape(512, 512, 12)
+    for tag in ("a", "b"):
+        y, x = ref[f"at_{tag}"]
+        d = np.abs(img[y:y + 64, x:x + 64].astype(int) - ref[f"q_crop_{tag}"].astype(int))
+        assert d.max() <= 1 and (d == 0).mean() > 0.999
+    assert np.abs(img.reshape(-1, 12).astype(np.int64).sum(0) - ref["q_channel_sums"]).max() <= 64

@@ -4,7 +4,8 @@ read and written back byte for byte; the writer, fed the model file the same run
 reference's file byte for byte (palette, post-hoc grid, --qes grid and DCT levels, padding, --clamp);
 the values the container holds decode (oracle) to the reference's own recon_q_final and to its
 standalone decoder's output; corrupted files are refused with the reference's reasons; the fp16
-rounding against the reference's own known answers (ntcb_selfcheck, main.cpp:2456-2470)."""
+rounding against the reference's own known answers (ntcb_selfcheck, main.cpp:2456-2470); the decoder's
+post-hoc 8-bit rule applied to the run's model file gives exactly the container's values."""
 import ctypes as C
 import os
 import struct
@@ -192,3 +193,12 @@ def test_sync_values_distinct():
     for base in (ntcb.SYNC_LEVEL, ntcb.SYNC_CHANNEL, ntcb.SYNC_MLP, ntcb.SYNC_END):
         v = {ntcb.sync_value(base, l, c) for l in range(4) for c in range(4 if base == ntcb.SYNC_CHANNEL else 1)}
         assert len(v) == (16 if base == ntcb.SYNC_CHANNEL else 4)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_post_hoc_grid_of_the_model_file_is_the_containers(case):
+    """decode.load's --q8 rule on the run's model file gives exactly the values its container holds"""
+    from neural_block_textures_amd import decode
+    m = decode.load(os.path.join(GOLDEN, f"ntcb_{case}_model.bin"))
+    n = ntcb.parse(raw(case)).to_model_file()
+    assert np.array_equal(m.z, n.z)
