@@ -154,6 +154,10 @@ void ntc_trainer_set_profiling_only(ntc_trainer* t, const char* names);
 int ntc_trainer_kernel_time(ntc_trainer* t, const char* name, double* total_ms, long long* launches);
 // 1 if the stage ("pop_eval", "lat_pair", "qat_search") runs on the FP32 matrix cores for this model, else 0
 int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage);
+/* on = 0: every stage of this trainer runs on the VALU kernels from the next call on (the matrix-core
+ * kernels' parity and speed are then measured against them); on = 1 (the default): the matrix cores
+ * take every stage whose shape they pay off for */
+void ntc_trainer_set_matrix_cores(ntc_trainer* t, int on);
 /* the device's Gaussian draws for indices index0 .. index0 + n - 1 of one (seed, stream, step, pair) */
 void ntc_trainer_debug_gauss(ntc_trainer* t, uint32_t stream, uint32_t step, uint32_t pair, uint64_t index0, size_t n,
                              float* out);

@@ -169,6 +169,8 @@ int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage) {
     return 0;
 }
 
+void ntc_trainer_set_matrix_cores(ntc_trainer* t, int on) { t->t.im->valu_only = on == 0; }
+
 int ntc_trainer_kernel_time(ntc_trainer* t, const char* name, double* total_ms, long long* launches) {
     auto& I = *t->t.im;
     ntc_hip::resolve_times(I);

@@ -85,10 +85,12 @@ __device__ __forceinline__ float out_of(float s, bool clamp) {
     return clamp ? __builtin_amdgcn_fmed3f(s + 0.5f, 0.0f, 1.0f) : sigmoid_hw2(s);
 }
 
-// Where a member's parameters come from: the weight sets of a central-difference step (wsets), or -
-// in an ES step - the block's own draw of the pair's Gaussians (NS_MLP, step, pair, k): both members'
-// weights w0 +- sigma eps (one fused operation each, main.cpp:1852-1856) go to LDS, and the chunk-0
-// block writes the Gaussians to eps for the update.
+// Where a member's parameters come from: the weight sets of a central-difference step (kSets), or -
+// in an ES step - both members' weights w0 +- sigma eps (one fused operation each, main.cpp:1852-1856)
+// staged in LDS, from the block's own draw of the pair's Gaussians (NS_MLP, step, pair, k; the chunk-0
+// block writes them to eps for the update: kDraw, for populations with one or two chunks per pair) or
+// from the Gaussians a separate kernel drew once for all chunks (kReadEps).
+enum PopFrom : int { kSets = 0, kDraw = 1, kReadEps = 2 };
 struct PopSource {
     const float* wsets;                    // central differences: 2 pairs x P
     NoiseFix nt; uint64_t seed; uint32_t step; float sigma;
@@ -99,11 +101,12 @@ struct PopSource {
 template <class S>
 constexpr int pop_occupancy() { return MfmaShape<S>::kH > 32 ? 2 : (MfmaShape<S>::kIn <= 8 ? 4 : 3); }
 
-template <class S, bool LeakUnit, bool Clamp, bool Es>
+template <class S, bool LeakUnit, bool Clamp, int From>
 __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_per_eu(pop_occupancy<S>()))) k_pop_mfma(DevModel m, PopSource src, int M, int Mcap,
                                                            int chunk, int chunks, const float* __restrict__ feat,
                                                            const float* __restrict__ btgt, double* __restrict__ part) {
     using Q = MfmaShape<S>;
+    constexpr bool Es = From != kSets;
     __shared__ double red[kPopWaves];
     __shared__ float wpm_s[Es ? 2 * Q::kP : 1];   // ES: the + member's weights, then the - member's
     const int lane = threadIdx.x & 63;
@@ -115,10 +118,16 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
         const uint64_t head = noise_head(src.seed, NS_MLP, src.step, (uint32_t)pair);
         float* eg = src.eps + (size_t)pair * Q::kP;
         for (int k = threadIdx.x; k < Q::kP; k += 64 * kPopWaves) {
-            const float e = gauss_at(src.nt, head, (uint64_t)k), w0 = src.w0[k];
+            float e;
+            if constexpr (From == kDraw) {
+                e = gauss_at(src.nt, head, (uint64_t)k);
+                if (ch == 0) eg[k] = e;
+            } else {
+                e = eg[k];
+            }
+            const float w0 = src.w0[k];
             wpm_s[k] = __builtin_fmaf(src.sigma, e, w0);
             wpm_s[Q::kP + k] = __builtin_fmaf(-src.sigma, e, w0);
-            if (ch == 0) eg[k] = e;
         }
         __syncthreads();
         mfma_load<S, false>(W, wpm_s + sgn * Q::kP, lane);
@@ -420,13 +429,14 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
 }
 
 bool qat_on_matrix_cores(const Impl& I) {
-    if (!I.lv0_unit_cells) return false;
+    if (!I.lv0_unit_cells || I.valu_only) return false;
     bool ok = false;
     dispatch_shape(I.dm, [&](auto s) { ok = MfmaShape<decltype(s)>::kOk; });
     return ok;
 }
 
 bool pop_on_matrix_cores(const Impl& I) {
+    if (I.valu_only) return false;
     bool ok = false;
     dispatch_shape(I.dm, [&](auto s) { ok = MfmaShape<decltype(s)>::kOk; });
     return ok;
@@ -442,9 +452,9 @@ int pop_chunk(const Impl& I, int pairs, int M) {
     return std::min(M, 1024);
 }
 
-template <class S, bool LeakUnit, bool Es>
+template <class S, bool LeakUnit, int From>
 static void launch_pop_mfma(Impl& I, const PopSource& src, int pairs, int M, int chunk, int chunks) {
-    auto kern = I.dm.clamp_out ? k_pop_mfma<S, LeakUnit, true, Es> : k_pop_mfma<S, LeakUnit, false, Es>;
+    auto kern = I.dm.clamp_out ? k_pop_mfma<S, LeakUnit, true, From> : k_pop_mfma<S, LeakUnit, false, From>;
     hipLaunchKernelGGL(kern, dim3(pairs, chunks), dim3(64 * kPopWaves), 0, I.stream, I.dm, src, M, I.Mcap, chunk, chunks, I.feat,
                        I.btgt, I.part);
 }
@@ -461,13 +471,13 @@ static void check_pop_launch(const Impl& I, int pairs, int chunk, int chunks) {
     }
 }
 
-template <bool Es>
+template <int From>
 static void launch_pop_matrix(Impl& I, const PopSource& src, int pairs, int M, int chunk, int chunks) {
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         if constexpr (MfmaShape<S>::kOk) {
-            if (I.dm.leak >= 0.0f && I.dm.leak <= 1.0f) launch_pop_mfma<S, true, Es>(I, src, pairs, M, chunk, chunks);
-            else launch_pop_mfma<S, false, Es>(I, src, pairs, M, chunk, chunks);
+            if (I.dm.leak >= 0.0f && I.dm.leak <= 1.0f) launch_pop_mfma<S, true, From>(I, src, pairs, M, chunk, chunks);
+            else launch_pop_mfma<S, false, From>(I, src, pairs, M, chunk, chunks);
         }
     });
     NTC_CHECK(hipGetLastError());
@@ -487,16 +497,20 @@ void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks) {
     check_pop_launch(I, pairs, chunk, chunks);
     PopSource src{};
     src.wsets = I.wsets;
-    launch_pop_matrix<false>(I, src, pairs, M, chunk, chunks);
+    launch_pop_matrix<kSets>(I, src, pairs, M, chunk, chunks);
 }
 
 void launch_pop_eval_es(Impl& I, int it, float sigma, int N, int M, int chunk, int chunks) {
-    ProfScope ps(I, "pop_eval");
     check_pop_launch(I, N, chunk, chunks);
     PopSource src{};
     src.nt = I.noise; src.seed = I.d.seed; src.step = (uint32_t)it; src.sigma = sigma;
     src.w0 = I.w; src.eps = I.eps_mlp;
-    launch_pop_matrix<true>(I, src, N, M, chunk, chunks);
+    // with three or more chunks per pair, the Gaussians are drawn once (not once per chunk)
+    const bool once = chunks >= 3;
+    if (once) launch_mlp_eps(I, it, N);
+    ProfScope ps(I, "pop_eval");
+    if (once) launch_pop_matrix<kReadEps>(I, src, N, M, chunk, chunks);
+    else launch_pop_matrix<kDraw>(I, src, N, M, chunk, chunks);
 }
 
 bool lat_pair_on_matrix_cores(const Impl& I) { return pop_on_matrix_cores(I); }

@@ -15,6 +15,12 @@
 // tile); the next layer wants lane group q to hold unit 4 ks + q. A 4 x 4 transpose across
 // (lane group, register) - two v_permlane32_swap and two v_permlane16_swap per 16-unit tile -
 // turns the activated D registers of tile t into the B operands of k-steps 4t .. 4t + 3.
+//
+// Hidden widths that are not a multiple of 16 pad the last tile with zero weights and biases. Its
+// rows are ordered so that the units sit in the first registers of the four lane groups (row 4g + r
+// holds unit 4r + g of the tile): the registers past the last unit hold padding only, and the next
+// layer skips their k-steps (36 units: 9 k-steps, not 12). Padded rows compute fma(0, x, 0) chains
+// and activate to zero, so the real units are unchanged.
 #pragma once
 #include "device_common.hpp"
 
@@ -27,17 +33,39 @@ struct MfmaShape { static constexpr bool kOk = false; };
 template <class S>
 struct MfmaShape<S, true> {
     static constexpr int kIn = S::kNin, kH = S::kH, kNL = S::kNL, kNout = S::kNout;
-    static constexpr bool kOk = kH % 16 == 0 && kNout <= 16 && kNL >= 1;
-    static constexpr int kKs1 = (kIn + 3) / 4;   // k-steps of the first layer (inputs padded with zeros)
-    static constexpr int kHt = kH / 16;          // 16-unit tiles of a hidden layer
-    static constexpr int kKsH = kH / 4;          // k-steps of a layer fed by a hidden layer
+    static constexpr int kHt = (kH + 15) / 16;            // 16-unit tiles of a hidden layer (the last one may be partial)
+    static constexpr int kLastU = kH - 16 * (kHt - 1);    // units of the last tile (1 .. 16)
+    static constexpr int kLastR = (kLastU + 3) / 4;       // its registers that hold units
+    static constexpr int kKs1 = (kIn + 3) / 4;            // k-steps of the first layer (inputs padded with zeros)
+    static constexpr int kKsH = 4 * (kHt - 1) + kLastR;   // k-steps of a layer fed by a hidden layer
     static constexpr int kDeep = kNL > 1 ? kNL - 1 : 1;
     static constexpr int kP = kH * kIn + kH + (kNL - 1) * (kH * kH + kH) + kNout * kH + kNout;   // parameters
+    // matrix instructions per 16-pixel tile, and the fraction of their multiply-adds that are the model's
+    static constexpr int kMfmaPerTile = kHt * kKs1 + (kNL - 1) * kHt * kKsH + kKsH;
+    static constexpr int kMacs = kIn * kH + (kNL - 1) * kH * kH + kH * kNout;
+    static constexpr double kUseful = (double)kMacs / (64.0 * kMfmaPerTile);
+    // the matrix cores take the shape when at least half of their multiply-adds are the model's (a
+    // matrix instruction does twice the multiply-adds per cycle of a VALU one); others run on the VALU
+    static constexpr bool kOk = kNout <= 16 && kNL >= 1 && kUseful >= 0.5;
+    // registers of hidden tile ot that hold units
+    static constexpr int regs(int ot) { return ot == kHt - 1 ? kLastR : 4; }
+    static constexpr bool partial(int ot) { return ot == kHt - 1 && kLastU < 16; }
 };
 
-// The hidden-layer input that lane group g feeds at k-step ks (see mfma_load).
-template <bool Exact>
-__device__ __forceinline__ int hidden_input(int ks, int g) { return Exact ? 4 * ks + g : 16 * (ks >> 2) + 4 * g + (ks & 3); }
+// The unit in row i of hidden tile ot (a partial last tile: row 4g + r holds unit 4r + g of the tile).
+template <class Q>
+__host__ __device__ constexpr int unit_of(int ot, int i) { return Q::partial(ot) ? 16 * ot + 4 * (i & 3) + (i >> 2) : 16 * ot + i; }
+
+// The hidden-layer input that lane group g feeds at k-step ks. Exact: the inputs in ascending order
+// (k-step ks = inputs 4 ks .. 4 ks + 3; the activations are transposed to match). Otherwise the
+// register of the previous layer's D layout as it stands: k-step 4 t + r takes register r of tile t,
+// which lane group g holds as unit_of(t, 4 g + r).
+template <class Q, bool Exact>
+__host__ __device__ constexpr int hidden_input(int ks, int g) {
+    if (Exact) return 4 * ks + g;
+    const int t = (ks >> 2) < Q::kHt - 1 ? (ks >> 2) : Q::kHt - 1;
+    return unit_of<Q>(t, 4 * g + (ks - 4 * t));
+}
 
 // One member's parameters in operand layout.
 template <class S>
@@ -54,38 +82,53 @@ struct MfmaWeights {
 // Gathers a member's flat parameter vector (per layer W[out][in] row-major, then b[out]) into
 // operand layout; lane = threadIdx.x % 64. Exact: the k-steps of a layer fed by a hidden layer take
 // the inputs in ascending order (k-step ks = inputs 4 ks .. 4 ks + 3; the activations are transposed
-// to match). Otherwise k-step 4 t + r takes inputs 16 t + 4 q + r (q = 0..3), the order in which a
-// 16-unit tile's D registers hold them, and the activations feed the next layer untransposed: the
-// same products, summed in another order.
+// to match). Otherwise k-step 4 t + r takes the inputs in the order in which register r of hidden
+// tile t holds them across the lane groups, and the activations feed the next layer untransposed:
+// the same products, summed in another order. Padding units and inputs get zero weights.
 template <class S, bool Exact, class Get>
 __device__ __forceinline__ void mfma_load_from(MfmaWeights<S>& W, const Get& w, int lane) {
     using Q = MfmaShape<S>;
+    static_assert(!Exact || Q::kLastU == 16, "the ascending-order layout needs whole 16-unit tiles");
     constexpr int NIN = Q::kIn, H = Q::kH, NO = Q::kNout;
     const int i16 = lane & 15, g = lane >> 4;
 #pragma unroll
     for (int ot = 0; ot < Q::kHt; ot++) {
+        const int u = unit_of<Q>(ot, i16);
 #pragma unroll
         for (int ks = 0; ks < Q::kKs1; ks++) {
             const int in = 4 * ks + g;
-            W.a1[ot][ks] = in < NIN ? w((16 * ot + i16) * NIN + in) : 0.0f;
+            W.a1[ot][ks] = (in < NIN && u < H) ? w(u * NIN + in) : 0.0f;
         }
 #pragma unroll
-        for (int r = 0; r < 4; r++) W.c1[ot][r] = w(H * NIN + 16 * ot + 4 * g + r);
+        for (int r = 0; r < 4; r++) {
+            const int ur = unit_of<Q>(ot, 4 * g + r);
+            W.c1[ot][r] = ur < H ? w(H * NIN + ur) : 0.0f;
+        }
     }
     int p = H * NIN + H;
 #pragma unroll
     for (int l = 0; l < Q::kNL - 1; l++) {
 #pragma unroll
         for (int ot = 0; ot < Q::kHt; ot++) {
+            const int u = unit_of<Q>(ot, i16);
 #pragma unroll
-            for (int ks = 0; ks < Q::kKsH; ks++) W.ah[l][ot][ks] = w(p + (16 * ot + i16) * H + hidden_input<Exact>(ks, g));
+            for (int ks = 0; ks < Q::kKsH; ks++) {
+                const int in = hidden_input<Q, Exact>(ks, g);
+                W.ah[l][ot][ks] = (u < H && in < H) ? w(p + u * H + in) : 0.0f;
+            }
 #pragma unroll
-            for (int r = 0; r < 4; r++) W.ch[l][ot][r] = w(p + H * H + 16 * ot + 4 * g + r);
+            for (int r = 0; r < 4; r++) {
+                const int ur = unit_of<Q>(ot, 4 * g + r);
+                W.ch[l][ot][r] = ur < H ? w(p + H * H + ur) : 0.0f;
+            }
         }
         p += H * H + H;
     }
 #pragma unroll
-    for (int ks = 0; ks < Q::kKsH; ks++) W.ao[ks] = i16 < NO ? w(p + i16 * H + hidden_input<Exact>(ks, g)) : 0.0f;
+    for (int ks = 0; ks < Q::kKsH; ks++) {
+        const int in = hidden_input<Q, Exact>(ks, g);
+        W.ao[ks] = (i16 < NO && in < H) ? w(p + i16 * H + in) : 0.0f;
+    }
 #pragma unroll
     for (int r = 0; r < 4; r++) W.co[r] = 4 * g + r < NO ? w(p + NO * H + 4 * g + r) : 0.0f;
 }
@@ -181,11 +224,11 @@ __device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const floa
 #pragma unroll
             for (int ot = 0; ot < Q::kHt; ot++) {
 #pragma unroll
-                for (int r = 0; r < 4; r++) acc[u][ot][r] = act<LeakUnit>(acc[u][ot][r], leak);
+                for (int r = 0; r < Q::regs(ot); r++) acc[u][ot][r] = act<LeakUnit>(acc[u][ot][r], leak);
                 if constexpr (Exact) transpose4(acc[u][ot], x[u] + 4 * ot);
                 else {
 #pragma unroll
-                    for (int r = 0; r < 4; r++) x[u][4 * ot + r] = acc[u][ot][r];
+                    for (int r = 0; r < Q::regs(ot); r++) x[u][4 * ot + r] = acc[u][ot][r];
                 }
             }
     }
@@ -207,11 +250,11 @@ __device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const floa
 #pragma unroll
             for (int ot = 0; ot < Q::kHt; ot++) {
 #pragma unroll
-                for (int r = 0; r < 4; r++) acc[u][ot][r] = act<LeakUnit>(acc[u][ot][r], leak);
+                for (int r = 0; r < Q::regs(ot); r++) acc[u][ot][r] = act<LeakUnit>(acc[u][ot][r], leak);
                 if constexpr (Exact) transpose4(acc[u][ot], x[u] + 4 * ot);
                 else {
 #pragma unroll
-                    for (int r = 0; r < 4; r++) x[u][4 * ot + r] = acc[u][ot][r];
+                    for (int r = 0; r < Q::regs(ot); r++) x[u][4 * ot + r] = acc[u][ot][r];
                 }
             }
     }

@@ -18,6 +18,13 @@ using ShapeDct17 = FixedShape<1, 4, 0, 1, 17, 2, 3>;      // 1-channel DCT plane
 using ShapeDct2x17 = FixedShape<2, 4, 0, 1, 17, 2, 3>;    // 2-channel DCT plane + 4 channels, 17,17 (8-17-17-3)
 using ShapeDct11 = FixedShape<1, 4, 0, 1, 11, 2, 3>;      // 7-11-11-3
 using ShapeDct7 = FixedShape<1, 4, 0, 1, 7, 2, 3>;        // 7-7-7-3
+// the reference's published GPU training runs (README.md:358, 382, 531, 956, 1119): selector planes
+// with --qat, a nearest block latent, --pos lv1local, 36,36 or 27,27
+using ShapeChief1 = FixedShape<1, 2, 0, 1, 36, 2, 3>;     // chief1 --qat 2, 512x512x1 + 128x128x2 (5-36-36-3)
+using ShapeMatQat = FixedShape<2, 4, 0, 1, 36, 2, 12>;    // 4 maps --qat 2, 512x512x2 + 128x128x4 (8-36-36-12)
+using ShapeChief31 = FixedShape<2, 4, 0, 1, 36, 2, 3>;    // chief1 --qat 3,1, 512x512x2 + 128x128x4 (8-36-36-3)
+using ShapeMat3x2 = FixedShape<3, 4, 0, 1, 36, 2, 12>;    // 4 maps, three 2-bit selector channels (9-36-36-12)
+using ShapeImage3 = FixedShape<1, 4, 0, 1, 27, 2, 3>;     // --block 8 --qat 4 --qes 8, 27,27 (7-27-27-3)
 
 template <class F>
 inline const char* dispatch_shape(const DevModel& m, F&& f) {
@@ -32,6 +39,11 @@ inline const char* dispatch_shape(const DevModel& m, F&& f) {
     if (ShapeDct2x17::matches(m)) { f(ShapeDct2x17{}); return "2+4|uv|17x2|3"; }
     if (ShapeDct11::matches(m)) { f(ShapeDct11{}); return "1+4|uv|11x2|3"; }
     if (ShapeDct7::matches(m)) { f(ShapeDct7{}); return "1+4|uv|7x2|3"; }
+    if (ShapeChief1::matches(m)) { f(ShapeChief1{}); return "1+2|uv|36x2|3"; }
+    if (ShapeMatQat::matches(m)) { f(ShapeMatQat{}); return "2+4|uv|36x2|12"; }
+    if (ShapeChief31::matches(m)) { f(ShapeChief31{}); return "2+4|uv|36x2|3"; }
+    if (ShapeMat3x2::matches(m)) { f(ShapeMat3x2{}); return "3+4|uv|36x2|12"; }
+    if (ShapeImage3::matches(m)) { f(ShapeImage3{}); return "1+4|uv|27x2|3"; }
     f(RuntimeShape{});
     return "runtime";
 }

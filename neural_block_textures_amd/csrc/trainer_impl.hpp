@@ -80,6 +80,7 @@ struct ntc_cuda::Trainer::Impl {
     float* qat_grid = nullptr; // 9 x 257
     int* qat_bits = nullptr;   // MAX_CH
     bool lv0_unit_cells = false;   // level 0 nearest at the image's size: every texel's cell is its own pixel
+    bool valu_only = false;        // instrumentation: every stage on the VALU kernels (ntc_trainer_set_matrix_cores)
 
     bool qes = false;
     ntc_cuda::QesDesc* qes_dev = nullptr;
@@ -142,6 +143,8 @@ std::vector<uint32_t> noise_fix_summary(const std::vector<uint32_t>& fix);
 void launch_fill(Impl& I, float* p, size_t n, float v);
 void launch_batch(Impl& I, int it, int M);
 void launch_perturb(Impl& I, int it, float sigma, int N);
+// the Gaussians of one ES step (NS_MLP, it, pair, k) into eps_mlp, N x P
+void launch_mlp_eps(Impl& I, int it, int N);
 void launch_fd_sets(Impl& I, float h);
 // which stages run on the matrix cores for this trainer's model
 bool pop_on_matrix_cores(const Impl& I);

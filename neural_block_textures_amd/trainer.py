@@ -103,6 +103,7 @@ def library() -> C.CDLL:
             "ntc_trainer_set_profiling_only": (None, [P, C.c_char_p]),
             "ntc_trainer_kernel_time": (C.c_int, [P, C.c_char_p, P, P]),
             "ntc_trainer_on_matrix_cores": (C.c_int, [P, C.c_char_p]),
+            "ntc_trainer_set_matrix_cores": (None, [P, C.c_int]),
             "ntc_trainer_dct_probe": (None, [P, P, P]),
             "ntc_trainer_dct_refit": (None, [P, P]),
             "ntc_trainer_decode_error": (None, [P, P, C.c_int, C.c_int, P, P]),
@@ -418,6 +419,10 @@ class Trainer:
     def on_matrix_cores(self, stage: str) -> bool:
         """whether the stage ("pop_eval", "lat_pair", "qat_search") runs on the FP32 matrix cores"""
         return bool(self._lib.ntc_trainer_on_matrix_cores(self._h, stage.encode()))
+
+    def set_matrix_cores(self, on: bool):
+        """on=False: every stage on the VALU kernels from the next call on (instrumentation)"""
+        self._lib.ntc_trainer_set_matrix_cores(self._h, 1 if on else 0)
 
     def kernel_time(self, name):
         ms, n = C.c_double(), C.c_longlong()

@@ -20,7 +20,18 @@ LAYOUTS = {
     "large": Layout(48, 48, [(24, 24, 4, False), (6, 6, 8, False)], [64, 64], T=4, leak=0.0),
     "runtime": Layout(50, 38, [(13, 10, 3, True), (5, 4, 4, False), (3, 3, 2, False)], [20, 12], T=2,
                       pos=[PK_LV1LOCAL, PK_UV], leak=0.02, clamp_out=True, weights=[1.0, 3.0]),
+    # the reference's published runs (README.md:358, 382, 531): selector plane, nearest block latent,
+    # lv1local, hidden widths that pad the matrix tiles (36 -> 48, 27 -> 32)
+    "chief1_36": Layout(64, 48, [(64, 48, 1, True), (16, 12, 2, True)], [36, 36], pos=[PK_LV1LOCAL], leak=1 / 1024),
+    "mat_qat_36": Layout(48, 40, [(48, 40, 2, True), (12, 10, 4, True)], [36, 36], T=4, pos=[PK_LV1LOCAL],
+                         leak=1 / 1024, weights=[1.0, 2.0, 0.5, 1.5]),
+    "image3_27": Layout(64, 48, [(64, 48, 1, True), (8, 6, 4, False)], [27, 27], pos=[PK_LV1LOCAL], leak=1 / 1024),
 }
+# the same layouts with every stage forced onto the VALU kernels (ntc_trainer_set_matrix_cores(0))
+for _name in ("material", "chief1_36"):
+    _lay = Layout(**{k: getattr(LAYOUTS[_name], k) for k in LAYOUTS[_name].__dataclass_fields__})
+    _lay.valu_only = True
+    LAYOUTS[_name + "_valu"] = _lay
 
 
 def say(*a):
@@ -41,6 +52,8 @@ def trainer(layout: Layout, z, p, tgt, *, max_pairs=64, max_batch=4096, seed=5, 
     tr = Trainer()
     d = Trainer.model_desc(layout, max_pairs=max_pairs, max_batch=max_batch, seed=seed, **kw)
     tr.init(d, z, p, tgt, layout)
+    if getattr(layout, "valu_only", False):
+        tr.set_matrix_cores(False)
     return tr
 
 

@@ -83,7 +83,7 @@ def test_mlp_es_step(orc, name):
     assert abs(loss - 0.5 * (lp + lm).mean()) < 1e-12 and dstd > 0
 
 
-@pytest.mark.parametrize("name", ["rgb_16x2", "material", "runtime"])
+@pytest.mark.parametrize("name", ["rgb_16x2", "material", "runtime", "chief1_36", "material_valu"])
 def test_mlp_es_two_steps_and_fd(orc, name):
     lay = LAYOUTS[name]
     say("mlp es+fd", name)
@@ -138,7 +138,8 @@ def test_latent_step(orc, name):
     assert np.abs(tr.debug_last_zgrad() - g2_o).max() < 1e-3 * np.sqrt((g2_o.astype(np.float64) ** 2).mean())
 
 
-QAT = {"material": [2, 3], "dct_plane": [1], "runtime": [2, 1, 3]}
+QAT = {"material": [2, 3], "dct_plane": [1], "runtime": [2, 1, 3], "chief1_36": [2], "mat_qat_36": [2, 2], "image3_27": [4],
+       "material_valu": [2, 3], "chief1_36_valu": [2]}
 
 
 @pytest.mark.parametrize("name", list(QAT))
