@@ -28,6 +28,10 @@ namespace ntc_hip {
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
+#ifndef NTC_MFMA_MIN_USEFUL
+#define NTC_MFMA_MIN_USEFUL 0.5
+#endif
+
 template <class S, bool = S::kFixed>
 struct MfmaShape { static constexpr bool kOk = false; };
 template <class S>
@@ -46,7 +50,7 @@ struct MfmaShape<S, true> {
     static constexpr double kUseful = (double)kMacs / (64.0 * kMfmaPerTile);
     // the matrix cores take the shape when at least half of their multiply-adds are the model's (a
     // matrix instruction does twice the multiply-adds per cycle of a VALU one); others run on the VALU
-    static constexpr bool kOk = kNout <= 16 && kNL >= 1 && kUseful >= 0.5;
+    static constexpr bool kOk = kNout <= 16 && kNL >= 1 && kUseful >= NTC_MFMA_MIN_USEFUL;
     // registers of hidden tile ot that hold units
     static constexpr int regs(int ot) { return ot == kHt - 1 ? kLastR : 4; }
     static constexpr bool partial(int ot) { return ot == kHt - 1 && kLastU < 16; }
