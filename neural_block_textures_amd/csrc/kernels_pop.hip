@@ -1,13 +1,15 @@
 // The population evaluation (MlpTrainer::step's member losses, main.cpp:1848-1861) on the FP32
-// matrix cores of gfx950, for the fixed shapes whose hidden width is a multiple of 16; other
-// shapes use the VALU kernel of kernels_mlp.hip. In an ES step the kernel draws the pair's
-// perturbation itself (no member weight sets in memory).
+// matrix cores of gfx950, for the fixed shapes the matrix cores pay off for (MfmaShape::kOk) and
+// 0 <= leak <= 1; other models use the VALU kernel of kernels_mlp.hip. In an ES step the kernel
+// stages the pair's perturbed weights itself (no member weight sets in memory).
 //
 // On this chip an FP32 matrix instruction and a VALU instruction do not run concurrently on a
 // SIMD (a 16x16x4 f32 step costs 32 cycles, a VALU instruction 4, and their mixes take the sum),
 // so everything around the matrix operations is counted in instructions: the activation is one
-// v_max_f32 (this file is compiled with relaxed NaN handling and the IEEE mode bit off, so the
-// maximum needs no canonicalising copies); a hidden layer's outputs feed the next layer in the order
+// instruction (kActZero's v_max_f32, or kActFold's fused multiply-add on hidden layers whose weights
+// were scaled by (1 + leak) / 2 when the member's weights were staged; this file is compiled with
+// relaxed NaN handling and the IEEE mode bit off, so a maximum needs no canonicalising copies); a
+// hidden layer's outputs feed the next layer in the order
 // the matrix instruction leaves them (no transpose; each unit's sum takes its inputs in another
 // order than the reference's ascending one); the sigmoid is the hardware exp2 and reciprocal, its
 // -log2(e) folded into the output layer; a lane's channel terms cw d d are fused multiply-adds in float
@@ -101,7 +103,7 @@ struct PopSource {
 template <class S>
 constexpr int pop_occupancy() { return MfmaShape<S>::kH > 32 ? 2 : (MfmaShape<S>::kIn <= 8 ? 4 : 3); }
 
-template <class S, bool LeakUnit, bool Clamp, int From>
+template <class S, int Act, bool Clamp, int From>
 __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_per_eu(pop_occupancy<S>()))) k_pop_mfma(DevModel m, PopSource src, int M, int Mcap,
                                                            int chunk, int chunks, const float* __restrict__ feat,
                                                            const float* __restrict__ btgt, double* __restrict__ part) {
@@ -135,6 +137,8 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
         mfma_load<S, false>(W, src.wsets + (size_t)(2 * pair + sgn) * Q::kP, lane);
     }
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
+    if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
+    const float ak = act_k(Act, m.leak);
     constexpr bool kPack = pop_pack<S>();
     // the channel weight of each of this lane's output registers (rows 4 g + r; packed: rows r of
     // lane group g's tile, groups 2 and 3 unused), zero past the last output
@@ -174,7 +178,7 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
                 if (4 * (Q::kKs1 - 1) + g >= Q::kIn) c.b1[u][Q::kKs1 - 1] = 0.0f;
         }
         f4v o[U];
-        mfma_forward<S, U, LeakUnit, false>(W, c.b1, m.leak, o);
+        mfma_forward<S, U, Act, false>(W, c.b1, ak, o);
         if constexpr (kPack) {
             // lane group 0 of each tile holds its outputs: tile 1's move to lane group 1
             f4v op;
@@ -252,7 +256,7 @@ template <class S>
 constexpr int lat_pix() { return MfmaShape<S>::kIn <= 8 ? 512 : 256; }
 
 
-template <class S, bool LeakUnit, bool Clamp>
+template <class S, int Act, bool Clamp>
 __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* __restrict__ w, const float* __restrict__ zdec,
                                                       const float* __restrict__ eps, const float* __restrict__ tgt, float sg,
                                                       unsigned mask, float* __restrict__ dpix) {
@@ -268,6 +272,8 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     MfmaWeights<S> W;
     mfma_load<S, false>(W, w, lane);
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
+    if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
+    const float ak = act_k(Act, m.leak);
     float cw[4];
     if constexpr (kPack) {
 #pragma unroll
@@ -314,7 +320,7 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
 #pragma unroll
             for (int ks = 0; ks < Q::kKs1; ks++) { b1[0][ks] = bp[t][ks]; b1[1][ks] = bm[t][ks]; }
             f4v o[2];
-            mfma_forward<S, 2, LeakUnit, false>(W, b1, m.leak, o);
+            mfma_forward<S, 2, Act, false>(W, b1, ak, o);
             const int p = base + 16 * t + i16;
             if constexpr (kPack) {
                 float ev = 0.0f;   // group 0: e+, group 1: e-
@@ -405,8 +411,8 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                     for (int ks = 0; ks < Q::kKs1; ks++) b2[v][ks] = b[t][ks];
                 if (g == c % 4) { b2[0][c / 4] = gv[kc]; b2[1][c / 4] = gv[kc + 1]; }
                 f4v o[2];
-                if (unit_leak) mfma_forward<S, 2, true, false>(W, b2, m.leak, o);
-                else mfma_forward<S, 2, false, false>(W, b2, m.leak, o);
+                if (unit_leak) mfma_forward<S, 2, kActMax, false>(W, b2, m.leak, o);
+                else mfma_forward<S, 2, kActAny, false>(W, b2, m.leak, o);
 #pragma unroll
                 for (int v = 0; v < 2; v++) {
                     double l = 0.0;   // this lane's channels in ascending order, then the pixel's lanes
@@ -435,8 +441,9 @@ bool qat_on_matrix_cores(const Impl& I) {
     return ok;
 }
 
+// the population and latent-pair evaluations on the matrix cores take 0 <= leak <= 1 (kActZero, kActFold)
 bool pop_on_matrix_cores(const Impl& I) {
-    if (I.valu_only) return false;
+    if (I.valu_only || !(I.dm.leak >= 0.0f && I.dm.leak <= 1.0f)) return false;
     bool ok = false;
     dispatch_shape(I.dm, [&](auto s) { ok = MfmaShape<decltype(s)>::kOk; });
     return ok;
@@ -452,9 +459,9 @@ int pop_chunk(const Impl& I, int pairs, int M) {
     return std::min(M, 1024);
 }
 
-template <class S, bool LeakUnit, int From>
+template <class S, int Act, int From>
 static void launch_pop_mfma(Impl& I, const PopSource& src, int pairs, int M, int chunk, int chunks) {
-    auto kern = I.dm.clamp_out ? k_pop_mfma<S, LeakUnit, true, From> : k_pop_mfma<S, LeakUnit, false, From>;
+    auto kern = I.dm.clamp_out ? k_pop_mfma<S, Act, true, From> : k_pop_mfma<S, Act, false, From>;
     hipLaunchKernelGGL(kern, dim3(pairs, chunks), dim3(64 * kPopWaves), 0, I.stream, I.dm, src, M, I.Mcap, chunk, chunks, I.feat,
                        I.btgt, I.part);
 }
@@ -476,8 +483,11 @@ static void launch_pop_matrix(Impl& I, const PopSource& src, int pairs, int M, i
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         if constexpr (MfmaShape<S>::kOk) {
-            if (I.dm.leak >= 0.0f && I.dm.leak <= 1.0f) launch_pop_mfma<S, true, From>(I, src, pairs, M, chunk, chunks);
-            else launch_pop_mfma<S, false, From>(I, src, pairs, M, chunk, chunks);
+            // central differences compare members one weight apart (w_j +- h): their activations are the
+            // reference's bit for bit; the ES members (w +- sigma eps) take the one-instruction folded form
+            if (I.dm.leak == 0.0f) launch_pop_mfma<S, kActZero, From>(I, src, pairs, M, chunk, chunks);
+            else if constexpr (From == kSets) launch_pop_mfma<S, kActMax, From>(I, src, pairs, M, chunk, chunks);
+            else launch_pop_mfma<S, kActFold, From>(I, src, pairs, M, chunk, chunks);
         }
     });
     NTC_CHECK(hipGetLastError());
@@ -515,9 +525,9 @@ void launch_pop_eval_es(Impl& I, int it, float sigma, int N, int M, int chunk, i
 
 bool lat_pair_on_matrix_cores(const Impl& I) { return pop_on_matrix_cores(I); }
 
-template <class S, bool LeakUnit>
+template <class S, int Act>
 static void launch_lat_mfma(Impl& I, int K, float sigma, unsigned mask) {
-    auto kern = I.dm.clamp_out ? k_lat_pair_mfma<S, LeakUnit, true> : k_lat_pair_mfma<S, LeakUnit, false>;
+    auto kern = I.dm.clamp_out ? k_lat_pair_mfma<S, Act, true> : k_lat_pair_mfma<S, Act, false>;
     constexpr int kLatPix = lat_pix<S>();
     hipLaunchKernelGGL(kern, dim3((unsigned)((I.npix + kLatPix - 1) / kLatPix), K), dim3(256), 0, I.stream, I.dm, I.w, I.zdec,
                        I.eps_lat, I.tgt, sigma, mask, I.dpix);
@@ -532,8 +542,8 @@ void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask) {
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         if constexpr (MfmaShape<S>::kOk) {
-            if (I.dm.leak >= 0.0f && I.dm.leak <= 1.0f) launch_lat_mfma<S, true>(I, K, sigma, mask);
-            else launch_lat_mfma<S, false>(I, K, sigma, mask);
+            if (I.dm.leak == 0.0f) launch_lat_mfma<S, kActZero>(I, K, sigma, mask);
+            else launch_lat_mfma<S, kActFold>(I, K, sigma, mask);
         }
     });
     NTC_CHECK(hipGetLastError());

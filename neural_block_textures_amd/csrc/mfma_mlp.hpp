@@ -193,21 +193,57 @@ __device__ __forceinline__ void tiles_of(const float (&f)[S::kMaxIn], float (&b)
     }
 }
 
-// The activation of main.cpp:560, x > 0 ? x : leak x. For 0 <= leak <= 1 this is max(x, leak x)
-// bit for bit (also for signed zeros and NaN), one instruction fewer.
-template <bool LeakUnit>
-__device__ __forceinline__ float act(float x, float leak) {
-    if constexpr (LeakUnit) return fmaxf(x, leak * x);
-    else return x > 0.0f ? x : leak * x;
+// How a kernel applies the activation of main.cpp:560, x > 0 ? x : leak x, to the matrix results.
+enum ActMode : int {
+    kActAny = 0,    // any leak: a compare and a select
+    kActMax = 1,    // 0 <= leak <= 1: max(x, leak x), bit for bit (also for signed zeros), one multiply and one maximum
+    kActZero = 2,   // leak = 0: max(x, -0), one instruction (x > 0: x, otherwise a zero)
+    kActFold = 3,   // 0 < leak <= 1, with every hidden layer's weights and biases scaled by b = (1 + leak) / 2
+                    // (scale_hidden): x' = b x and act = x' + c |x'| with c = (1 - leak) / (1 + leak), one fused
+                    // multiply-add with an absolute-value operand - x for x > 0, leak x otherwise, within two
+                    // roundings of the reference's value
+};
+// k: leak (kActAny, kActMax) or c (kActFold)
+template <int Act>
+__device__ __forceinline__ float act(float x, float k) {
+    if constexpr (Act == kActMax) return fmaxf(x, k * x);
+    else if constexpr (Act == kActZero) return fmaxf(x, -0.0f);
+    else if constexpr (Act == kActFold) return __builtin_fmaf(k, __builtin_fabsf(x), x);
+    else return x > 0.0f ? x : k * x;
+}
+// the activation constant k of act<Act> for a model's leak, and the hidden layers' weight scale b of kActFold
+__host__ __device__ inline float act_k(int mode, float leak) { return mode == kActFold ? (1.0f - leak) / (1.0f + leak) : leak; }
+__host__ __device__ inline float fold_scale(float leak) { return 0.5f * (1.0f + leak); }
+
+// Every hidden layer's weights and biases times b (kActFold).
+template <class S>
+__device__ __forceinline__ void scale_hidden(MfmaWeights<S>& W, float b) {
+    using Q = MfmaShape<S>;
+#pragma unroll
+    for (int ot = 0; ot < Q::kHt; ot++) {
+#pragma unroll
+        for (int ks = 0; ks < Q::kKs1; ks++) W.a1[ot][ks] *= b;
+#pragma unroll
+        for (int r = 0; r < 4; r++) W.c1[ot][r] *= b;
+    }
+#pragma unroll
+    for (int l = 0; l < Q::kNL - 1; l++)
+#pragma unroll
+        for (int ot = 0; ot < Q::kHt; ot++) {
+#pragma unroll
+            for (int ks = 0; ks < Q::kKsH; ks++) W.ah[l][ot][ks] *= b;
+#pragma unroll
+            for (int r = 0; r < 4; r++) W.ch[l][ot][r] *= b;
+        }
 }
 
 // U independent 16-pixel tiles through the MLP (interleaved, so one tile's activations overlap
 // the other's matrix operations): b1[u] = the first layer's B operands of tile u (input 4 ks + l / 16
 // of pixel l % 16, zero past nin); returns the output layer's pre-activations of each tile in D layout
 // (lane l, register r = output 4 (l / 16) + r of pixel l % 16). Every lane of the wave must be active.
-// Exact must match the weights' mfma_load.
-template <class S, int U, bool LeakUnit, bool Exact = true>
-__device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const float (&b1)[U][MfmaShape<S>::kKs1], float leak,
+// Exact must match the weights' mfma_load; k is act_k(Act, leak).
+template <class S, int U, int Act, bool Exact = true>
+__device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const float (&b1)[U][MfmaShape<S>::kKs1], float k,
                                              f4v (&o)[U]) {
     using Q = MfmaShape<S>;
     float x[U][Q::kKsH];
@@ -228,7 +264,7 @@ __device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const floa
 #pragma unroll
             for (int ot = 0; ot < Q::kHt; ot++) {
 #pragma unroll
-                for (int r = 0; r < Q::regs(ot); r++) acc[u][ot][r] = act<LeakUnit>(acc[u][ot][r], leak);
+                for (int r = 0; r < Q::regs(ot); r++) acc[u][ot][r] = act<Act>(acc[u][ot][r], k);
                 if constexpr (Exact) transpose4(acc[u][ot], x[u] + 4 * ot);
                 else {
 #pragma unroll
@@ -254,7 +290,7 @@ __device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const floa
 #pragma unroll
             for (int ot = 0; ot < Q::kHt; ot++) {
 #pragma unroll
-                for (int r = 0; r < Q::regs(ot); r++) acc[u][ot][r] = act<LeakUnit>(acc[u][ot][r], leak);
+                for (int r = 0; r < Q::regs(ot); r++) acc[u][ot][r] = act<Act>(acc[u][ot][r], k);
                 if constexpr (Exact) transpose4(acc[u][ot], x[u] + 4 * ot);
                 else {
 #pragma unroll
