@@ -25,6 +25,13 @@ using ShapeMatQat = FixedShape<2, 4, 0, 1, 36, 2, 12>;    // 4 maps --qat 2, 512
 using ShapeChief31 = FixedShape<2, 4, 0, 1, 36, 2, 3>;    // chief1 --qat 3,1, 512x512x2 + 128x128x4 (8-36-36-3)
 using ShapeMat3x2 = FixedShape<3, 4, 0, 1, 36, 2, 12>;    // 4 maps, three 2-bit selector channels (9-36-36-12)
 using ShapeImage3 = FixedShape<1, 4, 0, 1, 27, 2, 3>;     // --block 8 --qat 4 --qes 8, 27,27 (7-27-27-3)
+// the other command lines of the reference's README (README.md:274, 298, 990, 991, 1121, 1123)
+using ShapeQat1x4 = FixedShape<1, 4, 0, 1, 36, 2, 3>;     // --qat 2 plane + 4-channel block latent, 36,36 (7-36-36-3)
+using ShapeMatQat1x4 = FixedShape<1, 4, 0, 1, 36, 2, 12>; // the same for the 4-texture material (7-36-36-12)
+using ShapeRun8 = FixedShape<8, 0, 0, 1, 24, 2, 3>;       // --latent 128 128 8, default 24,24 (10-24-24-3)
+using ShapeRun8x3 = FixedShape<8, 4, 0, 1, 24, 2, 9>;     // 3 textures, --latent 128 128 8 --latent2 64 64 4 (14-24-24-9)
+using ShapeQes17 = FixedShape<4, 4, 0, 1, 17, 2, 3>;      // --qes 6,8 on two bilinear levels, 17,17 (10-17-17-3)
+using ShapeDct2x27 = FixedShape<2, 4, 0, 1, 27, 2, 3>;    // two DCT-coded channels, 27,27 (8-27-27-3)
 
 template <class F>
 inline const char* dispatch_shape(const DevModel& m, F&& f) {
@@ -44,6 +51,12 @@ inline const char* dispatch_shape(const DevModel& m, F&& f) {
     if (ShapeChief31::matches(m)) { f(ShapeChief31{}); return "2+4|uv|36x2|3"; }
     if (ShapeMat3x2::matches(m)) { f(ShapeMat3x2{}); return "3+4|uv|36x2|12"; }
     if (ShapeImage3::matches(m)) { f(ShapeImage3{}); return "1+4|uv|27x2|3"; }
+    if (ShapeQat1x4::matches(m)) { f(ShapeQat1x4{}); return "1+4|uv|36x2|3"; }
+    if (ShapeMatQat1x4::matches(m)) { f(ShapeMatQat1x4{}); return "1+4|uv|36x2|12"; }
+    if (ShapeRun8::matches(m)) { f(ShapeRun8{}); return "8|uv|24x2|3"; }
+    if (ShapeRun8x3::matches(m)) { f(ShapeRun8x3{}); return "8+4|uv|24x2|9"; }
+    if (ShapeQes17::matches(m)) { f(ShapeQes17{}); return "4+4|uv|17x2|3"; }
+    if (ShapeDct2x27::matches(m)) { f(ShapeDct2x27{}); return "2+4|uv|27x2|3"; }
     f(RuntimeShape{});
     return "runtime";
 }

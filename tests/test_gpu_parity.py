@@ -139,7 +139,7 @@ def test_latent_step(orc, name):
 
 
 QAT = {"material": [2, 3], "dct_plane": [1], "runtime": [2, 1, 3], "chief1_36": [2], "mat_qat_36": [2, 2], "image3_27": [4],
-       "material_valu": [2, 3], "chief1_36_valu": [2]}
+       "material_valu": [2, 3], "chief1_36_valu": [2], "mat_qat1x4_36": [2]}
 
 
 @pytest.mark.parametrize("name", list(QAT))
