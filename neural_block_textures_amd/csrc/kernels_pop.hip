@@ -358,13 +358,15 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
 // of the image's size (each texel's cell is its own pixel): wave = 64 pixels in four 16-pixel tiles.
 // Every lane builds the features of its own pixel (features<S>) and tiles_of turns them into the four
 // tiles' B operands. Per channel and tile, every candidate value is one MLP evaluation of the tile with
-// that feature replaced (two candidates at a time), the pixel's loss the double sum of the float terms
-// of loss_subset over its channels (a lane's four in ascending order, then the pixel's four lanes
-// pairwise, the same value in each of them). The choice is the reference's: the current grid value
-// first, then every other value with strict <, so the first strictly smaller loss wins
+// that feature replaced (two candidates at a time). The choice is the reference's: the current grid
+// value first, then every other value with strict <, so the first strictly smaller loss wins
 // (main.cpp:2101-2132). The winner enters the features of the next channel and is written to the
-// decode buffer.
-template <class S>
+// decode buffer. A candidate's loss is the pixel's float sum of cw (d d) over its channels (a lane's
+// four, then the pixel's four lanes pairwise, the same value in each of them) with the hidden
+// activation of act<Act>: the reference adds the float terms in double with its own activation, so a
+// choice can differ from the reference's only between candidates whose losses agree to a few float
+// roundings (the reference's own check accepts such rounding ties, main.cpp:3143-3144).
+template <class S, int Act>
 __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __restrict__ w, float* __restrict__ zdec,
                                                  const float* __restrict__ tgt, const int* __restrict__ qat_bits,
                                                  const float* __restrict__ grid) {
@@ -374,9 +376,10 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
     MfmaWeights<S> W;
     mfma_load<S, false>(W, w, lane);
     if (!m.clamp_out) scale_output<S>(W, kNegLog2e);
+    if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
+    const float ak = act_k(Act, m.leak);
     float cw[4];
     lane_cw<NO>(m.cw, g, cw);
-    const bool unit_leak = m.leak >= 0.0f && m.leak <= 1.0f;
     const int base = blockIdx.x * 256 + wave * 64;   // tile t: pixels base + 16 t + j
     float f[S::kMaxIn];
     {
@@ -401,7 +404,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const int cur = __builtin_amdgcn_ds_bpermute((16 * t + i16) << 2, cur_own);
-            double cur_l = 0.0, best_l = 0.0;
+            float cur_l = 0.0f, best_l = 0.0f;
             int best_k = -1;
             for (int kc = 0; kc <= levels; kc += 2) {   // 2^bits candidates: two tiles at a time
                 float b2[2][Q::kKs1];
@@ -411,17 +414,16 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                     for (int ks = 0; ks < Q::kKs1; ks++) b2[v][ks] = b[t][ks];
                 if (g == c % 4) { b2[0][c / 4] = gv[kc]; b2[1][c / 4] = gv[kc + 1]; }
                 f4v o[2];
-                if (unit_leak) mfma_forward<S, 2, kActMax, false>(W, b2, m.leak, o);
-                else mfma_forward<S, 2, kActAny, false>(W, b2, m.leak, o);
+                mfma_forward<S, 2, Act, false>(W, b2, ak, o);
 #pragma unroll
                 for (int v = 0; v < 2; v++) {
-                    double l = 0.0;   // this lane's channels in ascending order, then the pixel's lanes
+                    float l = 0.0f;   // this lane's channels, then the pixel's lanes
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         const float d = out_of<S>(o[v][r], m.clamp_out != 0) - t4[t][r];
-                        l += (double)__fmul_rn(cw[r], __fmul_rn(d, d));
+                        l = __builtin_fmaf(__fmul_rn(cw[r], d), d, l);
                     }
-                    l = group_sum_d(l);
+                    l = group_sum_f(l);
                     if (kc + v == cur) cur_l = l;
                     else if (best_k < 0 || l < best_l) { best_l = l; best_k = kc + v; }
                 }
@@ -553,8 +555,13 @@ void launch_qat_mfma(Impl& I) {
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         if constexpr (MfmaShape<S>::kOk)
-            hipLaunchKernelGGL(k_qat_mfma<S>, dim3((unsigned)((I.npix + 255) / 256)), dim3(256), 0, I.stream, I.dm, I.w, I.zdec, I.tgt,
+        {
+            const float leak = I.dm.leak;
+            auto kern = leak == 0.0f ? k_qat_mfma<S, kActZero>
+                                     : (leak > 0.0f && leak <= 1.0f ? k_qat_mfma<S, kActFold> : k_qat_mfma<S, kActAny>);
+            hipLaunchKernelGGL(kern, dim3((unsigned)((I.npix + 255) / 256)), dim3(256), 0, I.stream, I.dm, I.w, I.zdec, I.tgt,
                                I.qat_bits, I.qat_grid);
+        }
     });
     NTC_CHECK(hipGetLastError());
 }

@@ -345,6 +345,14 @@ __device__ __forceinline__ double group_sum_d(double v) {
     return join(l16[0], h16[0]) + join(l16[1], h16[1]);
 }
 
+// The float sum of v over the four lane groups of each pixel, in every one of them: (g0 + g2) + (g1 + g3).
+__device__ __forceinline__ float group_sum_f(float v) {
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float s = __uint_as_float(h[0]) + __uint_as_float(h[1]);   // rows: g0 + g2, g1 + g3, g0 + g2, g1 + g3
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // loss_subset's per-pixel terms (main.cpp:1747): s += (double)(cw (d d)), double
 template <int NO>
 __device__ __forceinline__ double chain_err_d(const float (&dd)[4], const float (&cw)[4], int lane) {
