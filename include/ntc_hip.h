@@ -158,6 +158,10 @@ int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage);
  * kernels' parity and speed are then measured against them); on = 1 (the default): the matrix cores
  * take every stage whose shape they pay off for */
 void ntc_trainer_set_matrix_cores(ntc_trainer* t, int on);
+/* Compiles, with hipRTC and without loading it (no device needed), the kernel set that a trainer
+ * specialises at init for a model whose shape the library does not list (its hidden layers all one
+ * width); arch e.g. "gfx950". Returns 1, or 0 with the compiler's log in why. seconds: the compile time. */
+int ntc_jit_compile_check(const ntc_model_desc* d, const char* arch, double* seconds, char* why, size_t why_cap);
 /* the device's Gaussian draws for indices index0 .. index0 + n - 1 of one (seed, stream, step, pair) */
 void ntc_trainer_debug_gauss(ntc_trainer* t, uint32_t stream, uint32_t step, uint32_t pair, uint64_t index0, size_t n,
                              float* out);

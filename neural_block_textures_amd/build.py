@@ -20,7 +20,8 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libntc_hip.so")
-SOURCES = ["kernels_pop.hip", "kernels_mlp.hip", "kernels_latent.hip", "kernels_quant.hip", "trainer.cpp", "noise_fix.cpp", "capi.cpp"]
+SOURCES = ["kernels_pop.hip", "kernels_mlp.hip", "kernels_latent.hip", "kernels_quant.hip", "trainer.cpp", "noise_fix.cpp", "capi.cpp",
+           "jit.cpp"]
 ARCH = "gfx950"
 # The matrix-core population evaluation takes maxima of values that are never NaN for a finite
 # model (the reference's own build assumes no NaNs either, -ffast-math): with the IEEE mode bit
@@ -68,7 +69,7 @@ def build(verbose: bool = False, jobs: int = 4) -> str:
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(compile_one, SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [cc, "-shared", f"--offload-arch={ARCH}", "-o", tmp, *objs, "-lpthread"]
+    cmd = [cc, "-shared", f"--offload-arch={ARCH}", "-o", tmp, *objs, "-lpthread", "-lhiprtc", "-ldl"]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

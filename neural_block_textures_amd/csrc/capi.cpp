@@ -7,6 +7,7 @@
 #include <vector>
 
 #include "ntc_hip.h"
+#include "jit.hpp"
 #include "trainer_impl.hpp"
 
 using ntc_cuda::Trainer;
@@ -170,6 +171,18 @@ int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage) {
 }
 
 void ntc_trainer_set_matrix_cores(ntc_trainer* t, int on) { t->t.im->valu_only = on == 0; }
+
+int ntc_jit_compile_check(const ntc_model_desc* d, const char* arch, double* seconds, char* why, size_t why_cap) {
+    ntc_hip::DevModel m{};
+    m.nlev = d->nlev; m.npos = d->npos; m.nl = d->nhidden; m.nout = d->nout; m.nin = d->nin; m.leak = d->leak;
+    m.clamp_out = d->clamp_out ? 1 : 0;
+    for (int l = 0; l < d->nlev && l < ntc_hip::kMaxLevels; l++) m.lv[l].C = d->lv[l].C;
+    for (int l = 0; l < d->nhidden && l < ntc_hip::kMaxHidden; l++) m.hidden[l] = d->hidden[l];
+    std::string w;
+    const bool ok = ntc_hip::jit_compile_only(m, arch ? arch : "gfx950", w, seconds);
+    if (why && why_cap) snprintf(why, why_cap, "%s", w.c_str());
+    return ok ? 1 : 0;
+}
 
 int ntc_trainer_kernel_time(ntc_trainer* t, const char* name, double* total_ms, long long* launches) {
     auto& I = *t->t.im;

@@ -7,8 +7,13 @@
 // IEEE-rounded (hipcc's default). The one function with a different last bit in rare cases is
 // expf in the sigmoid output (the device's expf against the host C library's).
 #pragma once
+#ifdef __HIPCC_RTC__   // hipRTC provides the runtime itself and the fixed-width integer types in its own namespace
+using __hip_internal::int8_t; using __hip_internal::int16_t; using __hip_internal::int32_t; using __hip_internal::int64_t;
+using __hip_internal::uint8_t; using __hip_internal::uint16_t; using __hip_internal::uint32_t; using __hip_internal::uint64_t;
+#else
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#endif
 
 #include "noise_math.hpp"
 

@@ -5,12 +5,13 @@
 // Reference semantics (main.cpp): LatentTrainer::step_impl 1974-2044 (perturb texels, decode_err
 // twice, raster-order scatter into the distinct taps, grad += w * eps), dct_rate_pass 1935-1952,
 // qat_search 2088-2139.
+#include "kern_valu.hpp"
+#include "jit.hpp"
 #include "shapes.hpp"
 #include "trainer_impl.hpp"
 
 namespace ntc_hip {
 
-constexpr int kTPB = 256;
 
 __device__ __forceinline__ int level_of(const DevModel& m, long long i) {
     int l = 0;
@@ -29,30 +30,6 @@ __global__ void __launch_bounds__(kTPB) k_lat_eps(NoiseFix nt, DevModel m, uint6
     if (k == 0) zgrad[i] = 0.0f;
     const int l = level_of(m, i);
     if ((mask >> l) & 1u) eps[t] = gauss_at(nt, noise_head(seed, NS_LAT, step, (uint32_t)k), (uint64_t)i);
-}
-
-// One antithetic latent pair per blockIdx.y: the pixel's features are built from the decode
-// buffer with the pair's texels perturbed by +sg eps and by -sg eps (each texel value one fused
-// operation, as the reference perturbs the flat latent before sampling), two MLP forwards, and
-// dpix = (e+ - e-) * inv_px with the per-pixel errors fused in float (decode_err).
-template <class S>
-__global__ void __launch_bounds__(kTPB) k_lat_pair(DevModel m, const float* __restrict__ w, const float* __restrict__ zdec,
-                                                  const float* __restrict__ eps, const float* __restrict__ tgt, float sg,
-                                                  unsigned mask, float* __restrict__ dpix) {
-    const int p = blockIdx.x * kTPB + threadIdx.x;
-    if (p >= m.npix) return;
-    const int k = blockIdx.y;
-    const float* e = eps + (size_t)k * m.nz;
-    const int px = p % m.W, py = p / m.W;
-    const float* t = tgt + (size_t)p * m.nout;
-    float f[S::kMaxIn], o[S::kMaxOut];
-    features<S>(m, PerturbedLatent{ zdec, e, sg, mask }, px, py, f);
-    mlp_forward<S>(m, w, f, o);
-    const float ep = pixel_err_f(m, o, t);
-    features<S>(m, PerturbedLatent{ zdec, e, -sg, mask }, px, py, f);
-    mlp_forward<S>(m, w, f, o);
-    const float em = pixel_err_f(m, o, t);
-    dpix[(size_t)k * m.npix + p] = (ep - em) * m.inv_px;
 }
 
 // Footprint gather for one level (the gather form of the reference's raster-order scatter,
@@ -111,52 +88,6 @@ __global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevMod
         for (int c = 0; c < L.C; c++) adam_at(z, zm, zv, (size_t)(base + c), grad[base + c], lr, c1, c2);
 }
 
-// Exact per-texel search on the discrete nearest level 0 (qat_search): one thread per texel;
-// channels in order, the current grid value first, then every other value with strict <; the
-// cell loss is the double sum over the cell's pixels in raster order. The winner is written to
-// the decode buffer at once, so the next channel's features see it. Texels own disjoint cells, so
-// threads never read each other's level-0 values.
-template <class S>
-__global__ void __launch_bounds__(kTPB) k_qat_search(DevModel m, const float* __restrict__ w, float* __restrict__ zdec,
-                                                    const float* __restrict__ tgt, const int* __restrict__ ranges,
-                                                    const int* __restrict__ qat_bits, const float* __restrict__ grid) {
-    const DevLevel& L = m.lv[0];
-    const int t = blockIdx.x * kTPB + threadIdx.x;
-    if (t >= L.W * L.H) return;
-    const int tx = t % L.W, ty = t / L.W;
-    const int* R = ranges + L.rng;
-    const int x0 = R[tx], x1 = R[L.W + tx], y0 = R[2 * L.W + ty], y1 = R[2 * L.W + L.H + ty];
-    if (x0 >= x1 || y0 >= y1) return;
-    float* zt = zdec + L.off + (size_t)t * L.C;
-    constexpr int CMAX = S::kFixed ? S::kC0 : 16;
-#pragma unroll
-    for (int c = 0; c < CMAX; c++) {
-        if (c >= L.C) continue;
-        const int bits = qat_bits[c], levels = (1 << bits) - 1;
-        const float* g = grid + bits * 257;
-        auto cell_loss = [&](float val) {
-            double sum = 0.0;
-            for (int py = y0; py < y1; py++)
-                for (int px = x0; px < x1; px++) {
-                    float f[S::kMaxIn], o[S::kMaxOut];
-                    features<S>(m, PlainLatent{ zdec }, px, py, f);
-                    f[c] = val;
-                    mlp_forward<S>(m, w, f, o);
-                    sum += pixel_err_d(m, o, tgt + ((size_t)py * m.W + px) * m.nout);
-                }
-            return sum;
-        };
-        int best_k = qat_index(zt[c], bits);
-        double best = cell_loss(g[best_k]);
-        for (int k = 0; k <= levels; k++) {
-            if (k == best_k) continue;
-            const double sk = cell_loss(g[k]);
-            if (sk < best) { best = sk; best_k = k; }
-        }
-        zt[c] = g[best_k];
-    }
-}
-
 // ---------------------------------------------------------------- launchers
 void launch_lat_eps(Impl& I, int K, unsigned mask) {
     const size_t n = (size_t)K * I.nz;
@@ -167,7 +98,10 @@ void launch_lat_eps(Impl& I, int K, unsigned mask) {
 }
 
 void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask) {
-    dispatch_shape(I.dm, [&](auto s) {
+    if (I.jit) {
+        jit_launch(k_lat_pair<ShapeDefault>, I, "k_lat_pair", "", dim3(blocks_for(I.npix, kTPB), K), dim3(kTPB), 0, I.dm, I.w, I.zdec,
+                   I.eps_lat, I.tgt, sigma, mask, I.dpix);
+    } else dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         hipLaunchKernelGGL(k_lat_pair<S>, dim3(blocks_for(I.npix, kTPB), K), dim3(kTPB), 0, I.stream, I.dm, I.w, I.zdec, I.eps_lat,
                            I.tgt, sigma, mask, I.dpix);
@@ -193,7 +127,10 @@ void launch_qat_search(Impl& I) {
         launch_qat_mfma(I);
         return;
     }
-    dispatch_shape(I.dm, [&](auto s) {
+    if (I.jit) {
+        jit_launch(k_qat_search<ShapeDefault>, I, "k_qat_search", "", dim3(blocks_for(ntx, kTPB)), dim3(kTPB), 0, I.dm, I.w, I.zdec,
+                   I.tgt, I.ranges, I.qat_bits, I.qat_grid);
+    } else dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         hipLaunchKernelGGL(k_qat_search<S>, dim3(blocks_for(ntx, kTPB)), dim3(kTPB), 0, I.stream, I.dm, I.w, I.zdec, I.tgt, I.ranges,
                            I.qat_bits, I.qat_grid);

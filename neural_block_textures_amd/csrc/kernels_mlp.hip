@@ -3,39 +3,17 @@
 //
 // Reference semantics (main.cpp): MlpTrainer::draw_batch 1825-1833, MlpTrainer::step 1836-1876,
 // MlpTrainer::step_fd 1890-1920, Adam::step 1799-1809, Decoder::decode_full 1712-1718.
+#include "kern_valu.hpp"
+#include "jit.hpp"
 #include "shapes.hpp"
 #include "trainer_impl.hpp"
 
 namespace ntc_hip {
 
-constexpr int kTPB = 256;
 
 __global__ void __launch_bounds__(kTPB) k_fill(float* __restrict__ p, size_t n, float v) {
     const size_t i = (size_t)blockIdx.x * kTPB + threadIdx.x;
     if (i < n) p[i] = v;
-}
-
-// The minibatch (draw_batch with the counter draw): slot s -> pixel, its feature column
-// feat[.][s] and target column btgt[.][s] (structure of arrays, so the evaluation reads coalesced).
-template <class S>
-__global__ void __launch_bounds__(kTPB) k_batch(DevModel m, uint64_t head, int M, int Mcap, const float* __restrict__ zdec,
-                                               const float* __restrict__ tgt, int* __restrict__ bidx,
-                                               float* __restrict__ feat, float* __restrict__ btgt) {
-    const int s = blockIdx.x * kTPB + threadIdx.x;
-    if (s >= M) return;
-    const uint32_t u = (uint32_t)(noise_bits(head, (uint64_t)s) >> 32);
-    const int idx = (int)noise_uniform(u, (uint32_t)m.npix);
-    bidx[s] = idx;
-    float f[S::kMaxIn];
-    features<S>(m, PlainLatent{ zdec }, idx % m.W, idx / m.W, f);
-    if constexpr (S::kFixed) {
-#pragma unroll
-        for (int i = 0; i < S::kNin; i++) feat[(size_t)i * Mcap + s] = f[i];
-    } else {
-        for (int i = 0; i < m.nin; i++) feat[(size_t)i * Mcap + s] = f[i];
-    }
-    const float* t = tgt + (size_t)idx * m.nout;
-    for (int c = 0; c < m.nout; c++) btgt[(size_t)c * Mcap + s] = t[c];
 }
 
 // Member weights of one ES step: pair i, weight k -> w0 +- sigma * eps (one fused operation each,
@@ -75,44 +53,6 @@ __global__ void __launch_bounds__(kTPB) k_fd_sets(int P, float h, const float* _
     wsets[(size_t)(2 * j) * P + k] = hit ? wp : w;
     wsets[(size_t)(2 * j + 1) * P + k] = hit ? wm : w;
     if (hit) hh[j] = (double)wp - (double)wm;
-}
-
-// The population evaluation: block (pair, chunk) evaluates both members of the pair on the
-// chunk's minibatch slots; each slot's features are loaded once and run through the two weight
-// vectors, whose uniform addresses put the weights in SGPRs. Per-member weighted squared errors
-// are summed in double and reduced in a fixed order.
-template <class S>
-__global__ void __launch_bounds__(kTPB) k_pop_eval(DevModel m, const float* __restrict__ wsets, int M, int Mcap, int chunk,
-                                                  int chunks, const float* __restrict__ feat,
-                                                  const float* __restrict__ btgt, double* __restrict__ part) {
-    __shared__ double red[kTPB / 64];
-    const int pair = blockIdx.x, ch = blockIdx.y;
-    const float* __restrict__ wp = wsets + (size_t)(2 * pair) * m.P;
-    const float* __restrict__ wn = wp + m.P;
-    const int s0 = ch * chunk, s1 = min(M, s0 + chunk);
-    double ap = 0.0, an = 0.0;
-    for (int s = s0 + (int)threadIdx.x; s < s1; s += kTPB) {
-        float f[S::kMaxIn], t[S::kMaxOut], o[S::kMaxOut];
-        if constexpr (S::kFixed) {
-#pragma unroll
-            for (int i = 0; i < S::kNin; i++) f[i] = feat[(size_t)i * Mcap + s];
-#pragma unroll
-            for (int c = 0; c < S::kNout; c++) t[c] = btgt[(size_t)c * Mcap + s];
-        } else {
-            for (int i = 0; i < m.nin; i++) f[i] = feat[(size_t)i * Mcap + s];
-            for (int c = 0; c < m.nout; c++) t[c] = btgt[(size_t)c * Mcap + s];
-        }
-        mlp_forward<S>(m, wp, f, o);
-        ap += pixel_err_d(m, o, t);
-        mlp_forward<S>(m, wn, f, o);
-        an += pixel_err_d(m, o, t);
-    }
-    ap = block_sum<kTPB>(ap, red);
-    an = block_sum<kTPB>(an, red);
-    if (threadIdx.x == 0) {
-        part[(size_t)(2 * pair) * chunks + ch] = ap;
-        part[(size_t)(2 * pair + 1) * chunks + ch] = an;
-    }
 }
 
 // ES update direction (main.cpp:1868-1873): g[k] = sum over pairs of ((float)dl_i * scale) * eps_ik, one
@@ -203,19 +143,6 @@ __global__ void __launch_bounds__(kTPB) k_adam(float* __restrict__ theta, const 
     adam_at(theta, m, v, i, g[i], lr, c1, c2);
 }
 
-// Full decode (Decoder::decode_full): one pixel per thread.
-template <class S>
-__global__ void __launch_bounds__(kTPB) k_decode(DevModel m, const float* __restrict__ w, const float* __restrict__ z,
-                                                float* __restrict__ img) {
-    const int p = blockIdx.x * kTPB + threadIdx.x;
-    if (p >= m.npix) return;
-    float f[S::kMaxIn], o[S::kMaxOut];
-    features<S>(m, PlainLatent{ z }, p % m.W, p / m.W, f);
-    mlp_forward<S>(m, w, f, o);
-    float* dst = img + (size_t)p * m.nout;
-    for (int c = 0; c < m.nout; c++) dst[c] = o[c];
-}
-
 // A plain copy of known size, the reference point that turns the memory counters of a profile
 // into bytes (n4 float4 values read once and written once).
 __global__ void __launch_bounds__(kTPB) k_copy_calibration(const float4* __restrict__ src, float4* __restrict__ dst, size_t n4) {
@@ -294,7 +221,10 @@ void launch_fill(Impl& I, float* p, size_t n, float v) {
 void launch_batch(Impl& I, int it, int M) {
     const uint64_t head = noise_head(I.d.seed, NS_BATCH_PIX, (uint32_t)it, 0);
     ProfScope ps(I, "batch");
-    dispatch_shape(I.dm, [&](auto s) {
+    if (I.jit) {
+        jit_launch(k_batch<ShapeDefault>, I, "k_batch", "", dim3(blocks_for(M, kTPB)), dim3(kTPB), 0, I.dm, head, M, I.Mcap, I.zdec,
+                   I.tgt, I.bidx, I.feat, I.btgt);
+    } else dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         hipLaunchKernelGGL(k_batch<S>, dim3(blocks_for(M, kTPB)), dim3(kTPB), 0, I.stream, I.dm, head, M, I.Mcap, I.zdec, I.tgt,
                            I.bidx, I.feat, I.btgt);
@@ -326,7 +256,10 @@ void launch_fd_sets(Impl& I, float h) {
 }
 
 void launch_pop_eval_valu(Impl& I, int pairs, int M, int chunk, int chunks) {
-    dispatch_shape(I.dm, [&](auto s) {
+    if (I.jit) {
+        jit_launch(k_pop_eval<ShapeDefault>, I, "k_pop_eval", "", dim3(pairs, chunks), dim3(kTPB), 0, I.dm, I.wsets, M, I.Mcap, chunk,
+                   chunks, I.feat, I.btgt, I.part);
+    } else dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         hipLaunchKernelGGL(k_pop_eval<S>, dim3(pairs, chunks), dim3(kTPB), 0, I.stream, I.dm, I.wsets, M, I.Mcap, chunk, chunks,
                            I.feat, I.btgt, I.part);
@@ -369,7 +302,9 @@ void launch_adam(Impl& I, float* theta, const float* g, float* m, float* v, size
 
 void launch_decode(Impl& I, const float* z) {
     ProfScope ps(I, "decode");
-    dispatch_shape(I.dm, [&](auto s) {
+    if (I.jit) {
+        jit_launch(k_decode<ShapeDefault>, I, "k_decode", "", dim3(blocks_for(I.npix, kTPB)), dim3(kTPB), 0, I.dm, I.w, z, I.img);
+    } else dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         hipLaunchKernelGGL(k_decode<S>, dim3(blocks_for(I.npix, kTPB)), dim3(kTPB), 0, I.stream, I.dm, I.w, z, I.img);
     });

@@ -1,443 +1,14 @@
-// The population evaluation (MlpTrainer::step's member losses, main.cpp:1848-1861) on the FP32
-// matrix cores of gfx950, for the fixed shapes the matrix cores pay off for (MfmaShape::kOk) and
-// 0 <= leak <= 1; other models use the VALU kernel of kernels_mlp.hip. In an ES step the kernel
-// stages the pair's perturbed weights itself (no member weight sets in memory).
-//
-// On this chip an FP32 matrix instruction and a VALU instruction do not run concurrently on a
-// SIMD (a 16x16x4 f32 step costs 32 cycles, a VALU instruction 4, and their mixes take the sum),
-// so everything around the matrix operations is counted in instructions: the activation is one
-// instruction (kActZero's v_max_f32, or kActFold's fused multiply-add on hidden layers whose weights
-// were scaled by (1 + leak) / 2 when the member's weights were staged; this file is compiled with
-// relaxed NaN handling and the IEEE mode bit off, so a maximum needs no canonicalising copies); a
-// hidden layer's outputs feed the next layer in the order
-// the matrix instruction leaves them (no transpose; each unit's sum takes its inputs in another
-// order than the reference's ascending one); the sigmoid is the hardware exp2 and reciprocal, its
-// -log2(e) folded into the output layer; a lane's channel terms cw d d are fused multiply-adds in float
-// over the tiles a wave evaluates at once, then added into a double; tile
-// inputs are buffer loads with a loop-invariant lane offset and the tile's offset in an SGPR. Member
-// losses stay within 1e-5 relative of the reference's (they are not bit-identical here anyway:
-// the sigmoid differs in the last bits).
-//
-// Block (pair, chunk) has four waves: wave w evaluates member 2 pair + (w & 1) on the 16-slot
-// tiles 2 j + (w >> 1) of the chunk, two tiles at a time, the next two tiles' inputs loading
-// while the current ones compute. Each lane adds the float terms cw (d d) (main.cpp:1747) of its
-// output channels into a double; the two waves of a member are added in a fixed order.
-#include "mfma_mlp.hpp"
+// Launchers of the matrix-core kernels of kern_pop.hpp.
+#include "jit.hpp"
+#include "kern_pop.hpp"
 #include "shapes.hpp"
 #include "trainer_impl.hpp"
 
 namespace ntc_hip {
 
-constexpr int kPopWaves = 4;
-// 16-slot tiles a wave evaluates at once (two independent chains of matrix instructions; the 64-wide
-// models then hold 236 VGPRs at two waves per SIMD)
-template <class S>
-constexpr int pop_u() { return 2; }
-
-// A raw buffer over the minibatch arrays: loads take a loop-invariant 32-bit lane offset (VGPR) and
-// the tile's byte offset (SGPR), so no address arithmetic per load. num_records = the allocation
-// (every read stays inside it: the arrays carry 64 floats of slack past nin x Mcap / nout x Mcap).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const float* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ float buffer_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
-}
-
-// Models with at most 4 outputs keep all of them in lane group 0 of a tile's output registers: the
-// two tiles of a pass are packed into one register set (tile u in lane group u) before the sigmoid and
-// the error terms, which then run once for both tiles.
-template <class S>
-constexpr bool pop_pack() { return MfmaShape<S>::kNout <= 4 && pop_u<S>() == 2; }
-
-template <class S>
-struct PopTileIn {
-    float b1[pop_u<S>()][MfmaShape<S>::kKs1];
-    float t[pop_pack<S>() ? 1 : pop_u<S>()][4];   // packed: lane group u holds tile u's targets
-};
-
-// Inputs of tiles j .. j + U - 1 of this wave: soff = byte offset of tile j's first slot (uniform);
-// tile u sits 32 slots further per u (packed: the target offsets of lane group 1 already include it).
-template <class S>
-__device__ __forceinline__ void pop_load(PopTileIn<S>& in, __amdgpu_buffer_rsrc_t rf, __amdgpu_buffer_rsrc_t rt, uint32_t soff,
-                                         const uint32_t (&fo)[MfmaShape<S>::kKs1], const uint32_t (&to)[4]) {
-    using Q = MfmaShape<S>;
-#pragma unroll
-    for (int u = 0; u < pop_u<S>(); u++) {
-        const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane((int)(soff + 128u * u));   // uniform: an SGPR
-#pragma unroll
-        for (int ks = 0; ks < Q::kKs1; ks++) in.b1[u][ks] = buffer_f32(rf, fo[ks], so);
-        if (!pop_pack<S>() || u == 0) {
-#pragma unroll
-            for (int r = 0; r < 4; r++) in.t[u][r] = buffer_f32(rt, to[r], so);
-        }
-    }
-}
-
-// 1 / (1 + e^-s) from the hardware exp2 and reciprocal (each within about 1 ulp), given
-// s2 = -log2(e) s: the kernels scale the output layer by kNegLog2e (scale_output), so the matrix
-// instruction delivers s2 directly
-constexpr float kNegLog2e = -1.44269504088896341f;
-__device__ __forceinline__ float sigmoid_hw2(float s2) { return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(s2)); }
-
-// the output of a pre-activation: clamp(s + 0.5) with --clamp, else the sigmoid of a pre-activation
-// delivered as -log2(e) s (the output layer is scaled when !clamp)
-template <class S>
-__device__ __forceinline__ float out_of(float s, bool clamp) {
-    return clamp ? __builtin_amdgcn_fmed3f(s + 0.5f, 0.0f, 1.0f) : sigmoid_hw2(s);
-}
-
-// Where a member's parameters come from: the weight sets of a central-difference step (kSets), or -
-// in an ES step - both members' weights w0 +- sigma eps (one fused operation each, main.cpp:1852-1856)
-// staged in LDS, from the block's own draw of the pair's Gaussians (NS_MLP, step, pair, k; the chunk-0
-// block writes them to eps for the update: kDraw, for populations with one or two chunks per pair) or
-// from the Gaussians a separate kernel drew once for all chunks (kReadEps).
-enum PopFrom : int { kSets = 0, kDraw = 1, kReadEps = 2 };
-struct PopSource {
-    const float* wsets;                    // central differences: 2 pairs x P
-    NoiseFix nt; uint64_t seed; uint32_t step; float sigma;
-    const float* w0; float* eps;           // ES: the current weights and the step's Gaussians [pair][P]
-};
-
-// waves per SIMD the register allocation aims at (more would spill)
-template <class S>
-constexpr int pop_occupancy() { return MfmaShape<S>::kH > 32 ? 2 : (MfmaShape<S>::kIn <= 8 ? 4 : 3); }
-
-template <class S, int Act, bool Clamp, int From>
-__global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_per_eu(pop_occupancy<S>()))) k_pop_mfma(DevModel m, PopSource src, int M, int Mcap,
-                                                           int chunk, int chunks, const float* __restrict__ feat,
-                                                           const float* __restrict__ btgt, double* __restrict__ part) {
-    using Q = MfmaShape<S>;
-    constexpr bool Es = From != kSets;
-    __shared__ double red[kPopWaves];
-    __shared__ float wpm_s[Es ? 2 * Q::kP : 1];   // ES: the + member's weights, then the - member's
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int pair = blockIdx.x, ch = blockIdx.y, sgn = wave & 1, half = wave >> 1;
-    const int i16 = lane & 15, g = lane >> 4;
-    MfmaWeights<S> W;
-    if constexpr (Es) {
-        const uint64_t head = noise_head(src.seed, NS_MLP, src.step, (uint32_t)pair);
-        float* eg = src.eps + (size_t)pair * Q::kP;
-        for (int k = threadIdx.x; k < Q::kP; k += 64 * kPopWaves) {
-            float e;
-            if constexpr (From == kDraw) {
-                e = gauss_at(src.nt, head, (uint64_t)k);
-                if (ch == 0) eg[k] = e;
-            } else {
-                e = eg[k];
-            }
-            const float w0 = src.w0[k];
-            wpm_s[k] = __builtin_fmaf(src.sigma, e, w0);
-            wpm_s[Q::kP + k] = __builtin_fmaf(-src.sigma, e, w0);
-        }
-        __syncthreads();
-        mfma_load<S, false>(W, wpm_s + sgn * Q::kP, lane);
-    } else {
-        mfma_load<S, false>(W, src.wsets + (size_t)(2 * pair + sgn) * Q::kP, lane);
-    }
-    if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
-    if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
-    const float ak = act_k(Act, m.leak);
-    constexpr bool kPack = pop_pack<S>();
-    // the channel weight of each of this lane's output registers (rows 4 g + r; packed: rows r of
-    // lane group g's tile, groups 2 and 3 unused), zero past the last output
-    float cw[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        cw[r] = 0.0f;
-#pragma unroll
-        for (int c = 0; c < Q::kNout; c++)
-            if ((kPack ? (g <= 1 && r == c) : 4 * g + r == c)) cw[r] = m.cw[c];
-    }
-    // lane byte offsets of the feature rows 4 ks + g and target rows 4 g + r (rows past the last
-    // one are clamped to it: their weights, or their channel weights cw, are zero); packed: target
-    // row r of tile g (lane group 1 reads the pass's second tile)
-    uint32_t fo[Q::kKs1], to[4];
-#pragma unroll
-    for (int ks = 0; ks < Q::kKs1; ks++) fo[ks] = 4u * ((uint32_t)min(4 * ks + g, Q::kIn - 1) * (uint32_t)Mcap + (uint32_t)i16);
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-        to[r] = kPack ? 4u * ((uint32_t)min(r, Q::kNout - 1) * (uint32_t)Mcap + (uint32_t)i16) + (g == 1 ? 128u : 0u)
-                      : 4u * ((uint32_t)min(4 * g + r, Q::kNout - 1) * (uint32_t)Mcap + (uint32_t)i16);
-    const int s0 = ch * chunk, s1 = min(M, s0 + chunk);
-    const int tiles = (s1 - s0 + 15) >> 4;
-    const int mine = (tiles - half + 1) >> 1;   // this wave's tiles: 2 j + half, j < mine
-    double e = 0.0;
-    const __amdgpu_buffer_rsrc_t rf = buffer_of(feat, 4u * ((uint32_t)Q::kIn * (uint32_t)Mcap + 64u));
-    const __amdgpu_buffer_rsrc_t rt = buffer_of(btgt, 4u * ((uint32_t)Q::kNout * (uint32_t)Mcap + 64u));
-    constexpr int U = pop_u<S>();
-    // One pass: tiles j .. j + U - 1 from c, while tiles j + U .. load into n. The loop alternates
-    // two input sets, so no registers are copied between passes. The loads are issued on every pass
-    // (the last one reloads its own tiles) so that the wait for them falls in the next pass.
-    auto pass = [&](PopTileIn<S>& c, PopTileIn<S>& n, int j) {
-        pop_load<S>(n, rf, rt, 4u * (uint32_t)(s0 + 16 * (2 * (j + U < mine ? j + U : j) + half)), fo, to);
-        if constexpr (Q::kIn % 4 != 0) {   // inputs past nin are zero
-#pragma unroll
-            for (int u = 0; u < U; u++)
-                if (4 * (Q::kKs1 - 1) + g >= Q::kIn) c.b1[u][Q::kKs1 - 1] = 0.0f;
-        }
-        f4v o[U];
-        mfma_forward<S, U, Act, false>(W, c.b1, ak, o);
-        if constexpr (kPack) {
-            // lane group 0 of each tile holds its outputs: tile 1's move to lane group 1
-            f4v op;
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                op[r] = __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(o[0][r]), __float_as_uint(o[1][r]), false, false)[0]);
-            float tsum = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float d = out_of<S>(op[r], Clamp) - c.t[0][r];
-                tsum = __builtin_fmaf(__fmul_rn(cw[r], d), d, tsum);
-            }
-            if (j + U <= mine && s0 + 16 * (2 * (j + U - 1) + half) + 16 <= s1) e += (double)tsum;   // both tiles whole (uniform)
-            else {
-                const int gu = g & 1;   // this lane's tile (groups 2, 3 carry zeros)
-                if (j + gu < mine && s0 + 16 * (2 * (j + gu) + half) + i16 < s1) e += (double)tsum;
-            }
-        } else {
-            // this lane's channel terms cw (d d): one multiply and one fused multiply-add each, summed in
-            // float over the pass's tiles, then into the double
-            float dq[U][4], dd[U][4];
-#pragma unroll
-            for (int u = 0; u < U; u++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    dd[u][r] = out_of<S>(o[u][r], Clamp) - c.t[u][r];
-                    dq[u][r] = __fmul_rn(cw[r], dd[u][r]);
-                }
-            if (j + U <= mine && s0 + 16 * (2 * (j + U - 1) + half) + 16 <= s1) {   // all U tiles whole (uniform)
-                float tsum = 0.0f;
-#pragma unroll
-                for (int u = 0; u < U; u++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) tsum = __builtin_fmaf(dq[u][r], dd[u][r], tsum);
-                e += (double)tsum;
-            } else {
-#pragma unroll
-                for (int u = 0; u < U; u++) {
-                    const int st = s0 + 16 * (2 * (j + u) + half);   // first slot of the tile (uniform)
-                    float tsum = 0.0f;
-#pragma unroll
-                    for (int r = 0; r < 4; r++) tsum = __builtin_fmaf(dq[u][r], dd[u][r], tsum);
-                    if (j + u < mine && st + i16 < s1) e += (double)tsum;
-                }
-            }
-        }
-    };
-    PopTileIn<S> in0, in1;
-    pop_load<S>(in0, rf, rt, 4u * (uint32_t)(s0 + 16 * half), fo, to);
-    for (int j = 0; j < mine; j += 2 * U) {
-        pass(in0, in1, j);
-        if (j + U >= mine) break;
-        pass(in1, in0, j + U);
-    }
-    e = wave_sum(e);
-    if (lane == 0) red[wave] = e;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        part[(size_t)(2 * pair) * chunks + ch] = red[0] + red[2];
-        part[(size_t)(2 * pair + 1) * chunks + ch] = red[1] + red[3];
-    }
-}
-
-// The latent pair evaluation (LatentTrainer::step_impl, main.cpp:1990-2007) on the matrix cores:
-// block (512 or 256 pixels, pair k), each wave a quarter of them in rounds of 64. In a round every
-// lane builds the features of its own pixel with the pair's texels perturbed by +sg eps and by
-// -sg eps (features_pm: both members from one set of taps and texel loads), and four transposes
-// across the lane groups (tiles_of) turn the 64 pixels into the B operands of four 16-pixel tiles:
-// no shared memory and no barrier, so a wave's feature loads overlap other waves' matrix work. Each
-// tile's + and - members are evaluated together; a pixel's error is decode_err's float sum of
-// cw (d d) over its channels (a lane's four in ascending order, then the lane groups pairwise: within
-// a few ulp of the reference's ascending chain), and dpix = (e+ - e-) * inv_px.
-// pixels per block: 512, or 256 for wide inputs
-template <class S>
-constexpr int lat_pix() { return MfmaShape<S>::kIn <= 8 ? 512 : 256; }
-
-
-template <class S, int Act, bool Clamp>
-__global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* __restrict__ w, const float* __restrict__ zdec,
-                                                      const float* __restrict__ eps, const float* __restrict__ tgt, float sg,
-                                                      unsigned mask, float* __restrict__ dpix) {
-    using Q = MfmaShape<S>;
-    constexpr int NO = Q::kNout, kLatPix = lat_pix<S>(), kRounds = kLatPix / 256;
-    // at most 4 outputs: the + member's outputs stay in lane group 0, the - member's move to group 1,
-    // and each pixel's error is one lane's chain over its channels in ascending order
-    constexpr bool kPack = NO <= 4;
-    const int k = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
-    const float* e = eps + (size_t)k * m.nz;
-    float* out = dpix + (size_t)k * m.npix;
-    MfmaWeights<S> W;
-    mfma_load<S, false>(W, w, lane);
-    if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
-    if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
-    const float ak = act_k(Act, m.leak);
-    float cw[4];
-    if constexpr (kPack) {
-#pragma unroll
-        for (int r = 0; r < 4; r++) cw[r] = (g <= 1 && r < NO) ? m.cw[r] : 0.0f;
-    } else {
-        lane_cw<NO>(m.cw, g, cw);
-    }
-    // the targets of the tile at pixel t0: lane (g, j) reads channels 4 g .. 4 g + 3 of pixel t0 + j (one
-    // 16-byte load when a pixel's row is a whole number of float4; rows past the last are clamped);
-    // packed: channels 0 .. 3 in every lane group
-    auto load_t = [&](int t0, float (&t)[4]) {
-        const int pr = min(t0 + i16, m.npix - 1);
-        if constexpr (kPack) {
-#pragma unroll
-            for (int r = 0; r < 4; r++) t[r] = tgt[(size_t)pr * NO + min(r, NO - 1)];
-        } else if constexpr (NO % 4 == 0) {
-            const f4v v = *reinterpret_cast<const f4v*>(tgt + (size_t)pr * NO + min(4 * g, NO - 4));
-#pragma unroll
-            for (int r = 0; r < 4; r++) t[r] = v[r];
-        } else {
-#pragma unroll
-            for (int r = 0; r < 4; r++) t[r] = tgt[(size_t)pr * NO + min(4 * g + r, NO - 1)];
-        }
-    };
-    for (int rd = 0; rd < kRounds; rd++) {
-        const int base = blockIdx.x * kLatPix + (kLatPix / 4) * wave + 64 * rd;   // tile t: pixels base + 16 t + j
-        float tn[4];
-        load_t(base, tn);
-        float bp[4][Q::kKs1], bm[4][Q::kKs1];
-        {
-            const int pr = min(base + lane, m.npix - 1);
-            float fp[S::kMaxIn], fm[S::kMaxIn];
-            features_pm<S>(m, zdec, e, sg, mask, pr % m.W, pr / m.W, fp, fm);
-            tiles_of<S>(fp, bp);
-            tiles_of<S>(fm, bm);
-        }
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            float tt[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) tt[r] = tn[r];
-            if (t + 1 < 4) load_t(base + 16 * (t + 1), tn);
-            float b1[2][Q::kKs1];
-#pragma unroll
-            for (int ks = 0; ks < Q::kKs1; ks++) { b1[0][ks] = bp[t][ks]; b1[1][ks] = bm[t][ks]; }
-            f4v o[2];
-            mfma_forward<S, 2, Act, false>(W, b1, ak, o);
-            const int p = base + 16 * t + i16;
-            if constexpr (kPack) {
-                float ev = 0.0f;   // group 0: e+, group 1: e-
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float op = __uint_as_float(
-                        __builtin_amdgcn_permlane16_swap(__float_as_uint(o[0][r]), __float_as_uint(o[1][r]), false, false)[0]);
-                    const float d = out_of<S>(op, Clamp) - tt[r];
-                    ev = __builtin_fmaf(cw[r], __fmul_rn(d, d), ev);
-                }
-                const auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(ev), __float_as_uint(ev), false, false);
-                if (g == 0 && p < m.npix) out[p] = __fmul_rn(__uint_as_float(x[0]) - __uint_as_float(x[1]), m.inv_px);
-                continue;
-            }
-            // each lane's four channel terms cw (d d) in ascending order, then the four lane groups
-            // added pairwise (permlane swaps): e+ in lanes 0-31, e- in lanes 32-63, then e+ - e-
-            float ep = 0.0f, em = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float dp = out_of<S>(o[0][r], Clamp) - tt[r], dm = out_of<S>(o[1][r], Clamp) - tt[r];
-                ep = __builtin_fmaf(cw[r], __fmul_rn(dp, dp), ep);
-                em = __builtin_fmaf(cw[r], __fmul_rn(dm, dm), em);
-            }
-            const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(ep), __float_as_uint(em), false, false);
-            const float s = __uint_as_float(h[0]) + __uint_as_float(h[1]);   // groups 0 + 2 and 1 + 3
-            const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
-            const float c = __uint_as_float(q[0]) + __uint_as_float(q[1]);   // lanes 0-31: e+, 32-63: e-
-            const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);
-            if (g == 0 && p < m.npix) out[p] = __fmul_rn(__uint_as_float(x[0]) - __uint_as_float(x[1]), m.inv_px);
-        }
-    }
-}
-
-// The selector search (qat_search, main.cpp:2088-2139) on the matrix cores, for a nearest level 0
-// of the image's size (each texel's cell is its own pixel): wave = 64 pixels in four 16-pixel tiles.
-// Every lane builds the features of its own pixel (features<S>) and tiles_of turns them into the four
-// tiles' B operands. Per channel and tile, every candidate value is one MLP evaluation of the tile with
-// that feature replaced (two candidates at a time). The choice is the reference's: the current grid
-// value first, then every other value with strict <, so the first strictly smaller loss wins
-// (main.cpp:2101-2132). The winner enters the features of the next channel and is written to the
-// decode buffer. A candidate's loss is the pixel's float sum of cw (d d) over its channels (a lane's
-// four, then the pixel's four lanes pairwise, the same value in each of them) with the hidden
-// activation of act<Act>: the reference adds the float terms in double with its own activation, so a
-// choice can differ from the reference's only between candidates whose losses agree to a few float
-// roundings (the reference's own check accepts such rounding ties, main.cpp:3143-3144).
-template <class S, int Act>
-__global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __restrict__ w, float* __restrict__ zdec,
-                                                 const float* __restrict__ tgt, const int* __restrict__ qat_bits,
-                                                 const float* __restrict__ grid) {
-    using Q = MfmaShape<S>;
-    constexpr int NO = Q::kNout, C0 = S::kC0;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
-    MfmaWeights<S> W;
-    mfma_load<S, false>(W, w, lane);
-    if (!m.clamp_out) scale_output<S>(W, kNegLog2e);
-    if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
-    const float ak = act_k(Act, m.leak);
-    float cw[4];
-    lane_cw<NO>(m.cw, g, cw);
-    const int base = blockIdx.x * 256 + wave * 64;   // tile t: pixels base + 16 t + j
-    float f[S::kMaxIn];
-    {
-        const int pr = min(base + lane, m.npix - 1);
-        features<S>(m, PlainLatent{ zdec }, pr % m.W, pr / m.W, f);
-    }
-    float b[4][Q::kKs1];
-    tiles_of<S>(f, b);
-    float t4[4][4];   // targets: lane (g, j) holds channels 4 g .. 4 g + 3 of pixel j of each tile
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const int pr = min(base + 16 * t + i16, m.npix - 1);
-#pragma unroll
-        for (int r = 0; r < 4; r++) t4[t][r] = tgt[(size_t)pr * NO + min(4 * g + r, NO - 1)];
-    }
-#pragma unroll
-    for (int c = 0; c < C0; c++) {
-        const int bits = qat_bits[c], levels = (1 << bits) - 1;
-        const float* gv = grid + bits * 257;
-        // this channel's current value of every pixel, from the lane that built the pixel's features
-        const int cur_own = qat_index(f[c], bits);
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int cur = __builtin_amdgcn_ds_bpermute((16 * t + i16) << 2, cur_own);
-            float cur_l = 0.0f, best_l = 0.0f;
-            int best_k = -1;
-            for (int kc = 0; kc <= levels; kc += 2) {   // 2^bits candidates: two tiles at a time
-                float b2[2][Q::kKs1];
-#pragma unroll
-                for (int v = 0; v < 2; v++)
-#pragma unroll
-                    for (int ks = 0; ks < Q::kKs1; ks++) b2[v][ks] = b[t][ks];
-                if (g == c % 4) { b2[0][c / 4] = gv[kc]; b2[1][c / 4] = gv[kc + 1]; }
-                f4v o[2];
-                mfma_forward<S, 2, Act, false>(W, b2, ak, o);
-#pragma unroll
-                for (int v = 0; v < 2; v++) {
-                    float l = 0.0f;   // this lane's channels, then the pixel's lanes
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const float d = out_of<S>(o[v][r], m.clamp_out != 0) - t4[t][r];
-                        l = __builtin_fmaf(__fmul_rn(cw[r], d), d, l);
-                    }
-                    l = group_sum_f(l);
-                    if (kc + v == cur) cur_l = l;
-                    else if (best_k < 0 || l < best_l) { best_l = l; best_k = kc + v; }
-                }
-            }
-            const int win = (best_k >= 0 && best_l < cur_l) ? best_k : cur;
-            if (g == c % 4) b[t][c / 4] = gv[win];
-            const int p = base + 16 * t + i16;
-            if (g == 0 && p < m.npix) zdec[m.lv[0].off + (size_t)p * m.lv[0].C + c] = gv[win];
-        }
-    }
-}
-
 bool qat_on_matrix_cores(const Impl& I) {
     if (!I.lv0_unit_cells || I.valu_only) return false;
+    if (I.jit) return jit_mfma(I);
     bool ok = false;
     dispatch_shape(I.dm, [&](auto s) { ok = MfmaShape<decltype(s)>::kOk; });
     return ok;
@@ -446,6 +17,7 @@ bool qat_on_matrix_cores(const Impl& I) {
 // the population and latent-pair evaluations on the matrix cores take 0 <= leak <= 1 (kActZero, kActFold)
 bool pop_on_matrix_cores(const Impl& I) {
     if (I.valu_only || !(I.dm.leak >= 0.0f && I.dm.leak <= 1.0f)) return false;
+    if (I.jit) return jit_mfma(I);
     bool ok = false;
     dispatch_shape(I.dm, [&](auto s) { ok = MfmaShape<decltype(s)>::kOk; });
     return ok;
@@ -482,6 +54,14 @@ static void check_pop_launch(const Impl& I, int pairs, int chunk, int chunks) {
 
 template <int From>
 static void launch_pop_matrix(Impl& I, const PopSource& src, int pairs, int M, int chunk, int chunks) {
+    if (I.jit) {   // the same choice of activation as below
+        const int act = I.dm.leak == 0.0f ? kActZero : (From == kSets ? kActMax : kActFold);
+        jit_launch(k_pop_mfma<ShapeMaterial, kActZero, false, From>, I, "k_pop_mfma",
+                   std::to_string(act) + (I.dm.clamp_out ? ", true, " : ", false, ") + std::to_string(From), dim3(pairs, chunks),
+                   dim3(64 * kPopWaves), 0, I.dm, src, M, I.Mcap, chunk, chunks, I.feat, I.btgt, I.part);
+        NTC_CHECK(hipGetLastError());
+        return;
+    }
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         if constexpr (MfmaShape<S>::kOk) {
@@ -525,6 +105,9 @@ void launch_pop_eval_es(Impl& I, int it, float sigma, int N, int M, int chunk, i
     else launch_pop_matrix<kDraw>(I, src, N, M, chunk, chunks);
 }
 
+// lat_pix<S>() for the shape the kernels were specialised for
+static int jit_lat_pix(const Impl& I) { return I.dm.nin <= 8 ? 512 : 256; }
+
 bool lat_pair_on_matrix_cores(const Impl& I) { return pop_on_matrix_cores(I); }
 
 template <class S, int Act>
@@ -541,6 +124,15 @@ void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask) {
         launch_lat_pair_valu(I, K, sigma, mask);
         return;
     }
+    if (I.jit) {
+        const int act = I.dm.leak == 0.0f ? kActZero : kActFold;
+        const int lp = jit_lat_pix(I);
+        jit_launch(k_lat_pair_mfma<ShapeMaterial, kActZero, false>, I, "k_lat_pair_mfma",
+                   std::to_string(act) + (I.dm.clamp_out ? ", true" : ", false"), dim3((unsigned)((I.npix + lp - 1) / lp), K), dim3(256), 0,
+                   I.dm, I.w, I.zdec, I.eps_lat, I.tgt, sigma, mask, I.dpix);
+        NTC_CHECK(hipGetLastError());
+        return;
+    }
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         if constexpr (MfmaShape<S>::kOk) {
@@ -552,6 +144,14 @@ void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask) {
 }
 
 void launch_qat_mfma(Impl& I) {
+    if (I.jit) {
+        const float leak = I.dm.leak;
+        const int act = leak == 0.0f ? kActZero : (leak > 0.0f && leak <= 1.0f ? kActFold : kActAny);
+        jit_launch(k_qat_mfma<ShapeMaterial, kActZero>, I, "k_qat_mfma", std::to_string(act), dim3((unsigned)((I.npix + 255) / 256)),
+                   dim3(256), 0, I.dm, I.w, I.zdec, I.tgt, I.qat_bits, I.qat_grid);
+        NTC_CHECK(hipGetLastError());
+        return;
+    }
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         if constexpr (MfmaShape<S>::kOk)

@@ -7,13 +7,13 @@
 // bit counts equal the reference's host functions bit for bit. The one exception is the decoder
 // sensitivity probe (an estimate in the reference too), which evaluates the MLP as the decode does. Reference (main.cpp): qes_index /
 // qes_snap_level 446-495; dct_clampf .. dct_clamp_level0 783-976; dct_rate_block 884-896.
+#include "kern_valu.hpp"
+#include "jit.hpp"
 #include "shapes.hpp"
 #include "trainer_impl.hpp"
 
 namespace ntc_hip {
 
-constexpr int kTPB = 256;
-constexpr int kTPB_DCT = 64;   // the probe: one (block, channel) per thread
 
 // ---------------------------------------------------------------- --qes
 __device__ __forceinline__ int qes_index(float v, float lo, float range, int levels) {
@@ -290,48 +290,6 @@ void launch_dct_clamp0(Impl& I) {
     hipLaunchKernelGGL(k_dct_clamp0, dim3(blocks_for(n0, kTPB)), dim3(kTPB), 0, I.stream, I.z, I.zq, (size_t)I.d.lv[0].off, n0);
     NTC_CHECK(hipGetLastError());
 }
-// The decoder sensitivity probe of a DCT-coded level 0 (dct_probe_codes, main.cpp:1001-1032), on the
-// device: one thread per (block, channel). At the 4 positions (8 bx + {2, 5}, 8 by + {2, 5}) the
-// features are built once from the decode buffer and the MLP evaluated with level-0 channel c set to
-// -1, -0.5, 0, 0.5, 1; segment gain g = (255 / 16) sqrt(sum_o cw_o (out_{j+1} - out_j)^2 / wsum), block
-// gain = RMS over the 16 (position, segment) pairs, code = round(log2(g / g_floor) / 0.6) in [0, 15].
-// The reference calls the probe an estimate (not strict FP): the device's expf and log2 can move a
-// gain that sits on a code boundary to the neighbouring code.
-template <class S>
-__global__ void __launch_bounds__(kTPB_DCT) k_dct_probe(DevModel m, const float* __restrict__ w, const float* __restrict__ zdec,
-                                                       int BW, int BH, int C, uint8_t* __restrict__ code, float* __restrict__ gain) {
-    const int t = blockIdx.x * kTPB_DCT + threadIdx.x;
-    if (t >= BW * BH * C) return;
-    const int c = t % C, b = t / C, bx = b % BW, by = b / BW;
-    const int P[2] = { 2, 5 };
-    const float SJ[5] = { -1.0f, -0.5f, 0.0f, 0.5f, 1.0f };
-    double acc = 0.0;
-    for (int py = 0; py < 2; py++)
-        for (int px = 0; px < 2; px++) {
-            float f[S::kMaxIn], out[5][S::kMaxOut];
-            features<S>(m, PlainLatent{ zdec }, bx * 8 + P[px], by * 8 + P[py], f);
-            for (int j = 0; j < 5; j++) {
-                f[c] = SJ[j];
-                mlp_forward<S>(m, w, f, out[j]);
-            }
-            for (int j = 0; j < 4; j++) {
-                double ss = 0.0;
-                for (int o = 0; o < m.nout; o++) {
-                    const double d = (double)out[j + 1][o] - (double)out[j][o];
-                    ss = __dadd_rn(ss, __dmul_rn(__dmul_rn((double)m.cw[o], d), d));
-                }
-                const double g = (255.0 / 16.0) * sqrt(ss / (double)m.wsum);
-                acc += g * g;
-            }
-        }
-    const double gb = sqrt(acc / 16.0);
-    const double gf = 14.0 / 64.0;
-    const double gc = gb > gf ? gb : gf;
-    const long long k = (long long)round(log2(gc / gf) / 0.6);
-    code[t] = (uint8_t)(k < 0 ? 0 : (k > 15 ? 15 : k));
-    if (gain) gain[t] = (float)gb;
-}
-
 void launch_dct_snap(Impl& I) {
     ProfScope ps(I, "dct_snap");
     hipLaunchKernelGGL(k_dct_snap, dim3(blocks_for(I.ddct.n, kDctWaves)), dim3(64 * kDctWaves), 0, I.stream, I.ddct, I.dm.lv[0], I.z, I.zq,
@@ -356,7 +314,10 @@ void launch_shadow_pull(Impl& I, size_t off, size_t n, float f) {
 
 void launch_dct_probe(Impl& I, uint8_t* code, float* gain) {
     ProfScope ps(I, "dct_probe");
-    dispatch_shape(I.dm, [&](auto s) {
+    if (I.jit) {
+        jit_launch(k_dct_probe<ShapeDefault>, I, "k_dct_probe", "", dim3(blocks_for(I.ddct.n, kTPB_DCT)), dim3(kTPB_DCT), 0, I.dm, I.w,
+                   I.zdec, I.ddct.BW, I.ddct.BH, I.ddct.C, code, gain);
+    } else dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         hipLaunchKernelGGL(k_dct_probe<S>, dim3(blocks_for(I.ddct.n, kTPB_DCT)), dim3(kTPB_DCT), 0, I.stream, I.dm, I.w, I.zdec,
                            I.ddct.BW, I.ddct.BH, I.ddct.C, code, gain);

@@ -32,6 +32,19 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 #define NTC_MFMA_MIN_USEFUL 0.5
 #endif
 
+// The fraction of the multiply-adds of a 16-pixel tile's matrix instructions that are the model's, for
+// an nin -> H (x NL hidden layers) -> nout MLP with the hidden tiles padded to 16 units and the padding's
+// k-steps skipped, and whether that pays off: a 16x16x4 instruction does 32 multiply-adds per cycle, a
+// VALU FMA 16, so the matrix cores take a shape when at least half of their work is the model's.
+__host__ __device__ constexpr int mfma_per_tile(int nin, int H, int NL) {
+    return ((H + 15) / 16) * ((nin + 3) / 4) + (NL - 1) * ((H + 15) / 16) * (4 * ((H + 15) / 16 - 1) + (H - 16 * ((H + 15) / 16 - 1) + 3) / 4) +
+           (4 * ((H + 15) / 16 - 1) + (H - 16 * ((H + 15) / 16 - 1) + 3) / 4);
+}
+__host__ __device__ constexpr bool mfma_pays(int nin, int H, int NL, int nout) {
+    return nout <= 16 && NL >= 1 && H >= 1 &&
+           (double)(nin * H + (NL - 1) * H * H + H * nout) >= NTC_MFMA_MIN_USEFUL * 64.0 * (double)mfma_per_tile(nin, H, NL);
+}
+
 template <class S, bool = S::kFixed>
 struct MfmaShape { static constexpr bool kOk = false; };
 template <class S>
@@ -46,11 +59,10 @@ struct MfmaShape<S, true> {
     static constexpr int kP = kH * kIn + kH + (kNL - 1) * (kH * kH + kH) + kNout * kH + kNout;   // parameters
     // matrix instructions per 16-pixel tile, and the fraction of their multiply-adds that are the model's
     static constexpr int kMfmaPerTile = kHt * kKs1 + (kNL - 1) * kHt * kKsH + kKsH;
+    static_assert(kMfmaPerTile == mfma_per_tile(kIn, kH, kNL), "the runtime count must follow the tile layout");
     static constexpr int kMacs = kIn * kH + (kNL - 1) * kH * kH + kH * kNout;
     static constexpr double kUseful = (double)kMacs / (64.0 * kMfmaPerTile);
-    // the matrix cores take the shape when at least half of their multiply-adds are the model's (a
-    // matrix instruction does twice the multiply-adds per cycle of a VALU one); others run on the VALU
-    static constexpr bool kOk = kNout <= 16 && kNL >= 1 && kUseful >= NTC_MFMA_MIN_USEFUL;
+    static constexpr bool kOk = mfma_pays(kIn, kH, kNL, kNout);
     // registers of hidden tile ot that hold units
     static constexpr int regs(int ot) { return ot == kHt - 1 ? kLastR : 4; }
     static constexpr bool partial(int ot) { return ot == kHt - 1 && kLastU < 16; }

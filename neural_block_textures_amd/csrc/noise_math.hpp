@@ -13,8 +13,13 @@
 // Only IEEE operations that round identically on x86-64 and gfx950 are used: +, -, *, /, fma and
 // round-to-nearest-even, no library functions.
 #pragma once
+#ifdef __HIPCC_RTC__   // hipRTC provides the runtime itself and the fixed-width integer types in its own namespace
+using __hip_internal::int8_t; using __hip_internal::int16_t; using __hip_internal::int32_t; using __hip_internal::int64_t;
+using __hip_internal::uint8_t; using __hip_internal::uint16_t; using __hip_internal::uint32_t; using __hip_internal::uint64_t;
+#else
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#endif
 
 namespace ntc_hip {
 

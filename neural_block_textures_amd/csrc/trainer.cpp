@@ -10,6 +10,7 @@
 #include <algorithm>
 
 #include "shapes.hpp"
+#include "jit.hpp"
 #include "trainer_impl.hpp"
 
 using namespace ntc_hip;
@@ -298,6 +299,7 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
     m.P = I.P;
     m.nz = (long long)I.nz;
     I.shape_name = dispatch_shape(m, [](auto) {});
+    I.jit = nullptr;
 
     // ---- buffers
     dev_alloc(&I.ranges, ranges.size());
@@ -350,6 +352,17 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
     NTC_CHECK(hipMemset(I.zm, 0, I.nz * sizeof(float))); NTC_CHECK(hipMemset(I.zv, 0, I.nz * sizeof(float)));
     NTC_CHECK(hipMemset(I.wm, 0, I.P * sizeof(float))); NTC_CHECK(hipMemset(I.wv, 0, I.P * sizeof(float)));
     NTC_CHECK(hipMemcpy(I.tgt, target, I.npix * d.nout * sizeof(float), hipMemcpyHostToDevice));
+    if (I.shape_name == "runtime") {   // a shape shapes.hpp does not list: the fixed-shape kernels compiled for it now
+        std::string jwhy;
+        JitShape js{};
+        if (jit_prepare(I, jwhy) && jit_shape_of(I.dm, js)) {
+            char b[96];
+            snprintf(b, sizeof(b), "%d+%d+%d|%dpos|%dx%d|%d (specialised at init)", js.C0, js.C1, js.C2, js.npos, js.H, js.NL, js.nout);
+            I.shape_name = b;
+        } else {
+            fprintf(stderr, "ntc_hip backend: the runtime-shaped kernels run this model (%s)\n", jwhy.c_str());
+        }
+    }
     upload_model(z, p);
     return true;
 }
@@ -358,7 +371,7 @@ std::string Trainer::banner() const {
     const Impl& I = *im;
     char buf[320];
     snprintf(buf, sizeof(buf), "%s (%s, %d CUs), HIP runtime %d.%d, MLP shape %s", I.dev_name.c_str(), I.arch.c_str(), I.cus,
-             I.rt_ver / 10000000, (I.rt_ver / 100000) % 100, I.shape_name);
+             I.rt_ver / 10000000, (I.rt_ver / 100000) % 100, I.shape_name.c_str());
     return buf;
 }
 

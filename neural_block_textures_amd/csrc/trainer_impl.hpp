@@ -43,6 +43,8 @@ struct DevDct {
     int zigzag[64];
 };
 
+struct JitModuleSet;   // jit.cpp: the kernels specialised for one model shape
+
 struct KernelTimes {
     std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
     double total_ms = 0.0;
@@ -103,7 +105,8 @@ struct ntc_cuda::Trainer::Impl {
 
     std::string dev_name, arch;
     int cus = 0, rt_ver = 0;
-    const char* shape_name = "runtime";
+    std::string shape_name = "runtime";
+    ntc_hip::JitModuleSet* jit = nullptr;   // kernels specialised at init for a shape shapes.hpp does not list
 
     bool profiling = false;
     std::string prof_only;     // comma-separated kernel families to time; empty = all

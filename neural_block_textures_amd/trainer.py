@@ -104,6 +104,7 @@ def library() -> C.CDLL:
             "ntc_trainer_kernel_time": (C.c_int, [P, C.c_char_p, P, P]),
             "ntc_trainer_on_matrix_cores": (C.c_int, [P, C.c_char_p]),
             "ntc_trainer_set_matrix_cores": (None, [P, C.c_int]),
+            "ntc_jit_compile_check": (C.c_int, [C.POINTER(ModelDesc), C.c_char_p, C.POINTER(C.c_double), C.c_char_p, C.c_size_t]),
             "ntc_trainer_dct_probe": (None, [P, P, P]),
             "ntc_trainer_dct_refit": (None, [P, P]),
             "ntc_trainer_decode_error": (None, [P, P, C.c_int, C.c_int, P, P]),
@@ -423,6 +424,14 @@ class Trainer:
     def set_matrix_cores(self, on: bool):
         """on=False: every stage on the VALU kernels from the next call on (instrumentation)"""
         self._lib.ntc_trainer_set_matrix_cores(self._h, 1 if on else 0)
+
+    @staticmethod
+    def jit_compile_check(d: ModelDesc, arch: str = "gfx950"):
+        """compile (hipRTC, no device) the kernels a trainer specialises at init for d's shape:
+        (seconds, "") or (None, the compiler's reason)"""
+        sec, why = C.c_double(), C.create_string_buffer(4096)
+        ok = library().ntc_jit_compile_check(C.byref(d), arch.encode(), C.byref(sec), why, 4096)
+        return (sec.value, "") if ok else (None, why.value.decode(errors="replace"))
 
     def kernel_time(self, name):
         ms, n = C.c_double(), C.c_longlong()

@@ -30,6 +30,11 @@ LAYOUTS = {
     "run8x3": Layout(64, 48, [(32, 24, 8, False), (16, 12, 4, False)], [24, 24], T=3, weights=[1.0, 1.0, 0.5]),
     "mat_qat1x4_36": Layout(48, 40, [(48, 40, 1, True), (12, 10, 4, True)], [36, 36], T=4, pos=[PK_LV1LOCAL],
                             leak=1 / 1024),
+    # shapes the library does not list: kernels specialised at init (hipRTC); VALU only, and with the
+    # matrix cores
+    "jit_valu_20": Layout(64, 48, [(16, 12, 4, False)], [20, 20], leak=0.01),
+    "jit_mfma_28": Layout(48, 40, [(48, 40, 2, True), (12, 10, 4, False)], [28, 28], T=4, pos=[PK_LV1LOCAL], leak=0.01,
+                          weights=[1.0, 0.5, 2.0, 1.0]),
 }
 # the same layouts with every stage forced onto the VALU kernels (ntc_trainer_set_matrix_cores(0))
 for _name in ("material", "chief1_36"):

@@ -83,7 +83,7 @@ def test_mlp_es_step(orc, name):
     assert abs(loss - 0.5 * (lp + lm).mean()) < 1e-12 and dstd > 0
 
 
-@pytest.mark.parametrize("name", ["rgb_16x2", "material", "runtime", "chief1_36", "material_valu"])
+@pytest.mark.parametrize("name", ["rgb_16x2", "material", "runtime", "chief1_36", "material_valu", "jit_valu_20", "jit_mfma_28"])
 def test_mlp_es_two_steps_and_fd(orc, name):
     lay = LAYOUTS[name]
     say("mlp es+fd", name)
@@ -139,7 +139,7 @@ def test_latent_step(orc, name):
 
 
 QAT = {"material": [2, 3], "dct_plane": [1], "runtime": [2, 1, 3], "chief1_36": [2], "mat_qat_36": [2, 2], "image3_27": [4],
-       "material_valu": [2, 3], "chief1_36_valu": [2], "mat_qat1x4_36": [2]}
+       "material_valu": [2, 3], "chief1_36_valu": [2], "mat_qat1x4_36": [2], "jit_mfma_28": [2, 1]}
 
 
 @pytest.mark.parametrize("name", list(QAT))
@@ -187,3 +187,14 @@ def test_qat_search_and_frozen_level(orc, name):
     for c in range(C0):
         col = zg[:n0].reshape(-1, C0)[:, c]
         assert np.array_equal(synth.qat_snap(col, bits[c], grid), col)
+
+
+@pytest.mark.parametrize("name", ["jit_valu_20", "jit_mfma_28"])
+def test_specialised_shape_in_use(orc, name):
+    """a shape the library does not list runs on kernels specialised for it at init, not the runtime-shaped ones"""
+    lay = LAYOUTS[name]
+    z, p, tgt = data(lay, 8)
+    tr = trainer(lay, z, p, tgt)
+    say("banner", tr.banner())
+    assert "specialised at init" in tr.banner()
+    assert tr.on_matrix_cores("pop_eval") == (name == "jit_mfma_28")
