@@ -46,33 +46,31 @@ __device__ __forceinline__ float buffer_f32(__amdgpu_buffer_rsrc_t r, uint32_t v
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
 }
 
-// Models with at most 4 outputs keep all of them in lane group 0 of a tile's output registers: the
-// two tiles of a pass are packed into one register set (tile u in lane group u) before the sigmoid and
-// the error terms, which then run once for both tiles.
+// The targets a lane needs per tile: models with at most 4 outputs take their output layer on the VALU
+// (valu_out_g), which leaves output g of pixel j in lane (g, j): one target; otherwise the D layout's
+// four (outputs 4 g + r).
 template <class S>
-constexpr bool pop_pack() { return MfmaShape<S>::kNout <= 4 && pop_u<S>() == 2; }
+constexpr int pop_nt() { return valu_out<S>() ? 1 : 4; }
 
 template <class S>
 struct PopTileIn {
     float b1[pop_u<S>()][MfmaShape<S>::kKs1];
-    float t[pop_pack<S>() ? 1 : pop_u<S>()][4];   // packed: lane group u holds tile u's targets
+    float t[pop_u<S>()][pop_nt<S>()];
 };
 
 // Inputs of tiles j .. j + U - 1 of this wave: soff = byte offset of tile j's first slot (uniform);
-// tile u sits 32 slots further per u (packed: the target offsets of lane group 1 already include it).
+// tile u sits 32 slots further per u.
 template <class S>
 __device__ __forceinline__ void pop_load(PopTileIn<S>& in, __amdgpu_buffer_rsrc_t rf, __amdgpu_buffer_rsrc_t rt, uint32_t soff,
-                                         const uint32_t (&fo)[MfmaShape<S>::kKs1], const uint32_t (&to)[4]) {
+                                         const uint32_t (&fo)[MfmaShape<S>::kKs1], const uint32_t (&to)[pop_nt<S>()]) {
     using Q = MfmaShape<S>;
 #pragma unroll
     for (int u = 0; u < pop_u<S>(); u++) {
         const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane((int)(soff + 128u * u));   // uniform: an SGPR
 #pragma unroll
         for (int ks = 0; ks < Q::kKs1; ks++) in.b1[u][ks] = buffer_f32(rf, fo[ks], so);
-        if (!pop_pack<S>() || u == 0) {
 #pragma unroll
-            for (int r = 0; r < 4; r++) in.t[u][r] = buffer_f32(rt, to[r], so);
-        }
+        for (int r = 0; r < pop_nt<S>(); r++) in.t[u][r] = buffer_f32(rt, to[r], so);
     }
 }
 
@@ -141,27 +139,26 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
     const float ak = act_k(Act, m.leak);
-    constexpr bool kPack = pop_pack<S>();
-    // the channel weight of each of this lane's output registers (rows 4 g + r; packed: rows r of
-    // lane group g's tile, groups 2 and 3 unused), zero past the last output
-    float cw[4];
+    constexpr bool kVOut = valu_out<S>();
+    constexpr int NT = pop_nt<S>();
+    // the channel weight of each of this lane's outputs (D layout: rows 4 g + r; VALU output layer:
+    // output g), zero past the last output
+    float cw[NT];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < NT; r++) {
         cw[r] = 0.0f;
 #pragma unroll
         for (int c = 0; c < Q::kNout; c++)
-            if ((kPack ? (g <= 1 && r == c) : 4 * g + r == c)) cw[r] = m.cw[c];
+            if ((kVOut ? g : 4 * g + r) == c) cw[r] = m.cw[c];
     }
-    // lane byte offsets of the feature rows 4 ks + g and target rows 4 g + r (rows past the last
-    // one are clamped to it: their weights, or their channel weights cw, are zero); packed: target
-    // row r of tile g (lane group 1 reads the pass's second tile)
-    uint32_t fo[Q::kKs1], to[4];
+    // lane byte offsets of the feature rows 4 ks + g and target rows 4 g + r, or g (rows past the last
+    // one are clamped to it: their weights, or their channel weights cw, are zero)
+    uint32_t fo[Q::kKs1], to[NT];
 #pragma unroll
     for (int ks = 0; ks < Q::kKs1; ks++) fo[ks] = 4u * ((uint32_t)min(4 * ks + g, Q::kIn - 1) * (uint32_t)Mcap + (uint32_t)i16);
 #pragma unroll
-    for (int r = 0; r < 4; r++)
-        to[r] = kPack ? 4u * ((uint32_t)min(r, Q::kNout - 1) * (uint32_t)Mcap + (uint32_t)i16) + (g == 1 ? 128u : 0u)
-                      : 4u * ((uint32_t)min(4 * g + r, Q::kNout - 1) * (uint32_t)Mcap + (uint32_t)i16);
+    for (int r = 0; r < NT; r++)
+        to[r] = 4u * ((uint32_t)min(kVOut ? g : 4 * g + r, Q::kNout - 1) * (uint32_t)Mcap + (uint32_t)i16);
     const int s0 = ch * chunk, s1 = min(M, s0 + chunk);
     const int tiles = (s1 - s0 + 15) >> 4;
     const int mine = (tiles - half + 1) >> 1;   // this wave's tiles: 2 j + half, j < mine
@@ -179,42 +176,35 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
             for (int u = 0; u < U; u++)
                 if (4 * (Q::kKs1 - 1) + g >= Q::kIn) c.b1[u][Q::kKs1 - 1] = 0.0f;
         }
-        f4v o[U];
-        mfma_forward<S, U, Act, false>(W, c.b1, ak, o);
-        if constexpr (kPack) {
-            // lane group 0 of each tile holds its outputs: tile 1's move to lane group 1
-            f4v op;
+        // this lane's outputs' channel terms cw (d d): one multiply and one fused multiply-add each,
+        // summed in float over the pass's tiles, then into the double
+        float dq[U][NT], dd[U][NT];
+        if constexpr (kVOut) {
+            float x[U][Q::kKsH];
+            mfma_hidden<S, U, Act, false>(W, c.b1, ak, x);
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                op[r] = __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(o[0][r]), __float_as_uint(o[1][r]), false, false)[0]);
-            float tsum = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float d = out_of<S>(op[r], Clamp) - c.t[0][r];
-                tsum = __builtin_fmaf(__fmul_rn(cw[r], d), d, tsum);
-            }
-            if (j + U <= mine && s0 + 16 * (2 * (j + U - 1) + half) + 16 <= s1) e += (double)tsum;   // both tiles whole (uniform)
-            else {
-                const int gu = g & 1;   // this lane's tile (groups 2, 3 carry zeros)
-                if (j + gu < mine && s0 + 16 * (2 * (j + gu) + half) + i16 < s1) e += (double)tsum;
+            for (int u = 0; u < U; u++) {
+                dd[u][0] = out_of<S>(valu_out_g<S>(W, x[u]), Clamp) - c.t[u][0];
+                dq[u][0] = __fmul_rn(cw[0], dd[u][0]);
             }
         } else {
-            // this lane's channel terms cw (d d): one multiply and one fused multiply-add each, summed in
-            // float over the pass's tiles, then into the double
-            float dq[U][4], dd[U][4];
+            f4v o[U];
+            mfma_forward<S, U, Act, false>(W, c.b1, ak, o);
 #pragma unroll
             for (int u = 0; u < U; u++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
+                for (int r = 0; r < NT; r++) {
                     dd[u][r] = out_of<S>(o[u][r], Clamp) - c.t[u][r];
                     dq[u][r] = __fmul_rn(cw[r], dd[u][r]);
                 }
+        }
+        {
             if (j + U <= mine && s0 + 16 * (2 * (j + U - 1) + half) + 16 <= s1) {   // all U tiles whole (uniform)
                 float tsum = 0.0f;
 #pragma unroll
                 for (int u = 0; u < U; u++)
 #pragma unroll
-                    for (int r = 0; r < 4; r++) tsum = __builtin_fmaf(dq[u][r], dd[u][r], tsum);
+                    for (int r = 0; r < NT; r++) tsum = __builtin_fmaf(dq[u][r], dd[u][r], tsum);
                 e += (double)tsum;
             } else {
 #pragma unroll
@@ -222,7 +212,7 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
                     const int st = s0 + 16 * (2 * (j + u) + half);   // first slot of the tile (uniform)
                     float tsum = 0.0f;
 #pragma unroll
-                    for (int r = 0; r < 4; r++) tsum = __builtin_fmaf(dq[u][r], dd[u][r], tsum);
+                    for (int r = 0; r < NT; r++) tsum = __builtin_fmaf(dq[u][r], dd[u][r], tsum);
                     if (j + u < mine && st + i16 < s1) e += (double)tsum;
                 }
             }
@@ -264,9 +254,8 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
                                                       unsigned mask, float* __restrict__ dpix) {
     using Q = MfmaShape<S>;
     constexpr int NO = Q::kNout, kLatPix = lat_pix<S>(), kRounds = kLatPix / 256;
-    // at most 4 outputs: the + member's outputs stay in lane group 0, the - member's move to group 1,
-    // and each pixel's error is one lane's chain over its channels in ascending order
-    constexpr bool kPack = NO <= 4;
+    // at most 4 outputs: the output layer on the VALU leaves output g of pixel j in lane (g, j)
+    constexpr bool kVOut = valu_out<S>();
     const int k = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
     const float* e = eps + (size_t)k * m.nz;
@@ -277,20 +266,21 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
     const float ak = act_k(Act, m.leak);
     float cw[4];
-    if constexpr (kPack) {
+    if constexpr (kVOut) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) cw[r] = (g <= 1 && r < NO) ? m.cw[r] : 0.0f;
+        for (int r = 0; r < 4; r++) cw[r] = (r == 0 && g < NO) ? m.cw[g] : 0.0f;
     } else {
         lane_cw<NO>(m.cw, g, cw);
     }
     // the targets of the tile at pixel t0: lane (g, j) reads channels 4 g .. 4 g + 3 of pixel t0 + j (one
     // 16-byte load when a pixel's row is a whole number of float4; rows past the last are clamped);
-    // packed: channels 0 .. 3 in every lane group
+    // VALU output layer: channel g
     auto load_t = [&](int t0, float (&t)[4]) {
         const int pr = min(t0 + i16, m.npix - 1);
-        if constexpr (kPack) {
+        if constexpr (kVOut) {
+            t[0] = tgt[(size_t)pr * NO + min(g, NO - 1)];
 #pragma unroll
-            for (int r = 0; r < 4; r++) t[r] = tgt[(size_t)pr * NO + min(r, NO - 1)];
+            for (int r = 1; r < 4; r++) t[r] = 0.0f;
         } else if constexpr (NO % 4 == 0) {
             const f4v v = *reinterpret_cast<const f4v*>(tgt + (size_t)pr * NO + min(4 * g, NO - 4));
 #pragma unroll
@@ -321,30 +311,26 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
             float b1[2][Q::kKs1];
 #pragma unroll
             for (int ks = 0; ks < Q::kKs1; ks++) { b1[0][ks] = bp[t][ks]; b1[1][ks] = bm[t][ks]; }
-            f4v o[2];
-            mfma_forward<S, 2, Act, false>(W, b1, ak, o);
             const int p = base + 16 * t + i16;
-            if constexpr (kPack) {
-                float ev = 0.0f;   // group 0: e+, group 1: e-
+            // each lane's channel terms cw (d d) (its four in ascending order, or its one on the VALU output
+            // layer), then the four lane groups added pairwise (permlane swaps): e+ in lanes 0-31, e- in
+            // lanes 32-63, then e+ - e-
+            float ep = 0.0f, em = 0.0f;
+            if constexpr (kVOut) {
+                float x[2][Q::kKsH];
+                mfma_hidden<S, 2, Act, false>(W, b1, ak, x);
+                const float dp = out_of<S>(valu_out_g<S>(W, x[0]), Clamp) - tt[0], dm = out_of<S>(valu_out_g<S>(W, x[1]), Clamp) - tt[0];
+                ep = __fmul_rn(cw[0], __fmul_rn(dp, dp));
+                em = __fmul_rn(cw[0], __fmul_rn(dm, dm));
+            } else {
+                f4v o[2];
+                mfma_forward<S, 2, Act, false>(W, b1, ak, o);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const float op = __uint_as_float(
-                        __builtin_amdgcn_permlane16_swap(__float_as_uint(o[0][r]), __float_as_uint(o[1][r]), false, false)[0]);
-                    const float d = out_of<S>(op, Clamp) - tt[r];
-                    ev = __builtin_fmaf(cw[r], __fmul_rn(d, d), ev);
+                    const float dp = out_of<S>(o[0][r], Clamp) - tt[r], dm = out_of<S>(o[1][r], Clamp) - tt[r];
+                    ep = __builtin_fmaf(cw[r], __fmul_rn(dp, dp), ep);
+                    em = __builtin_fmaf(cw[r], __fmul_rn(dm, dm), em);
                 }
-                const auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(ev), __float_as_uint(ev), false, false);
-                if (g == 0 && p < m.npix) out[p] = __fmul_rn(__uint_as_float(x[0]) - __uint_as_float(x[1]), m.inv_px);
-                continue;
-            }
-            // each lane's four channel terms cw (d d) in ascending order, then the four lane groups
-            // added pairwise (permlane swaps): e+ in lanes 0-31, e- in lanes 32-63, then e+ - e-
-            float ep = 0.0f, em = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float dp = out_of<S>(o[0][r], Clamp) - tt[r], dm = out_of<S>(o[1][r], Clamp) - tt[r];
-                ep = __builtin_fmaf(cw[r], __fmul_rn(dp, dp), ep);
-                em = __builtin_fmaf(cw[r], __fmul_rn(dm, dm), em);
             }
             const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(ep), __float_as_uint(em), false, false);
             const float s = __uint_as_float(h[0]) + __uint_as_float(h[1]);   // groups 0 + 2 and 1 + 3
@@ -380,8 +366,14 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
     if (!m.clamp_out) scale_output<S>(W, kNegLog2e);
     if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
     const float ak = act_k(Act, m.leak);
+    constexpr bool kVOut = valu_out<S>();   // the output layer on the VALU: output g of pixel j in lane (g, j)
     float cw[4];
-    lane_cw<NO>(m.cw, g, cw);
+    if constexpr (kVOut) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) cw[r] = (r == 0 && g < NO) ? m.cw[g] : 0.0f;
+    } else {
+        lane_cw<NO>(m.cw, g, cw);
+    }
     const int base = blockIdx.x * 256 + wave * 64;   // tile t: pixels base + 16 t + j
     float f[S::kMaxIn];
     {
@@ -390,12 +382,12 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
     }
     float b[4][Q::kKs1];
     tiles_of<S>(f, b);
-    float t4[4][4];   // targets: lane (g, j) holds channels 4 g .. 4 g + 3 of pixel j of each tile
+    float t4[4][4];   // targets: lane (g, j) holds channels 4 g .. 4 g + 3 (VALU output layer: g) of pixel j of each tile
 #pragma unroll
     for (int t = 0; t < 4; t++) {
         const int pr = min(base + 16 * t + i16, m.npix - 1);
 #pragma unroll
-        for (int r = 0; r < 4; r++) t4[t][r] = tgt[(size_t)pr * NO + min(4 * g + r, NO - 1)];
+        for (int r = 0; r < 4; r++) t4[t][r] = tgt[(size_t)pr * NO + min(kVOut ? g : 4 * g + r, NO - 1)];
     }
 #pragma unroll
     for (int c = 0; c < C0; c++) {
@@ -415,17 +407,31 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
 #pragma unroll
                     for (int ks = 0; ks < Q::kKs1; ks++) b2[v][ks] = b[t][ks];
                 if (g == c % 4) { b2[0][c / 4] = gv[kc]; b2[1][c / 4] = gv[kc + 1]; }
-                f4v o[2];
-                mfma_forward<S, 2, Act, false>(W, b2, ak, o);
+                float lv[2];   // this lane's channels, then the pixel's lanes
+                if constexpr (kVOut) {
+                    float x[2][Q::kKsH];
+                    mfma_hidden<S, 2, Act, false>(W, b2, ak, x);
+#pragma unroll
+                    for (int v = 0; v < 2; v++) {
+                        const float d = out_of<S>(valu_out_g<S>(W, x[v]), m.clamp_out != 0) - t4[t][0];
+                        lv[v] = __fmul_rn(__fmul_rn(cw[0], d), d);
+                    }
+                } else {
+                    f4v o[2];
+                    mfma_forward<S, 2, Act, false>(W, b2, ak, o);
+#pragma unroll
+                    for (int v = 0; v < 2; v++) {
+                        lv[v] = 0.0f;
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const float d = out_of<S>(o[v][r], m.clamp_out != 0) - t4[t][r];
+                            lv[v] = __builtin_fmaf(__fmul_rn(cw[r], d), d, lv[v]);
+                        }
+                    }
+                }
 #pragma unroll
                 for (int v = 0; v < 2; v++) {
-                    float l = 0.0f;   // this lane's channels, then the pixel's lanes
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const float d = out_of<S>(o[v][r], m.clamp_out != 0) - t4[t][r];
-                        l = __builtin_fmaf(__fmul_rn(cw[r], d), d, l);
-                    }
-                    l = group_sum_f(l);
+                    const float l = group_sum_f(lv[v]);
                     if (kc + v == cur) cur_l = l;
                     else if (best_k < 0 || l < best_l) { best_l = l; best_k = kc + v; }
                 }

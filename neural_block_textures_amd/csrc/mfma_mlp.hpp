@@ -83,6 +83,11 @@ __host__ __device__ constexpr int hidden_input(int ks, int g) {
     return unit_of<Q>(t, 4 * g + (ks - 4 * t));
 }
 
+// Models with at most 4 outputs take their output layer on the VALU (valu_out_g): a matrix tile would
+// spend 16 rows on them.
+template <class S>
+constexpr bool valu_out() { return MfmaShape<S>::kNout <= 4; }
+
 // One member's parameters in operand layout.
 template <class S>
 struct MfmaWeights {
@@ -91,8 +96,10 @@ struct MfmaWeights {
     f4v c1[Q::kHt];
     float ah[Q::kDeep][Q::kHt][Q::kKsH];
     f4v ch[Q::kDeep][Q::kHt];
-    float ao[Q::kKsH];
+    float ao[Q::kKsH];                    // the output layer on the matrix cores
     f4v co;
+    float wo[valu_out<S>() ? 4 : 1][Q::kKsH];   // the output layer on the VALU: output c's weight of the input this
+    float bo[valu_out<S>() ? 4 : 1];            // lane group feeds at k-step ks; output c's bias in lane group 0
 };
 
 // Gathers a member's flat parameter vector (per layer W[out][in] row-major, then b[out]) into
@@ -140,13 +147,25 @@ __device__ __forceinline__ void mfma_load_from(MfmaWeights<S>& W, const Get& w, 
         }
         p += H * H + H;
     }
+    if constexpr (valu_out<S>()) {
 #pragma unroll
-    for (int ks = 0; ks < Q::kKsH; ks++) {
-        const int in = hidden_input<Q, Exact>(ks, g);
-        W.ao[ks] = (i16 < NO && in < H) ? w(p + i16 * H + in) : 0.0f;
+        for (int c = 0; c < 4; c++) {
+#pragma unroll
+            for (int ks = 0; ks < Q::kKsH; ks++) {
+                const int in = hidden_input<Q, Exact>(ks, g);
+                W.wo[c][ks] = (c < NO && in < H) ? w(p + c * H + in) : 0.0f;
+            }
+            W.bo[c] = (c < NO && g == 0) ? w(p + NO * H + c) : 0.0f;
+        }
+    } else {
+#pragma unroll
+        for (int ks = 0; ks < Q::kKsH; ks++) {
+            const int in = hidden_input<Q, Exact>(ks, g);
+            W.ao[ks] = (i16 < NO && in < H) ? w(p + i16 * H + in) : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) W.co[r] = 4 * g + r < NO ? w(p + NO * H + 4 * g + r) : 0.0f;
     }
-#pragma unroll
-    for (int r = 0; r < 4; r++) W.co[r] = 4 * g + r < NO ? w(p + NO * H + 4 * g + r) : 0.0f;
 }
 
 // parameter k of a member: a flat vector, or w0 + sg eps as one fused operation (main.cpp:1856)
@@ -168,10 +187,19 @@ __device__ __forceinline__ void mfma_load(MfmaWeights<S>& W, const float* __rest
 // into the output layer: the pre-activations come out as the exp2 argument).
 template <class S>
 __device__ __forceinline__ void scale_output(MfmaWeights<S>& W, float sc) {
+    if constexpr (valu_out<S>()) {
 #pragma unroll
-    for (int ks = 0; ks < MfmaShape<S>::kKsH; ks++) W.ao[ks] *= sc;
+        for (int c = 0; c < 4; c++) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) W.co[r] *= sc;
+            for (int ks = 0; ks < MfmaShape<S>::kKsH; ks++) W.wo[c][ks] *= sc;
+            W.bo[c] *= sc;
+        }
+    } else {
+#pragma unroll
+        for (int ks = 0; ks < MfmaShape<S>::kKsH; ks++) W.ao[ks] *= sc;
+#pragma unroll
+        for (int r = 0; r < 4; r++) W.co[r] *= sc;
+    }
 }
 
 __device__ __forceinline__ f4v mfma4(float a, float b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
@@ -249,16 +277,15 @@ __device__ __forceinline__ void scale_hidden(MfmaWeights<S>& W, float b) {
         }
 }
 
-// U independent 16-pixel tiles through the MLP (interleaved, so one tile's activations overlap
-// the other's matrix operations): b1[u] = the first layer's B operands of tile u (input 4 ks + l / 16
-// of pixel l % 16, zero past nin); returns the output layer's pre-activations of each tile in D layout
-// (lane l, register r = output 4 (l / 16) + r of pixel l % 16). Every lane of the wave must be active.
-// Exact must match the weights' mfma_load; k is act_k(Act, leak).
+// U independent 16-pixel tiles through the hidden layers (interleaved, so one tile's activations
+// overlap the other's matrix operations): b1[u] = the first layer's B operands of tile u (input 4 ks +
+// l / 16 of pixel l % 16, zero past nin); x[u] = the last hidden layer's activations of tile u as the
+// next layer's B operands (k-step ks: hidden_input<Exact>(ks, l / 16) of pixel l % 16). Every lane of
+// the wave must be active. Exact must match the weights' mfma_load; k is act_k(Act, leak).
 template <class S, int U, int Act, bool Exact = true>
-__device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const float (&b1)[U][MfmaShape<S>::kKs1], float k,
-                                             f4v (&o)[U]) {
+__device__ __forceinline__ void mfma_hidden(const MfmaWeights<S>& W, const float (&b1)[U][MfmaShape<S>::kKs1], float k,
+                                            float (&x)[U][MfmaShape<S>::kKsH]) {
     using Q = MfmaShape<S>;
-    float x[U][Q::kKsH];
     {
         f4v acc[U][Q::kHt];
 #pragma unroll
@@ -310,12 +337,47 @@ __device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const floa
                 }
             }
     }
+}
+// ... and through the output layer on the matrix cores: the pre-activations of each tile in D layout
+// (lane l, register r = output 4 (l / 16) + r of pixel l % 16).
+template <class S, int U, int Act, bool Exact = true>
+__device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const float (&b1)[U][MfmaShape<S>::kKs1], float k,
+                                             f4v (&o)[U]) {
+    using Q = MfmaShape<S>;
+    float x[U][Q::kKsH];
+    mfma_hidden<S, U, Act, Exact>(W, b1, k, x);
 #pragma unroll
     for (int u = 0; u < U; u++) o[u] = W.co;
 #pragma unroll
     for (int ks = 0; ks < Q::kKsH; ks++)
 #pragma unroll
         for (int u = 0; u < U; u++) o[u] = mfma4(W.ao[ks], x[u][ks], o[u]);
+}
+
+// The output layer on the VALU for at most 4 outputs: lane (g, j) forms the partial sums of every
+// output over the hidden inputs it holds (x, the last hidden layer in the order mfma_hidden leaves it),
+// and a reduce-scatter over the four lane groups - two permlane32 swaps, one permlane16 swap, three adds
+// - leaves output g of pixel j in lane (g, j), summed (g0 + g2) + (g1 + g3) over the lane groups' parts.
+// Lane groups g >= nout hold zeros.
+template <class S>
+__device__ __forceinline__ float valu_out_g(const MfmaWeights<S>& W, const float (&x)[MfmaShape<S>::kKsH]) {
+    static_assert(valu_out<S>(), "at most 4 outputs");
+    constexpr int NO = MfmaShape<S>::kNout;
+    float p[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        p[c] = W.bo[c];
+        if (c < NO) {
+#pragma unroll
+            for (int ks = 0; ks < MfmaShape<S>::kKsH; ks++) p[c] = __builtin_fmaf(W.wo[c][ks], x[ks], p[c]);
+        }
+    }
+    const auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(p[0]), __float_as_uint(p[2]), false, false);
+    const auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(p[1]), __float_as_uint(p[3]), false, false);
+    const float q02 = __uint_as_float(s02[0]) + __uint_as_float(s02[1]);   // groups 0, 1: output 0; groups 2, 3: output 2
+    const float q13 = __uint_as_float(s13[0]) + __uint_as_float(s13[1]);   // groups 0, 1: output 1; groups 2, 3: output 3
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(q02), __float_as_uint(q13), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 
