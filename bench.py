@@ -259,19 +259,28 @@ def run_gpu(w, steps, warmup, fd_steps=0, seconds=0.0):
         kernels["pop_eval"] = {"ms_total": round(pop_ms, 3), "launches": pop_n, "ms_mean": round(pop_ms / pop_n, 4)}
     fd = None
     if fd_steps > 0:
-        tr.reset_mlp_adam()
-        tr.synchronize()
-        t1 = time.perf_counter()
-        for _ in range(fd_steps):
-            it += 1
+        def fd_iter():
             tr.mlp_step_fd(it, np.float32(w.fd_h), w.mlp_lr, w.mlp_batch)
             tr.lat_step(it, w.lat_sigma, w.lat_lr, w.lat_pairs)
             if w.qat_bits:
                 tr.qat_search()
+        tr.reset_mlp_adam()
+        it += 1
+        fd_iter()   # the first step sizes the weight-set buffer
+        tr.set_profiling(True, only=["pop_eval"])
+        tr.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(fd_steps):
+            it += 1
+            fd_iter()
         tr.synchronize()
         fd_el = time.perf_counter() - t1
+        fd_pop_ms, fd_pop_n = tr.kernel_time("pop_eval")
+        tr.set_profiling(False)
         fd = {"iters_per_s": fd_steps / fd_el, "ms_per_iter": 1e3 * fd_el / fd_steps,
-              "evals_per_s": (2 * (w.layout.nparams + 1) * w.mlp_batch) * fd_steps / fd_el}
+              "evals_per_s": (2 * (w.layout.nparams + 1) * w.mlp_batch) * fd_steps / fd_el,
+              "pop_eval_ms": round(fd_pop_ms / max(fd_pop_n, 1), 4),
+              "pop_kernel": "k_pop_mfma" if tr.on_matrix_cores("pop_eval") else "k_pop_eval"}
     refit = None
     if w.dct_q:   # the device refit (probe + re-snap) against the reference's host path for the same step
         tr.synchronize()

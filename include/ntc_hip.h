@@ -152,7 +152,8 @@ void ntc_trainer_set_profiling(ntc_trainer* t, int on);
  * event pair costs the stream a few microseconds */
 void ntc_trainer_set_profiling_only(ntc_trainer* t, const char* names);
 int ntc_trainer_kernel_time(ntc_trainer* t, const char* name, double* total_ms, long long* launches);
-// 1 if the stage ("pop_eval", "lat_pair", "qat_search") runs on the FP32 matrix cores for this model, else 0
+// 1 if the stage ("pop_eval": the ES and central-difference populations, "lat_pair", "qat_search") runs on
+// the FP32 matrix cores for this model, else 0
 int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage);
 /* on = 0: every stage of this trainer runs on the VALU kernels from the next call on (the matrix-core
  * kernels' parity and speed are then measured against them); on = 1 (the default): the matrix cores

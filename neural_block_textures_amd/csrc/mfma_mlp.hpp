@@ -28,25 +28,34 @@ namespace ntc_hip {
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
+// The least fraction of model multiply-adds in a shape's matrix instructions for the matrix cores to
+// take it. A 16x16x4 instruction does 32 multiply-adds per cycle, a VALU FMA 16, so 0.5 breaks even
+// on the multiply-adds alone; the matrix kernels also spend fewer VALU instructions per tile on
+// everything else, and on the MI355X 17-wide hidden layers (42-47%) ran 5-11% faster per ES
+// iteration on them (and their central-difference populations, with the exact two-instruction leaky
+// activation, 9-10% faster per launch); 7-wide ones (38%) are left to the VALU.
 #ifndef NTC_MFMA_MIN_USEFUL
-#define NTC_MFMA_MIN_USEFUL 0.5
+#define NTC_MFMA_MIN_USEFUL 0.4
 #endif
 
 // The fraction of the multiply-adds of a 16-pixel tile's matrix instructions that are the model's, for
 // an nin -> H (x NL hidden layers) -> nout MLP with the hidden tiles padded to 16 units and the padding's
-// k-steps skipped, and whether that pays off: a 16x16x4 instruction does 32 multiply-adds per cycle, a
-// VALU FMA 16, so the matrix cores take a shape when at least half of their work is the model's.
-__host__ __device__ constexpr int mfma_per_tile(int nin, int H, int NL) {
+// k-steps skipped, and whether that pays off (NTC_MFMA_MIN_USEFUL).
+// (models with at most 4 outputs take their output layer on the VALU in either case: only their hidden
+// layers count)
+__host__ __device__ constexpr int mfma_per_tile(int nin, int H, int NL, int nout) {
     return ((H + 15) / 16) * ((nin + 3) / 4) + (NL - 1) * ((H + 15) / 16) * (4 * ((H + 15) / 16 - 1) + (H - 16 * ((H + 15) / 16 - 1) + 3) / 4) +
-           (4 * ((H + 15) / 16 - 1) + (H - 16 * ((H + 15) / 16 - 1) + 3) / 4);
+           (nout <= 4 ? 0 : (4 * ((H + 15) / 16 - 1) + (H - 16 * ((H + 15) / 16 - 1) + 3) / 4));
+}
+__host__ __device__ constexpr double mfma_useful(int nin, int H, int NL, int nout) {
+    return (double)(nin * H + (NL - 1) * H * H + (nout <= 4 ? 0 : H * nout)) / (64.0 * (double)mfma_per_tile(nin, H, NL, nout));
 }
 __host__ __device__ constexpr bool mfma_pays(int nin, int H, int NL, int nout) {
-    return nout <= 16 && NL >= 1 && H >= 1 &&
-           (double)(nin * H + (NL - 1) * H * H + H * nout) >= NTC_MFMA_MIN_USEFUL * 64.0 * (double)mfma_per_tile(nin, H, NL);
+    return nout <= 16 && NL >= 1 && H >= 1 && mfma_useful(nin, H, NL, nout) >= NTC_MFMA_MIN_USEFUL;
 }
 
 template <class S, bool = S::kFixed>
-struct MfmaShape { static constexpr bool kOk = false; };
+struct MfmaShape { static constexpr bool kOk = false; static constexpr double kUseful = 0.0; };
 template <class S>
 struct MfmaShape<S, true> {
     static constexpr int kIn = S::kNin, kH = S::kH, kNL = S::kNL, kNout = S::kNout;
@@ -58,10 +67,11 @@ struct MfmaShape<S, true> {
     static constexpr int kDeep = kNL > 1 ? kNL - 1 : 1;
     static constexpr int kP = kH * kIn + kH + (kNL - 1) * (kH * kH + kH) + kNout * kH + kNout;   // parameters
     // matrix instructions per 16-pixel tile, and the fraction of their multiply-adds that are the model's
-    static constexpr int kMfmaPerTile = kHt * kKs1 + (kNL - 1) * kHt * kKsH + kKsH;
-    static_assert(kMfmaPerTile == mfma_per_tile(kIn, kH, kNL), "the runtime count must follow the tile layout");
-    static constexpr int kMacs = kIn * kH + (kNL - 1) * kH * kH + kH * kNout;
+    static constexpr int kMfmaPerTile = kHt * kKs1 + (kNL - 1) * kHt * kKsH + (kNout <= 4 ? 0 : kKsH);
+    static_assert(kMfmaPerTile == mfma_per_tile(kIn, kH, kNL, kNout), "the runtime count must follow the tile layout");
+    static constexpr int kMacs = kIn * kH + (kNL - 1) * kH * kH + (kNout <= 4 ? 0 : kH * kNout);
     static constexpr double kUseful = (double)kMacs / (64.0 * kMfmaPerTile);
+    static_assert(kUseful == mfma_useful(kIn, kH, kNL, kNout), "the runtime fraction must follow the tile layout");
     static constexpr bool kOk = mfma_pays(kIn, kH, kNL, kNout);
     // registers of hidden tile ot that hold units
     static constexpr int regs(int ot) { return ot == kHt - 1 ? kLastR : 4; }

@@ -26,13 +26,15 @@ LAYOUTS = {
     "mat_qat_36": Layout(48, 40, [(48, 40, 2, True), (12, 10, 4, True)], [36, 36], T=4, pos=[PK_LV1LOCAL],
                          leak=1 / 1024, weights=[1.0, 2.0, 0.5, 1.5]),
     "image3_27": Layout(64, 48, [(64, 48, 1, True), (8, 6, 4, False)], [27, 27], pos=[PK_LV1LOCAL], leak=1 / 1024),
+    # README.md:620's 17-wide DCT decoder: 2 hidden tiles, the second with one unit
+    "dct_17": Layout(64, 48, [(64, 48, 1, True), (16, 12, 4, False)], [17, 17], pos=[PK_LV1LOCAL], leak=1 / 1024),
     # README.md:991's 3-texture material (9 outputs) and README.md:298's 4-texture --qat 2 with a 4-channel block
     "run8x3": Layout(64, 48, [(32, 24, 8, False), (16, 12, 4, False)], [24, 24], T=3, weights=[1.0, 1.0, 0.5]),
     "mat_qat1x4_36": Layout(48, 40, [(48, 40, 1, True), (12, 10, 4, True)], [36, 36], T=4, pos=[PK_LV1LOCAL],
                             leak=1 / 1024),
     # shapes the library does not list: kernels specialised at init (hipRTC); VALU only, and with the
     # matrix cores
-    "jit_valu_20": Layout(64, 48, [(16, 12, 4, False)], [20, 20], leak=0.01),
+    "jit_valu_7": Layout(64, 48, [(16, 12, 4, False)], [7, 7], leak=0.01),
     "jit_mfma_28": Layout(48, 40, [(48, 40, 2, True), (12, 10, 4, False)], [28, 28], T=4, pos=[PK_LV1LOCAL], leak=0.01,
                           weights=[1.0, 0.5, 2.0, 1.0]),
 }

@@ -83,7 +83,8 @@ def test_mlp_es_step(orc, name):
     assert abs(loss - 0.5 * (lp + lm).mean()) < 1e-12 and dstd > 0
 
 
-@pytest.mark.parametrize("name", ["rgb_16x2", "material", "runtime", "chief1_36", "material_valu", "jit_valu_20", "jit_mfma_28"])
+@pytest.mark.parametrize("name", ["rgb_16x2", "material", "runtime", "chief1_36", "dct_17", "material_valu", "jit_valu_7",
+                                  "jit_mfma_28"])
 def test_mlp_es_two_steps_and_fd(orc, name):
     lay = LAYOUTS[name]
     say("mlp es+fd", name)
@@ -189,7 +190,18 @@ def test_qat_search_and_frozen_level(orc, name):
         assert np.array_equal(synth.qat_snap(col, bits[c], grid), col)
 
 
-@pytest.mark.parametrize("name", ["jit_valu_20", "jit_mfma_28"])
+@pytest.mark.parametrize("name,mfma", [("rgb_16x2", True), ("material", True), ("dct_17", True), ("jit_valu_7", False),
+                                       ("material_valu", False)])
+def test_matrix_core_choice(orc, name, mfma):
+    """the populations run on the matrix cores from 40% useful multiply-adds on (17-wide hidden layers: 42-47%)"""
+    lay = LAYOUTS[name]
+    z, p, tgt = data(lay, 8)
+    tr = trainer(lay, z, p, tgt)
+    assert tr.on_matrix_cores("pop_eval") == mfma
+    assert tr.on_matrix_cores("lat_pair") == mfma
+
+
+@pytest.mark.parametrize("name", ["jit_valu_7", "jit_mfma_28"])
 def test_specialised_shape_in_use(orc, name):
     """a shape the library does not list runs on kernels specialised for it at init, not the runtime-shaped ones"""
     lay = LAYOUTS[name]

@@ -7,13 +7,15 @@ from neural_block_textures_amd.trainer import PK_LV1LOCAL, Layout, Trainer
 
 
 @pytest.mark.parametrize("layout", [
-    # 6-20-20-3: the matrix cores would do 48% useful work, so only the VALU kernels are specialised
+    # 6-7-7-3: the matrix cores would do 36% useful work, so only the VALU kernels are specialised
+    Layout(64, 48, [(16, 12, 4, False)], [7, 7], leak=0.01),
+    # 6-20-20-3 (58%, the output layer on the VALU)
     Layout(64, 48, [(16, 12, 4, False)], [20, 20], leak=0.01),
     # 8-28-28-12 with --qat and lv1local: the matrix-core kernels too (84% useful)
     Layout(48, 40, [(48, 40, 2, True), (12, 10, 4, False)], [28, 28], T=4, pos=[PK_LV1LOCAL], leak=0.0),
     # 3 levels, clamp output, a leak outside [0, 1] (the selector search's general activation)
     Layout(40, 40, [(40, 40, 1, True), (10, 10, 3, False), (5, 5, 2, False)], [40, 40, 40], leak=1.5, clamp_out=True),
-], ids=["valu_20", "mfma_28", "three_levels"])
+], ids=["valu_7", "mfma_20", "mfma_28", "three_levels"])
 def test_specialised_kernels_compile(layout):
     sec, why = Trainer.jit_compile_check(Trainer.model_desc(layout))
     assert sec is not None, why
