@@ -32,6 +32,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 FP32_PEAK_TFLOPS = 157.3
+VALU_F32_PEAK_TFLOPS = 78.6   # one FP32 FMA per lane per cycle (no packed instructions)
 METRIC = "member·pixel evals/sec + ES iterations/sec (512² 4-tex, pop 8192), % roofline"
 KERNELS = ("batch", "perturb", "pop_eval", "es_grad", "adam", "lat_eps", "lat_pair", "lat_gather", "qat_search", "decode",
            "fd_sets", "qes_snap", "dct_snap", "dct_rate")
@@ -82,6 +83,9 @@ def dct_host_state(w, codes=None):
             "lam_t16": t16, "rate_scale": scale}
 
 
+MATRIX_CORES = [True]   # False: every stage on the VALU kernels (--valu)
+
+
 def make_trainer(w, z, p, tgt):
     from neural_block_textures_amd import dct_host, synth
     from neural_block_textures_amd.trainer import DctDesc, Trainer
@@ -94,6 +98,8 @@ def make_trainer(w, z, p, tgt):
                   dct_zigzag=dct_host.zigzag())
     tr = Trainer()
     tr.init(Trainer.model_desc(lay, **kw), z, p, tgt, lay)
+    if not MATRIX_CORES[0]:
+        tr.set_matrix_cores(False)
     if w.dct_q:
         h = dct_host_state(w)
         d = DctDesc()
@@ -312,13 +318,15 @@ def roofline_of(w, r):
     pe = r["kernels"]["pop_eval"]
     pop_flop = ev["population"] * 2 * macs(w.layout)
     achieved = pop_flop / (pe["ms_mean"] * 1e-3) / 1e12
-    roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": None, "kernel": r["pop_kernel"],
+    # the VALU kernels (--valu) against the FP32 VALU peak without packed instructions
+    bound, peak = ("mfma", FP32_PEAK_TFLOPS) if r["pop_kernel"] == "k_pop_mfma" else ("valu", VALU_F32_PEAK_TFLOPS)
+    roof = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4), "traffic": None, "kernel": r["pop_kernel"],
             "flop_per_launch": pop_flop, "ms_per_launch": pe["ms_mean"]}
     # HBM bytes per launch from the committed counter runs (FETCH_SIZE and WRITE_SIZE, each scaled by the
     # same counter's reading for a plain copy of known size): profiles/traffic_<workload>.json
     tpath = os.path.join(ROOT, "profiles", f"traffic_{w.name}.json")
-    if os.path.exists(tpath):
+    if os.path.exists(tpath) and bound == "mfma":
         with open(tpath) as f:
             t = json.load(f)
         roof["traffic"] = t.get("pop_eval_bytes_per_launch")
@@ -378,9 +386,12 @@ def main():
     ap.add_argument("--fd-steps", type=int, default=5, help="extra timed --mlp-fd iterations, reported apart")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--all-configs", metavar="OUT_MD", help="run the five workloads and write a table")
+    ap.add_argument("--valu", action="store_true",
+                    help="every stage on the VALU kernels (the same work; measures the matrix-core choice against the alternative)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="FLOATS",
                     help="only run a plain device copy of FLOATS floats three times (the reference for memory counters)")
     args = ap.parse_args()
+    MATRIX_CORES[0] = not args.valu
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py runs on one GPU only (asked for {max(args.gpus, world)}): this backend has no multi-GPU path; "
