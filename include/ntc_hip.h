@@ -141,6 +141,9 @@ size_t ntc_abi_sizeof(const char* name);
 size_t ntc_trainer_debug_last_losses(const ntc_trainer* t, double* lplus, double* lminus, size_t cap);
 /* the MLP weight gradient of the last ES or central-difference step (before Adam), P floats */
 size_t ntc_trainer_debug_last_wgrad(const ntc_trainer* t, float* g, size_t cap);
+/* the per-pixel loss differences (l+ - l-) / (3 wsum W H) of the last latent ES step, K x W*H floats
+ * (pair-major); returns K * W * H, 0 before the first latent step */
+size_t ntc_trainer_debug_last_dpix(const ntc_trainer* t, float* d, size_t cap);
 long long ntc_trainer_nparams(const ntc_trainer* t);
 long long ntc_trainer_nz(const ntc_trainer* t);
 void* ntc_trainer_stream(const ntc_trainer* t);        /* the hipStream_t every launch of this trainer uses */

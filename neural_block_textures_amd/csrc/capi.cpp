@@ -114,6 +114,16 @@ size_t ntc_trainer_debug_last_zgrad(const ntc_trainer* t, float* g, size_t cap) 
     return v.size();
 }
 
+size_t ntc_trainer_debug_last_dpix(const ntc_trainer* t, float* d, size_t cap) {
+    auto& I = *t->t.im;
+    const size_t n = (size_t)I.lat_last_K * (size_t)I.npix;
+    if (d && cap && n) {
+        NTC_CHECK(hipMemcpyAsync(d, I.dpix, std::min(cap, n) * sizeof(float), hipMemcpyDeviceToHost, I.stream));
+        NTC_CHECK(hipStreamSynchronize(I.stream));
+    }
+    return n;
+}
+
 size_t ntc_trainer_debug_last_losses(const ntc_trainer* t, double* lplus, double* lminus, size_t cap) {
     auto& I = *t->t.im;
     const size_t n = (size_t)I.last_N;

@@ -38,10 +38,11 @@ __global__ void __launch_bounds__(kTPB) k_lat_eps(NoiseFix nt, DevModel m, uint6
 // range table, built with the same tap arithmetic); then grad += (d * scale) * eps per channel, pair
 // after pair. With the --dct-lambda rate term, level 0 also receives (rate_scale * dbits) * scale * eps
 // right after each pair's mse term. Block = 16 texels x 4 pairs: the 64 threads sum the footprints
-// of four pairs at once (each sum in raster order), then 16 threads apply the four pairs in order.
-// A texel's gradient is then final (one block owns it), so with `adam` the block also takes the
-// texel's Adam step (the latent ES step's update, main.cpp:2036-2037).
-constexpr int kGatherTex = 16, kGatherPairs = 4;
+// of four pairs at once (each sum in raster order), then apply the four pairs in order to the texels'
+// channels (four threads per texel, each on every fourth channel). A texel's gradient is then final
+// (one block owns it), so with `adam` the block also takes the texel's Adam step (the latent ES step's
+// update, main.cpp:2036-2037).
+constexpr int kGatherTex = 16, kGatherPairs = 4, kGatherRun = 32;
 __global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevModel m, int level, int K, float scale,
                                                                          const float* __restrict__ dpix,
                                                                          const float* __restrict__ eps, const int* __restrict__ ranges,
@@ -63,29 +64,67 @@ __global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevMod
     for (int k0 = 0; k0 < K; k0 += kGatherPairs) {
         const int k = k0 + q;
         if (live && k < K) {
+            // the rectangle's values in raster order, loaded in groups and then added in order (the loads of
+            // a group overlap; the sum stays one chain). A slot past the rectangle's end adds +0, which
+            // leaves the sum as it is: the sum starts at +0 and a rounded sum is -0 only when both operands
+            // are, so it is never -0. Rectangles up to 16 wide go in groups of kGatherRun values across row
+            // ends, wider ones a row at a time in runs of 16; a one-pixel rectangle is one load.
             const float* dp = dpix + (size_t)k * m.npix;
+            const int fw = x1 - x0, n = fw * (y1 - y0);
             float d = 0.0f;
-            for (int py = y0; py < y1; py++)
-                for (int px = x0; px < x1; px++) d += dp[(size_t)py * m.W + px];
+            if (n == 1) {
+                d += dp[(size_t)y0 * m.W + x0];
+            } else if (fw <= 16) {
+                int row = y0, col = 0;   // position of the group's first slot
+                for (int s = 0; s < n; s += kGatherRun) {
+                    float v[kGatherRun];
+                    int r = row, cc = col;
+#pragma unroll
+                    for (int i = 0; i < kGatherRun; i++) {
+                        v[i] = s + i < n ? dp[(size_t)r * m.W + x0 + cc] : 0.0f;
+                        if (++cc == fw) { cc = 0; r++; }
+                    }
+                    row = r; col = cc;
+#pragma unroll
+                    for (int i = 0; i < kGatherRun; i++) d += v[i];
+                }
+            } else {
+                for (int py = y0; py < y1; py++) {
+                    const float* rw = dp + (size_t)py * m.W;
+                    for (int px = x0; px < x1; px += 16) {
+                        float v[16];
+#pragma unroll
+                        for (int i = 0; i < 16; i++) v[i] = px + i < x1 ? rw[px + i] : 0.0f;
+#pragma unroll
+                        for (int i = 0; i < 16; i++) d += v[i];
+                    }
+                }
+            }
             dsum[q][j] = d;
         }
         __syncthreads();
-        if (live && q == 0) {
-            for (int kk = k0; kk < min(K, k0 + kGatherPairs); kk++) {
-                const float wgt = dsum[kk - k0][j] * scale;
-                const float* e = eps + (size_t)kk * m.nz;
-                for (int c = 0; c < L.C; c++) grad[base + c] = __builtin_fmaf(wgt, e[base + c], grad[base + c]);
-                if (rate) {
-                    const int32_t* db = dbits + (size_t)kk * dct_n + (size_t)blk * L.C;
-                    for (int c = 0; c < L.C; c++)
-                        grad[base + c] = __builtin_fmaf(__fmul_rn(__fmul_rn(rate_scale, (float)db[c]), scale), e[base + c], grad[base + c]);
+        // the round's pairs in order on every channel of the texel (thread q takes channels q, q + 4, ...),
+        // the channel's gradient in a register; after the last round the channel's Adam step
+        if (live) {
+            const int kn = min(K, k0 + kGatherPairs) - k0;
+            const bool last = k0 + kGatherPairs >= K;
+            for (int c = q; c < L.C; c += kGatherPairs) {
+                const size_t i = (size_t)(base + c);
+                float gc = grad[i];
+                for (int kk = 0; kk < kn; kk++) {
+                    const float ei = eps[(size_t)(k0 + kk) * m.nz + i];
+                    gc = __builtin_fmaf(dsum[kk][j] * scale, ei, gc);
+                    if (rate) {
+                        const int32_t db = dbits[(size_t)(k0 + kk) * dct_n + (size_t)blk * L.C + c];
+                        gc = __builtin_fmaf(__fmul_rn(__fmul_rn(rate_scale, (float)db), scale), ei, gc);
+                    }
                 }
+                grad[i] = gc;
+                if (adam && last) adam_at(z, zm, zv, i, gc, lr, c1, c2);
             }
         }
         __syncthreads();
     }
-    if (adam && live && q == 0)
-        for (int c = 0; c < L.C; c++) adam_at(z, zm, zv, (size_t)(base + c), grad[base + c], lr, c1, c2);
 }
 
 // ---------------------------------------------------------------- launchers

@@ -552,6 +552,7 @@ void Trainer::lat_step(int /*it*/, float sigma, float lr, int K) {
     if (mask) {
         launch_lat_eps(I, K, mask);   // also clears zgrad
         launch_lat_pair(I, K, sigma, mask);
+        I.lat_last_K = K;
         if (rate) { launch_dct_rate_pairs(I, K, sigma); I.dct_last_K = K; }
         const float scale = 1.0f / (2.0f * (float)K * sigma);
         // Adam on the perturbed levels inside their gathers. The other levels' gradients are zero at

@@ -98,6 +98,7 @@ struct ntc_cuda::Trainer::Impl {
     uint8_t* dct_probe_code = nullptr;   // the device probe's codes (n)
     float* dct_gain = nullptr;           // and block gains (n)
     int dct_evals = 0, dct_last_K = 0;
+    int lat_last_K = 0;            // pairs of the last latent ES step (the K x W*H rows of dpix it wrote)
 
     int mlp_t = 0, lat_t = 0, lat_step_no = 0;
     int last_N = 0, last_M = 0, last_chunk = 1;

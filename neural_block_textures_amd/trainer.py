@@ -95,6 +95,7 @@ def library() -> C.CDLL:
             "ntc_abi_sizeof": (C.c_size_t, [C.c_char_p]),
             "ntc_trainer_debug_last_losses": (C.c_size_t, [P, P, P, C.c_size_t]),
             "ntc_trainer_debug_last_wgrad": (C.c_size_t, [P, P, C.c_size_t]),
+            "ntc_trainer_debug_last_dpix": (C.c_size_t, [P, P, C.c_size_t]),
             "ntc_trainer_nparams": (C.c_longlong, [P]),
             "ntc_trainer_nz": (C.c_longlong, [P]),
             "ntc_trainer_stream": (P, [P]),
@@ -393,6 +394,13 @@ class Trainer:
         out = np.empty(self.nz, np.float32)
         self._lib.ntc_trainer_debug_last_zgrad(self._h, out.ctypes.data, self.nz)
         return out
+
+    def debug_last_dpix(self):
+        """the per-pixel loss differences of the last latent step, [K, W*H]"""
+        n = self._lib.ntc_trainer_debug_last_dpix(self._h, None, 0)
+        out = np.empty(n, np.float32)
+        self._lib.ntc_trainer_debug_last_dpix(self._h, out.ctypes.data, n)
+        return out.reshape(-1, self.layout.W * self.layout.H) if n else out
 
     def debug_gauss(self, stream, step, pair, index0, n):
         out = np.empty(n, np.float32)

@@ -476,15 +476,62 @@ void or_fd_grad(long long P, const double* dl, const double* hh, float* grad) {
 }
 
 // LatentTrainer::step_impl, main.cpp:1974-2044, and dct_rate_pass, main.cpp:1935-1952.
+// One pair's mse scatter (main.cpp:2011-2037): every pixel in raster order adds its loss difference d to
+// each distinct tap texel of every active level, then grad += (dtex * scale) * eps per texel channel.
+static void lat_scatter_pair(const OrModel& m, unsigned active_mask, const float* d, const float* eps, float scale,
+                             std::vector<float>& dtex, float* grad) {
+    for (int l = 0; l < m.nlev; l++) {
+        if (!((active_mask >> l) & 1u)) continue;
+        const OrLevel& L = m.lv[l];
+        const size_t ntex = (size_t)L.W * L.H;
+        std::fill(dtex.begin(), dtex.begin() + ntex, 0.0f);
+        for (int py = 0; py < m.H; py++) {
+            const float v = ((float)py + 0.5f) / (float)m.H;
+            for (int px = 0; px < m.W; px++) {
+                const float u = ((float)px + 0.5f) / (float)m.W;
+                const float dp = d[(size_t)py * m.W + px];
+                const Tap t = tap_of(L, u, v);
+                dtex[(size_t)t.y0 * L.W + t.x0] += dp;
+                if (t.x1 != t.x0) dtex[(size_t)t.y0 * L.W + t.x1] += dp;
+                if (t.y1 != t.y0) {
+                    dtex[(size_t)t.y1 * L.W + t.x0] += dp;
+                    if (t.x1 != t.x0) dtex[(size_t)t.y1 * L.W + t.x1] += dp;
+                }
+            }
+        }
+        for (size_t ti = 0; ti < ntex; ti++) {
+            const float w = dtex[ti] * scale;
+            const size_t base = (size_t)L.off + ti * L.C;
+            for (int c = 0; c < L.C; c++) grad[base + c] = fmaf(w, eps[base + c], grad[base + c]);
+        }
+    }
+}
+
+static size_t max_texels(const OrModel& m) {
+    size_t maxtex = 0;
+    for (int l = 0; l < m.nlev; l++) maxtex = std::max(maxtex, (size_t)m.lv[l].W * m.lv[l].H);
+    return maxtex;
+}
+
+// The latent gradient of K pairs from given per-pixel loss differences dpix [K][W*H] and Gaussians
+// eps [K][nz] (the scatter of or_lat_grad alone, without a rate term)
+void or_lat_scatter(const OrModel* mp, const float* eps, const float* dpix, int K, unsigned active_mask, float sigma,
+                    float* grad) {
+    const OrModel& m = *mp;
+    const size_t n = (size_t)nzof(m), npix = (size_t)m.W * m.H;
+    std::vector<float> dtex(max_texels(m));
+    std::fill(grad, grad + n, 0.0f);
+    const float scale = 1.0f / (2.0f * (float)K * sigma);
+    for (int k = 0; k < K; k++) lat_scatter_pair(m, active_mask, dpix + (size_t)k * npix, eps + (size_t)k * n, scale, dtex, grad);
+}
+
 void or_lat_grad(const OrModel* mp, const float* p, const float* zdec, const float* zshadow, const float* tgt,
                  uint64_t seed, int step_no, float sigma, int K, unsigned active_mask,
                  const OrDct* dct, float rate_scale, float* grad, float* dpix, int32_t* dbits_last, int* hits) {
     const OrModel& m = *mp;
     const size_t n = (size_t)nzof(m), npix = (size_t)m.W * m.H;
-    std::vector<float> eps(n), zp(n), zm(n), ep(npix), em(npix);
-    size_t maxtex = 0;
-    for (int l = 0; l < m.nlev; l++) maxtex = std::max(maxtex, (size_t)m.lv[l].W * m.lv[l].H);
-    std::vector<float> dtex(maxtex);
+    std::vector<float> eps(n), zp(n), zm(n), ep(npix), em(npix), d(npix);
+    std::vector<float> dtex(max_texels(m));
     std::fill(grad, grad + n, 0.0f);
     const float inv_px = 1.0f / (3.0f * m.wsum * (float)m.W * (float)m.H);
     const float sg = sigma;
@@ -504,34 +551,9 @@ void or_lat_grad(const OrModel* mp, const float* p, const float* zdec, const flo
         }
         or_decode_err(mp, p, zp.data(), tgt, ep.data());
         or_decode_err(mp, p, zm.data(), tgt, em.data());
-        if (dpix) for (size_t i = 0; i < npix; i++) dpix[(size_t)k * npix + i] = (ep[i] - em[i]) * inv_px;
-        for (int l = 0; l < m.nlev; l++) {
-            if (!((active_mask >> l) & 1u)) continue;
-            const OrLevel& L = m.lv[l];
-            const size_t ntex = (size_t)L.W * L.H;
-            const float scale = 1.0f / (2.0f * (float)K * sg);
-            std::fill(dtex.begin(), dtex.begin() + ntex, 0.0f);
-            for (int py = 0; py < m.H; py++) {
-                const float v = ((float)py + 0.5f) / (float)m.H;
-                for (int px = 0; px < m.W; px++) {
-                    const float u = ((float)px + 0.5f) / (float)m.W;
-                    const size_t pi = (size_t)py * m.W + px;
-                    const float d = (ep[pi] - em[pi]) * inv_px;
-                    const Tap t = tap_of(L, u, v);
-                    dtex[(size_t)t.y0 * L.W + t.x0] += d;
-                    if (t.x1 != t.x0) dtex[(size_t)t.y0 * L.W + t.x1] += d;
-                    if (t.y1 != t.y0) {
-                        dtex[(size_t)t.y1 * L.W + t.x0] += d;
-                        if (t.x1 != t.x0) dtex[(size_t)t.y1 * L.W + t.x1] += d;
-                    }
-                }
-            }
-            for (size_t ti = 0; ti < ntex; ti++) {
-                const float w = dtex[ti] * scale;
-                const size_t base = (size_t)L.off + ti * L.C;
-                for (int c = 0; c < L.C; c++) grad[base + c] = fmaf(w, eps[base + c], grad[base + c]);
-            }
-        }
+        for (size_t i = 0; i < npix; i++) d[i] = (ep[i] - em[i]) * inv_px;
+        if (dpix) std::copy(d.begin(), d.end(), dpix + (size_t)k * npix);
+        lat_scatter_pair(m, active_mask, d.data(), eps.data(), 1.0f / (2.0f * (float)K * sg), dtex, grad);
         if (dct) {   // the rate pass of this pair, after the mse scatter
             const OrLevel& L0 = m.lv[0];
             const size_t nbc = (size_t)dct->BW * dct->BH * dct->C;

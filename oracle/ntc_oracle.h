@@ -96,6 +96,9 @@ void or_fd_grad(long long P, const double* dl, const double* hh, float* grad);
 void or_lat_grad(const OrModel* m, const float* p, const float* zdec, const float* zshadow, const float* tgt,
                  uint64_t seed, int step_no, float sigma, int K, unsigned active_mask,
                  const OrDct* dct, float rate_scale, float* grad, float* dpix, int32_t* dbits_last, int* hits);
+// the scatter of or_lat_grad alone, from given dpix [K][W*H] and eps [K][nz] (no rate term)
+void or_lat_scatter(const OrModel* m, const float* eps, const float* dpix, int K, unsigned active_mask, float sigma,
+                    float* grad);
 
 /* ---- --qat (main.cpp:2054-2139) ---- */
 void or_qat_grid(float* grid /* 9 x 257 */);

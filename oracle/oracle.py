@@ -167,6 +167,7 @@ _SIGS = {
     "fd_grad": (None, [C.c_longlong, _P, _P, _P]),
     "lat_grad": (None, [_P, _P, _P, _P, _P, C.c_uint64, C.c_int, C.c_float, C.c_int, C.c_uint, _P, C.c_float,
                         _P, _P, _P, _P]),
+    "lat_scatter": (None, [_P, _P, _P, C.c_int, C.c_uint, C.c_float, _P]),
     "qat_grid": (None, [_P]),
     "qat_index": (C.c_int, [C.c_float, C.c_int]),
     "qat_search": (None, [_P, _P, _P, _P, _P, _P]),
@@ -193,7 +194,7 @@ _SIGS = {
 }
 _ORACLE_ONLY = {
     "gauss_fill", "gauss_radius", "gauss_cosine", "mlp_es_eval", "mlp_es_grad", "adam", "mlp_fd_eval",
-    "fd_grad", "lat_grad", "dct_tables", "round_fp16", "train_iter",
+    "fd_grad", "lat_grad", "lat_scatter", "dct_tables", "round_fp16", "train_iter",
 }
 
 
@@ -335,6 +336,16 @@ class Lib:
                        step_no, sigma, K, mask, C.byref(dct) if dct is not None else None, rate_scale, g.ctypes.data,
                        dpix.ctypes.data if dpix is not None else None, dbits.ctypes.data, C.addressof(hits))
         return g, dpix, dbits[:nbc], hits.value
+
+    def lat_scatter(self, m, eps, dpix, K, mask, sigma):
+        """the latent gradient of K pairs from given dpix [K][W*H] and eps [K][nz] (or_lat_grad's scatter)"""
+        mc = model_of(m)
+        nz = sum(mc.lv[l].W * mc.lv[l].H * mc.lv[l].C for l in range(mc.nlev))
+        g = np.zeros(nz, np.float32)
+        e, d = np.ascontiguousarray(eps, np.float32), np.ascontiguousarray(dpix, np.float32)
+        assert e.size == K * nz and d.size == K * mc.W * mc.H
+        self._lat_scatter(C.byref(mc), e.ctypes.data, d.ctypes.data, K, mask, sigma, g.ctypes.data)
+        return g
 
     def qat_search(self, m, p, z, tgt, ch_bits, grid):
         """in place on level 0 of z"""

@@ -118,6 +118,25 @@ def test_mlp_es_two_steps_and_fd(orc, name):
 
 
 @pytest.mark.parametrize("name", NAMES)
+def test_latent_gather_exact(orc, name):
+    """the footprint gather sums every texel's pixel rectangle in raster order, as the reference's scatter: the
+    latent gradient is the oracle's scatter of the device's own per-pixel differences, bit for bit (4 pairs per
+    block: 3 pairs, and 6 in two rounds)"""
+    lay = LAYOUTS[name]
+    say("latent gather", name)
+    z, p, tgt = data(lay, 5)
+    seed, sigma = 7, np.float32(0.05)
+    mask = (1 << len(lay.levels)) - 1
+    for K in (3, 6):
+        tr = trainer(lay, z, p, tgt, seed=seed)
+        tr.lat_step(1, sigma, 0.02, K)
+        dpix = tr.debug_last_dpix()
+        assert dpix.shape == (K, lay.W * lay.H)
+        eps = np.concatenate([orc.gauss_fill(seed, 1, 0, k, 0, lay.nz) for k in range(K)])
+        assert np.array_equal(tr.debug_last_zgrad(), orc.lat_scatter(lay, eps, dpix, K, mask, sigma))
+
+
+@pytest.mark.parametrize("name", NAMES)
 def test_latent_step(orc, name):
     lay = LAYOUTS[name]
     say("latent", name)

@@ -79,8 +79,11 @@ def test_latent_step(orc, name):
     z, p, tgt = fx["z"], fx["p"], fx["tgt"]
     for qat in ([0, 2] if lay.levels[0][3] else [0]):
         mask = sum(1 << l for l in range(len(lay.levels)) if not (qat and l == 0))
-        g, _, _, _ = orc.lat_grad(lay, p, z, z, tgt, int(fx["es_seed"]), 7, 0.05, 3, mask)
+        g, dpix, _, _ = orc.lat_grad(lay, p, z, z, tgt, int(fx["es_seed"]), 7, 0.05, 3, mask, want_dpix=True)
         assert np.array_equal(g, fx[f"lat{qat}_grad"])
+        # the scatter alone, from the same per-pixel differences and the step's Gaussians (stream 1)
+        eps = np.concatenate([orc.gauss_fill(int(fx["es_seed"]), 1, 7, k, 0, lay.nz) for k in range(3)])
+        assert np.array_equal(orc.lat_scatter(lay, eps, dpix, 3, mask, np.float32(0.05)), fx[f"lat{qat}_grad"])
         zz = z.copy()
         orc.adam(zz, g, np.zeros_like(zz), np.zeros_like(zz), 0.02, 1)
         assert np.array_equal(zz, fx[f"lat{qat}_z"])
