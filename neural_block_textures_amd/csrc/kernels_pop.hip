@@ -23,10 +23,13 @@ bool pop_on_matrix_cores(const Impl& I) {
     return ok;
 }
 
+#ifndef NTC_POP_MIN_BLOCKS
+#define NTC_POP_MIN_BLOCKS 2048
+#endif
 int pop_chunk(const Impl& I, int pairs, int M) {
     if (pop_on_matrix_cores(I)) {
-        // at least 2048 blocks where the population allows, at least 256 slots per chunk
-        const int want = std::max(1, std::min((2048 + pairs - 1) / pairs, M / 256));
+        // at least NTC_POP_MIN_BLOCKS blocks where the population allows, at least 256 slots per chunk
+        const int want = std::max(1, std::min((NTC_POP_MIN_BLOCKS + pairs - 1) / pairs, M / 256));
         const int chunk = ((M + want - 1) / want + 15) & ~15;
         return std::max(chunk, 16);
     }
