@@ -145,11 +145,12 @@ __device__ __forceinline__ void sample_level(const DevLevel& L, int l, const Src
 // weights stream through the scalar cache into SGPRs and every MAC is one v_fma_f32.
 template <int C0_, int C1_, int C2_, int NPOS_, int H_, int NL_, int NOUT_>
 struct FixedShape {
-    static constexpr bool kFixed = true;
+    static constexpr bool kFixed = true, kUniform = true;
     static constexpr int kC0 = C0_, kC1 = C1_, kC2 = C2_, kNpos = NPOS_, kH = H_, kNL = NL_, kNout = NOUT_;
     static constexpr int kNin = C0_ + C1_ + C2_ + 2 * NPOS_;
-    static constexpr int kMaxIn = kNin, kMaxOut = NOUT_;
+    static constexpr int kMaxIn = kNin, kMaxOut = NOUT_, kMaxH = H_;
     static constexpr int kLevels = C2_ > 0 ? 3 : (C1_ > 0 ? 2 : 1);
+    static constexpr int width(int) { return H_; }   // units of hidden layer l
     static bool matches(const DevModel& m) {
         if (m.nlev != kLevels || m.npos != kNpos || m.nl != kNL || m.nout != kNout || m.nin != kNin) return false;
         const int c[3] = { kC0, kC1, kC2 };
@@ -158,9 +159,33 @@ struct FixedShape {
         return true;
     }
 };
+// The same with a width per hidden layer (H_...: layer 0 first), for the VALU kernels only (the matrix
+// kernels tile one width): the kernels compiled at init for a model whose hidden layers differ in width.
+template <int C0_, int C1_, int C2_, int NPOS_, int NOUT_, int... H_>
+struct FixedShapeW {
+    static constexpr bool kFixed = true, kUniform = false;
+    static constexpr int kC0 = C0_, kC1 = C1_, kC2 = C2_, kNpos = NPOS_, kNL = (int)sizeof...(H_), kNout = NOUT_;
+    static constexpr int kNin = C0_ + C1_ + C2_ + 2 * NPOS_;
+    static constexpr int kW[sizeof...(H_)] = { H_... };
+    static constexpr int width(int l) { return kW[l]; }
+    static constexpr int max_width() {
+        int w = 0;
+        for (int l = 0; l < kNL; l++) w = kW[l] > w ? kW[l] : w;
+        return w;
+    }
+    static constexpr int kMaxIn = kNin, kMaxOut = NOUT_, kMaxH = max_width();
+    static constexpr int kLevels = C2_ > 0 ? 3 : (C1_ > 0 ? 2 : 1);
+    static bool matches(const DevModel& m) {
+        if (m.nlev != kLevels || m.npos != kNpos || m.nl != kNL || m.nout != kNout || m.nin != kNin) return false;
+        const int c[3] = { kC0, kC1, kC2 };
+        for (int l = 0; l < m.nlev; l++) if (m.lv[l].C != c[l]) return false;
+        for (int l = 0; l < m.nl; l++) if (m.hidden[l] != kW[l]) return false;
+        return true;
+    }
+};
 // Any shape inside the envelope: runtime loops over per-thread arrays.
 struct RuntimeShape {
-    static constexpr bool kFixed = false;
+    static constexpr bool kFixed = false, kUniform = false;
     static constexpr int kC0 = 16, kC1 = 64, kC2 = 64, kNpos = kMaxPos;
     static constexpr int kMaxIn = kMaxWidth, kMaxOut = ntc_hip::kMaxOut;
     static bool matches(const DevModel&) { return true; }
@@ -294,11 +319,33 @@ __device__ __forceinline__ float output_of(float s, int clamp_out) {            
 
 // mlp_forward (main.cpp:603-627): per unit s = b[j], then s = fma(w[j][i], a[i], s) for i
 // ascending; w is the flat parameter vector (per layer W[out][in] row-major, then b[out]).
+// Hidden layers L .. kNL - 1 of a fixed shape, one compile-time layer at a time (every width a constant,
+// so the activations stay in registers): a holds layer L - 1's outputs, p points at layer L's weights.
+template <class S, int L>
+__device__ __forceinline__ void mlp_hidden_from(const DevModel& m, const CFloat*& p, float (&a)[S::kMaxH]) {
+    if constexpr (L < S::kNL) {
+        constexpr int HI = S::width(L - 1), HO = S::width(L);
+        float t[HO];
+        const CFloat* b = p + HO * HI;
+#pragma unroll
+        for (int j = 0; j < HO; j++) {
+            float s = b[j];
+#pragma unroll
+            for (int i = 0; i < HI; i++) s = __builtin_fmaf(p[j * HI + i], a[i], s);
+            t[j] = activate(s, m.leak);
+        }
+#pragma unroll
+        for (int j = 0; j < HO; j++) a[j] = t[j];
+        p = b + HO;
+        mlp_hidden_from<S, L + 1>(m, p, a);
+    }
+}
+
 template <class S>
 __device__ __forceinline__ void mlp_forward(const DevModel& m, const float* __restrict__ w, const float (&in)[S::kMaxIn],
                                             float (&out)[S::kMaxOut]) {
     if constexpr (S::kFixed) {
-        constexpr int NIN = S::kNin, H = S::kH, NO = S::kNout;
+        constexpr int NIN = S::kNin, H0 = S::width(0), HL = S::width(S::kNL - 1), NO = S::kNout;
         // The weights are read through the constant address space from an SGPR address, so every
         // load is a scalar load into SGPRs; laundering the address through an empty asm keeps the
         // loads inside the caller's pixel loop (hoisted, the P loop-invariant weights overflow the
@@ -306,39 +353,25 @@ __device__ __forceinline__ void mlp_forward(const DevModel& m, const float* __re
         w = uniform_ptr(w);
         asm volatile("" : "+s"(w));
         const CFloat* __restrict__ wc = (const CFloat*)w;
-        float a[H];
+        float a[S::kMaxH];
         {
-            const CFloat* b = wc + H * NIN;
+            const CFloat* b = wc + H0 * NIN;
 #pragma unroll
-            for (int j = 0; j < H; j++) {
+            for (int j = 0; j < H0; j++) {
                 float s = b[j];
 #pragma unroll
                 for (int i = 0; i < NIN; i++) s = __builtin_fmaf(wc[j * NIN + i], in[i], s);
                 a[j] = activate(s, m.leak);
             }
         }
-        const CFloat* p = wc + H * NIN + H;
-#pragma unroll
-        for (int l = 1; l < S::kNL; l++) {
-            float t[H];
-            const CFloat* b = p + H * H;
-#pragma unroll
-            for (int j = 0; j < H; j++) {
-                float s = b[j];
-#pragma unroll
-                for (int i = 0; i < H; i++) s = __builtin_fmaf(p[j * H + i], a[i], s);
-                t[j] = activate(s, m.leak);
-            }
-#pragma unroll
-            for (int j = 0; j < H; j++) a[j] = t[j];
-            p = b + H;
-        }
-        const CFloat* b = p + NO * H;
+        const CFloat* p = wc + H0 * NIN + H0;
+        mlp_hidden_from<S, 1>(m, p, a);
+        const CFloat* b = p + NO * HL;
 #pragma unroll
         for (int j = 0; j < NO; j++) {
             float s = b[j];
 #pragma unroll
-            for (int i = 0; i < H; i++) s = __builtin_fmaf(p[j * H + i], a[i], s);
+            for (int i = 0; i < HL; i++) s = __builtin_fmaf(p[j * HL + i], a[i], s);
             out[j] = output_of(s, m.clamp_out);
         }
     } else {

@@ -166,25 +166,44 @@ bool build_program(const std::string& csrc, const std::string& arch, const std::
 
 }   // namespace
 
+bool JitShape::uniform() const {
+    for (int l = 1; l < NL; l++) if (H[l] != H[0]) return false;
+    return true;
+}
+
 bool jit_shape_of(const DevModel& m, JitShape& s) {
-    if (m.nlev < 1 || m.nlev > 3 || m.nl < 1) return false;
-    for (int l = 1; l < m.nl; l++) if (m.hidden[l] != m.hidden[0]) return false;
+    if (m.nlev < 1 || m.nlev > 3 || m.nl < 1 || m.nl > kMaxHidden) return false;
     s.C0 = m.lv[0].C; s.C1 = m.nlev > 1 ? m.lv[1].C : 0; s.C2 = m.nlev > 2 ? m.lv[2].C : 0;
-    s.npos = m.npos; s.H = m.hidden[0]; s.NL = m.nl; s.nout = m.nout;
-    // a level of zero channels would read as "no level" in FixedShape
-    return s.C0 > 0 && (m.nlev < 2 || s.C1 > 0) && (m.nlev < 3 || s.C2 > 0) && s.H >= 1 && s.H <= kMaxWidth && s.nout >= 1;
+    s.npos = m.npos; s.NL = m.nl; s.nout = m.nout;
+    for (int l = 0; l < m.nl; l++) {
+        s.H[l] = m.hidden[l];
+        if (s.H[l] < 1 || s.H[l] > kMaxWidth) return false;
+    }
+    // a level of zero channels would read as "no level" in the fixed shapes
+    return s.C0 > 0 && (m.nlev < 2 || s.C1 > 0) && (m.nlev < 3 || s.C2 > 0) && s.nout >= 1;
 }
 
 std::string jit_shape_name(const JitShape& s) {
-    char b[96];
-    snprintf(b, sizeof(b), "ntc_hip::FixedShape<%d, %d, %d, %d, %d, %d, %d>", s.C0, s.C1, s.C2, s.npos, s.H, s.NL, s.nout);
-    return b;
+    char b[64];
+    std::string n;
+    if (s.uniform()) {
+        snprintf(b, sizeof(b), "ntc_hip::FixedShape<%d, %d, %d, %d, %d, %d, %d>", s.C0, s.C1, s.C2, s.npos, s.H[0], s.NL, s.nout);
+        return b;
+    }
+    snprintf(b, sizeof(b), "ntc_hip::FixedShapeW<%d, %d, %d, %d, %d", s.C0, s.C1, s.C2, s.npos, s.nout);
+    n = b;
+    for (int l = 0; l < s.NL; l++) n += ", " + std::to_string(s.H[l]);
+    return n + ">";
+}
+
+bool jit_shape_mfma(const JitShape& s) {
+    return s.uniform() && mfma_pays(s.C0 + s.C1 + s.C2 + 2 * s.npos, s.H[0], s.NL, s.nout);
 }
 
 bool jit_prepare(Impl& I, std::string& why) {
     if (const char* e = getenv("NTC_HIP_JIT"); e && e[0] == '0') { why = "NTC_HIP_JIT=0"; return false; }
     JitShape js;
-    if (!jit_shape_of(I.dm, js)) { why = "the hidden layers are not all one width"; return false; }
+    if (!jit_shape_of(I.dm, js)) { why = "the model is outside the fixed shapes"; return false; }
     const std::string shape = jit_shape_name(js);
     const std::string csrc = source_dir();
     std::string key_src;
@@ -197,7 +216,7 @@ bool jit_prepare(Impl& I, std::string& why) {
     hiprtcVersion(&rv_major, &rv_minor);
     key_src += "|hiprtc " + std::to_string(rv_major) + "." + std::to_string(rv_minor);
     const std::string arch = I.arch.substr(0, I.arch.find(':'));
-    const bool mfma = mfma_pays(js.C0 + js.C1 + js.C2 + 2 * js.npos, js.H, js.NL, js.nout);
+    const bool mfma = jit_shape_mfma(js);
     const std::string setkey = std::to_string(I.device) + "|" + shape + "|" + std::to_string(I.dm.leak) + "|" + std::to_string(I.dm.clamp_out) +
                                "|" + std::to_string(fnv1a(key_src));
     std::lock_guard<std::mutex> lock(g_mu);
@@ -230,9 +249,9 @@ bool jit_mfma(const Impl& I) { return I.jit && I.jit->mfma; }
 
 bool jit_compile_only(const DevModel& m, const std::string& arch, std::string& why, double* seconds) {
     JitShape js;
-    if (!jit_shape_of(m, js)) { why = "the hidden layers are not all one width"; return false; }
+    if (!jit_shape_of(m, js)) { why = "the model is outside the fixed shapes"; return false; }
     const std::string shape = jit_shape_name(js), csrc = source_dir();
-    const bool mfma = mfma_pays(js.C0 + js.C1 + js.C2 + 2 * js.npos, js.H, js.NL, js.nout);
+    const bool mfma = jit_shape_mfma(js);
     const auto t0 = std::chrono::steady_clock::now();
     for (int pop = 0; pop < (mfma ? 2 : 1); pop++) {
         std::string code;

@@ -1,10 +1,10 @@
 // Kernels specialised at init for a model whose shape is none of the compiled ones (shapes.hpp).
 //
-// A FixedShape is (level channel counts, positional generators, one hidden width, depth, outputs). A
-// model of that form that shapes.hpp does not list would otherwise run on RuntimeShape's kernels,
-// whose per-thread activation arrays live in scratch memory. Instead, at init the trainer compiles the
-// shape-templated kernels (kern_valu.hpp, and kern_pop.hpp when the matrix cores pay off) for the
-// model's FixedShape with hipRTC, from the sources next to the library, with the build's own
+// A FixedShape is (level channel counts, positional generators, one hidden width, depth, outputs);
+// FixedShapeW the same with a width per hidden layer. A model that shapes.hpp does not list would
+// otherwise run on RuntimeShape's kernels, whose per-thread activation arrays live in scratch memory.
+// Instead, at init the trainer compiles the shape-templated kernels (kern_valu.hpp, and kern_pop.hpp
+// when its hidden layers are one width and the matrix cores pay off) for the model's shape with hipRTC, from the sources next to the library, with the build's own
 // compiler options, and launches them from the loaded code object; the result is the same code the
 // library holds for its listed shapes. Code objects are cached on disk, keyed by the sources, the
 // options and the instantiations (NTC_HIP_JIT_CACHE, else $XDG_CACHE_HOME/ntc_hip or
@@ -18,11 +18,19 @@
 
 namespace ntc_hip {
 
-// The model's FixedShape parameters; false if its hidden layers are not all one width or the shape is
-// outside what FixedShape describes.
-struct JitShape { int C0, C1, C2, npos, H, NL, nout; };
+// The model's fixed-shape parameters (level channels, positional generators, outputs, the width of each
+// hidden layer); false if the model is outside what the fixed shapes describe.
+struct JitShape {
+    int C0, C1, C2, npos, NL, nout;
+    int H[kMaxHidden];
+    bool uniform() const;   // every hidden layer one width: FixedShape (and the matrix kernels may pay off)
+};
 bool jit_shape_of(const DevModel& m, JitShape& s);
-std::string jit_shape_name(const JitShape& s);   // "ntc_hip::FixedShape<C0, C1, C2, npos, H, NL, nout>"
+// "ntc_hip::FixedShape<C0, C1, C2, npos, H, NL, nout>", or for unequal widths
+// "ntc_hip::FixedShapeW<C0, C1, C2, npos, nout, H0, H1, ...>"
+std::string jit_shape_name(const JitShape& s);
+// whether the matrix-core kernels pay off for the shape (one hidden width, mfma_pays)
+bool jit_shape_mfma(const JitShape& s);
 
 // Compiles (or loads from the cache) the kernels for this trainer's model and makes them current for it
 // (I.jit); false, with a reason, when the shape is not one FixedShape describes, hipRTC or the sources

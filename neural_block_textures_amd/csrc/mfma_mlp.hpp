@@ -54,7 +54,7 @@ __host__ __device__ constexpr bool mfma_pays(int nin, int H, int NL, int nout) {
     return nout <= 16 && NL >= 1 && H >= 1 && mfma_useful(nin, H, NL, nout) >= NTC_MFMA_MIN_USEFUL;
 }
 
-template <class S, bool = S::kFixed>
+template <class S, bool = S::kFixed && S::kUniform>
 struct MfmaShape { static constexpr bool kOk = false; static constexpr double kUseful = 0.0; };
 template <class S>
 struct MfmaShape<S, true> {

@@ -356,9 +356,12 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
         std::string jwhy;
         JitShape js{};
         if (jit_prepare(I, jwhy) && jit_shape_of(I.dm, js)) {
-            char b[96];
-            snprintf(b, sizeof(b), "%d+%d+%d|%dpos|%dx%d|%d (specialised at init)", js.C0, js.C1, js.C2, js.npos, js.H, js.NL, js.nout);
-            I.shape_name = b;
+            char b[64];
+            snprintf(b, sizeof(b), "%d+%d+%d|%dpos|", js.C0, js.C1, js.C2, js.npos);
+            std::string n = b;
+            if (js.uniform()) n += std::to_string(js.H[0]) + "x" + std::to_string(js.NL);
+            else for (int l = 0; l < js.NL; l++) n += (l ? "," : "") + std::to_string(js.H[l]);
+            I.shape_name = n + "|" + std::to_string(js.nout) + " (specialised at init)";
         } else {
             fprintf(stderr, "ntc_hip backend: the runtime-shaped kernels run this model (%s)\n", jwhy.c_str());
         }

@@ -1,6 +1,7 @@
 """Layouts and helpers of the GPU parity tests (HIP path through the C ABI against the oracle)."""
 from __future__ import annotations
 
+import os
 import sys
 
 import numpy as np
@@ -43,6 +44,10 @@ for _name in ("material", "chief1_36"):
     _lay = Layout(**{k: getattr(LAYOUTS[_name], k) for k in LAYOUTS[_name].__dataclass_fields__})
     _lay.valu_only = True
     LAYOUTS[_name + "_valu"] = _lay
+# "runtime" (hidden widths 20, 12) on the runtime-shaped kernels, and the same model on the kernels
+# specialised at init for its widths (FixedShapeW)
+LAYOUTS["jit_widths"] = Layout(**{k: getattr(LAYOUTS["runtime"], k) for k in LAYOUTS["runtime"].__dataclass_fields__})
+LAYOUTS["runtime"].runtime_kernels = True
 
 
 def say(*a):
@@ -62,7 +67,18 @@ def data(layout: Layout, seed: int, zscale=0.4):
 def trainer(layout: Layout, z, p, tgt, *, max_pairs=64, max_batch=4096, seed=5, **kw):
     tr = Trainer()
     d = Trainer.model_desc(layout, max_pairs=max_pairs, max_batch=max_batch, seed=seed, **kw)
-    tr.init(d, z, p, tgt, layout)
+    if getattr(layout, "runtime_kernels", False):   # NTC_HIP_JIT=0: the runtime-shaped kernels, not specialised ones
+        old = os.environ.get("NTC_HIP_JIT")
+        os.environ["NTC_HIP_JIT"] = "0"
+        try:
+            tr.init(d, z, p, tgt, layout)
+        finally:
+            if old is None:
+                del os.environ["NTC_HIP_JIT"]
+            else:
+                os.environ["NTC_HIP_JIT"] = old
+    else:
+        tr.init(d, z, p, tgt, layout)
     if getattr(layout, "valu_only", False):
         tr.set_matrix_cores(False)
     return tr

@@ -84,7 +84,7 @@ def test_mlp_es_step(orc, name):
 
 
 @pytest.mark.parametrize("name", ["rgb_16x2", "material", "runtime", "chief1_36", "dct_17", "material_valu", "jit_valu_7",
-                                  "jit_mfma_28"])
+                                  "jit_mfma_28", "jit_widths"])
 def test_mlp_es_two_steps_and_fd(orc, name):
     lay = LAYOUTS[name]
     say("mlp es+fd", name)
@@ -159,7 +159,7 @@ def test_latent_step(orc, name):
 
 
 QAT = {"material": [2, 3], "dct_plane": [1], "runtime": [2, 1, 3], "chief1_36": [2], "mat_qat_36": [2, 2], "image3_27": [4],
-       "material_valu": [2, 3], "chief1_36_valu": [2], "mat_qat1x4_36": [2], "jit_mfma_28": [2, 1]}
+       "material_valu": [2, 3], "chief1_36_valu": [2], "mat_qat1x4_36": [2], "jit_mfma_28": [2, 1], "jit_widths": [2, 1, 3]}
 
 
 @pytest.mark.parametrize("name", list(QAT))
@@ -220,12 +220,15 @@ def test_matrix_core_choice(orc, name, mfma):
     assert tr.on_matrix_cores("lat_pair") == mfma
 
 
-@pytest.mark.parametrize("name", ["jit_valu_7", "jit_mfma_28"])
+@pytest.mark.parametrize("name", ["jit_valu_7", "jit_mfma_28", "jit_widths", "runtime"])
 def test_specialised_shape_in_use(orc, name):
-    """a shape the library does not list runs on kernels specialised for it at init, not the runtime-shaped ones"""
+    """a shape the library does not list runs on kernels specialised for it at init (hidden layers of one width:
+    FixedShape, of several: FixedShapeW), not the runtime-shaped ones, unless NTC_HIP_JIT=0 ("runtime")"""
     lay = LAYOUTS[name]
     z, p, tgt = data(lay, 8)
     tr = trainer(lay, z, p, tgt)
     say("banner", tr.banner())
-    assert "specialised at init" in tr.banner()
+    assert ("specialised at init" in tr.banner()) == (name != "runtime")
+    if name == "jit_widths":
+        assert "|20,12|" in tr.banner()
     assert tr.on_matrix_cores("pop_eval") == (name == "jit_mfma_28")

@@ -55,7 +55,7 @@ def host_snap(orc, lay, q, grid, z):
     return z, zq
 
 
-@pytest.mark.parametrize("name,bits", [("two_level", [0, 5]), ("rgb_24x2", [6]), ("runtime", [0, 3, 12])])
+@pytest.mark.parametrize("name,bits", [("two_level", [0, 5]), ("rgb_24x2", [6]), ("runtime", [0, 3, 12]), ("jit_widths", [0, 3, 12])])
 def test_qes_snap(orc, name, bits):
     lay = LAYOUTS[name]
     say("qes", name, bits)
