@@ -64,9 +64,13 @@ __global__ void __launch_bounds__(kTPB) k_fd_sets(int P, float h, const float* _
 // the member's chunk sums added in ascending order, divided by the loss norm): dl_i = l+ - l-, and the
 // blocks of weight tile 0 store dl and the pair means for the statistics.
 constexpr int kChain = 32;
+// With one segment (N <= 128 pairs) the block's sum is the gradient: the block writes it and takes the
+// weight's Adam step itself (k_es_grad_final's work, the same operations), and no second kernel runs.
 __global__ void __launch_bounds__(kTPB) k_es_grad_part(int N, int P, float scale, const double* __restrict__ lpart, int chunks,
                                                       double norm, double* __restrict__ dl, double* __restrict__ lsum,
-                                                      const float* __restrict__ eps, float* __restrict__ part) {
+                                                      const float* __restrict__ eps, float* __restrict__ part,
+                                                      float* __restrict__ grad, float* __restrict__ theta, float* __restrict__ m,
+                                                      float* __restrict__ v, float lr, float c1, float c2) {
     __shared__ float lds[kTPB / 64][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int k = blockIdx.x * 64 + lane;
@@ -74,8 +78,19 @@ __global__ void __launch_bounds__(kTPB) k_es_grad_part(int N, int P, float scale
     float wl = 0.0f;   // lane q: ((float)dl_{i0 + q}) * scale
     if (i0 + lane < i1) {
         const int i = i0 + lane;
+        // the member's chunk sums in ascending order, loaded 8 at a time (one chain of adds each)
+        const double* pp = lpart + (size_t)(2 * i) * chunks;
+        const double* pm = pp + chunks;
         double lp = 0.0, lm = 0.0;
-        for (int j = 0; j < chunks; j++) { lp += lpart[(size_t)(2 * i) * chunks + j]; lm += lpart[(size_t)(2 * i + 1) * chunks + j]; }
+        int j = 0;
+        for (; j + 8 <= chunks; j += 8) {
+            double a[8], b[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) { a[q] = pp[j + q]; b[q] = pm[j + q]; }
+#pragma unroll
+            for (int q = 0; q < 8; q++) { lp += a[q]; lm += b[q]; }
+        }
+        for (; j < chunks; j++) { lp += pp[j]; lm += pm[j]; }
         lp /= norm; lm /= norm;
         const double d = lp - lm;
         if (blockIdx.x == 0) { dl[i] = d; lsum[i] = 0.5 * (lp + lm); }
@@ -103,7 +118,12 @@ __global__ void __launch_bounds__(kTPB) k_es_grad_part(int N, int P, float scale
         float s = lds[0][lane];
 #pragma unroll
         for (int q = 1; q < kTPB / 64; q++) s += lds[q][lane];
-        part[(size_t)blockIdx.y * P + k] = s;
+        if (gridDim.y == 1) {
+            grad[k] = s;
+            adam_at(theta, m, v, (size_t)k, s, lr, c1, c2);
+        } else {
+            part[(size_t)blockIdx.y * P + k] = s;
+        }
     }
 }
 // the segments added in order, then Adam on the weight
@@ -280,11 +300,13 @@ void launch_es_update(Impl& I, int chunks, double norm, float sigma, int N, floa
     ProfScope ps(I, "es_grad");
     float* part = I.gpart;
     hipLaunchKernelGGL(k_es_grad_part, dim3(blocks_for(I.P, 64), segs), dim3(kTPB), 0, I.stream, N, I.P, scale, I.part, chunks, norm,
-                       I.dl, I.lsum, I.eps_mlp, part);
+                       I.dl, I.lsum, I.eps_mlp, part, I.wgrad, I.w, I.wm, I.wv, lr, c1, c2);
     NTC_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(k_es_grad_final, dim3(blocks_for(I.P, kTPB)), dim3(kTPB), 0, I.stream, I.P, segs, part, I.wgrad, I.w, I.wm,
-                       I.wv, lr, c1, c2);
-    NTC_CHECK(hipGetLastError());
+    if (segs > 1) {
+        hipLaunchKernelGGL(k_es_grad_final, dim3(blocks_for(I.P, kTPB)), dim3(kTPB), 0, I.stream, I.P, segs, part, I.wgrad, I.w, I.wm,
+                           I.wv, lr, c1, c2);
+        NTC_CHECK(hipGetLastError());
+    }
 }
 
 void launch_fd_finish(Impl& I, int chunks, double norm) {
