@@ -20,16 +20,16 @@ __device__ __forceinline__ int level_of(const DevModel& m, long long i) {
 }
 
 // eps[k][i] = gauss(seed, NS_LAT, step, k, i) for the ES-perturbed levels (the other levels' entries are
-// never read and are left as they are); the pair-0 threads also clear the latent gradient.
-__global__ void __launch_bounds__(kTPB) k_lat_eps(NoiseFix nt, DevModel m, uint64_t seed, uint32_t step, int K, unsigned mask,
+// never read and are left as they are); the pair-0 threads also clear the latent gradient. Grid: latent
+// entries x pairs (blockIdx.y = pair k).
+__global__ void __launch_bounds__(kTPB) k_lat_eps(NoiseFix nt, DevModel m, uint64_t seed, uint32_t step, unsigned mask,
                                                  float* __restrict__ eps, float* __restrict__ zgrad) {
-    const long long t = (long long)blockIdx.x * kTPB + threadIdx.x;
-    if (t >= (long long)K * m.nz) return;
-    const int k = (int)(t / m.nz);
-    const long long i = t - (long long)k * m.nz;
+    const long long i = (long long)blockIdx.x * kTPB + threadIdx.x;
+    if (i >= m.nz) return;
+    const int k = blockIdx.y;
     if (k == 0) zgrad[i] = 0.0f;
     const int l = level_of(m, i);
-    if ((mask >> l) & 1u) eps[t] = gauss_at(nt, noise_head(seed, NS_LAT, step, (uint32_t)k), (uint64_t)i);
+    if ((mask >> l) & 1u) eps[(size_t)k * m.nz + i] = gauss_at(nt, noise_head(seed, NS_LAT, step, (uint32_t)k), (uint64_t)i);
 }
 
 // Footprint gather for one level (the gather form of the reference's raster-order scatter,
@@ -129,10 +129,9 @@ __global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevMod
 
 // ---------------------------------------------------------------- launchers
 void launch_lat_eps(Impl& I, int K, unsigned mask) {
-    const size_t n = (size_t)K * I.nz;
     ProfScope ps(I, "lat_eps");
-    hipLaunchKernelGGL(k_lat_eps, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, I.noise, I.dm, I.d.seed,
-                       (uint32_t)I.lat_step_no, K, mask, I.eps_lat, I.zgrad);
+    hipLaunchKernelGGL(k_lat_eps, dim3(blocks_for(I.nz, kTPB), K), dim3(kTPB), 0, I.stream, I.noise, I.dm, I.d.seed,
+                       (uint32_t)I.lat_step_no, mask, I.eps_lat, I.zgrad);
     NTC_CHECK(hipGetLastError());
 }
 

@@ -544,7 +544,7 @@ void Trainer::mlp_stats(double& batch_loss, double& diff_std) {
 
 void Trainer::lat_step(int /*it*/, float sigma, float lr, int K) {
     Impl& I = *im;
-    if (K < 1) die("lat_step with no pairs");
+    if (K < 1 || K > 65535) die("lat_step takes 1 to 65535 pairs");
     const bool qat = I.d.qat > 0;
     unsigned mask = 0;
     for (int l = 0; l < I.d.nlev; l++) if (!(qat && l == 0)) mask |= 1u << l;
