@@ -83,6 +83,30 @@ def test_mlp_es_step(orc, name):
     assert abs(loss - 0.5 * (lp + lm).mean()) < 1e-12 and dstd > 0
 
 
+@pytest.mark.parametrize("name", ["rgb_16x2", "material", "dct_17", "chief1_36", "runtime", "jit_widths", "material_valu"])
+def test_mlp_es_small_batches(orc, name):
+    """minibatches of less than one 16-slot tile, one slot past a tile and a few tiles, and one or a few pairs, on
+    one trainer in a row (each call sizes its own chunks): member losses to the bar, the update one chain exactly, and
+    Adam on it bit-exact"""
+    lay = LAYOUTS[name]
+    say("mlp es small", name)
+    z, p, tgt = data(lay, 6)
+    seed, sigma, lr = 11, 0.02, 0.005
+    tr = trainer(lay, z, p, tgt, max_pairs=8, max_batch=64, seed=seed)
+    pw, m, v = p.copy(), np.zeros_like(p), np.zeros_like(p)
+    for t, (it, N, M) in enumerate([(1, 1, 1), (2, 3, 13), (3, 5, 17), (4, 2, 33), (5, 8, 64)], start=1):
+        tr.mlp_step(it, sigma, lr, N, M)
+        idx = orc.draw_batch(seed, it, M, lay.W * lay.H)
+        assert np.array_equal(tr.debug_last_batch(), idx)
+        lp, lm = tr.debug_last_losses()
+        dl_o, _, lp_o, lm_o = orc.mlp_es_eval(lay, pw, z, tgt, seed, it, sigma, N, idx)
+        assert lp.size == N and rel(lp, lp_o).max() < 1e-5 and rel(lm, lm_o).max() < 1e-5, (N, M)
+        g = orc.mlp_es_grad(p.size, N, seed, it, sigma, tr.debug_last_dl())
+        assert np.array_equal(tr.debug_last_wgrad(), g), (N, M)
+        orc.adam(pw, g, m, v, lr, t)
+        assert np.array_equal(tr.download_model()[1], pw), (N, M)
+
+
 @pytest.mark.parametrize("name", ["rgb_16x2", "material", "runtime", "chief1_36", "dct_17", "material_valu", "jit_valu_7",
                                   "jit_mfma_28", "jit_widths"])
 def test_mlp_es_two_steps_and_fd(orc, name):
