@@ -145,13 +145,13 @@ def test_mlp_es_two_steps_and_fd(orc, name):
 def test_latent_gather_exact(orc, name):
     """the footprint gather sums every texel's pixel rectangle in raster order, as the reference's scatter: the
     latent gradient is the oracle's scatter of the device's own per-pixel differences, bit for bit (4 pairs per
-    block: 3 pairs, and 6 in two rounds)"""
+    block: 1 and 3 pairs, and 6 in two rounds)"""
     lay = LAYOUTS[name]
     say("latent gather", name)
     z, p, tgt = data(lay, 5)
     seed, sigma = 7, np.float32(0.05)
     mask = (1 << len(lay.levels)) - 1
-    for K in (3, 6):
+    for K in (1, 3, 6):
         tr = trainer(lay, z, p, tgt, seed=seed)
         tr.lat_step(1, sigma, 0.02, K)
         dpix = tr.debug_last_dpix()
