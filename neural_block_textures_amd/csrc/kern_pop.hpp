@@ -243,17 +243,18 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
 // tile's + and - members are evaluated together; a pixel's error is decode_err's float sum of
 // cw (d d) over its channels (a lane's four in ascending order, then the lane groups pairwise: within
 // a few ulp of the reference's ascending chain), and dpix = (e+ - e-) * inv_px.
-// pixels per block: 512, or 256 for wide inputs
+// rounds of 64 pixels per wave, at most: 2 (512 pixels per block), or 1 for wide inputs; the launch may
+// take fewer (`rounds`) to spread a small image over more blocks
 template <class S>
-constexpr int lat_pix() { return MfmaShape<S>::kIn <= 8 ? 512 : 256; }
+constexpr int lat_rounds() { return MfmaShape<S>::kIn <= 8 ? 2 : 1; }
 
 
 template <class S, int Act, bool Clamp>
 __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* __restrict__ w, const float* __restrict__ zdec,
                                                       const float* __restrict__ eps, const float* __restrict__ tgt, float sg,
-                                                      unsigned mask, float* __restrict__ dpix) {
+                                                      unsigned mask, float* __restrict__ dpix, int rounds) {
     using Q = MfmaShape<S>;
-    constexpr int NO = Q::kNout, kLatPix = lat_pix<S>(), kRounds = kLatPix / 256;
+    constexpr int NO = Q::kNout, kRounds = lat_rounds<S>();
     // at most 4 outputs: the output layer on the VALU leaves output g of pixel j in lane (g, j)
     constexpr bool kVOut = valu_out<S>();
     const int k = blockIdx.y;
@@ -291,7 +292,8 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
         }
     };
     for (int rd = 0; rd < kRounds; rd++) {
-        const int base = blockIdx.x * kLatPix + (kLatPix / 4) * wave + 64 * rd;   // tile t: pixels base + 16 t + j
+        if (rd >= rounds) break;
+        const int base = blockIdx.x * 256 * rounds + 64 * rounds * wave + 64 * rd;   // tile t: pixels base + 16 t + j
         float tn[4];
         load_t(base, tn);
         float bp[4][Q::kKs1], bm[4][Q::kKs1];

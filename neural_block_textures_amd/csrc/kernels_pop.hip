@@ -108,17 +108,21 @@ void launch_pop_eval_es(Impl& I, int it, float sigma, int N, int M, int chunk, i
     else launch_pop_matrix<kDraw>(I, src, N, M, chunk, chunks);
 }
 
-// lat_pix<S>() for the shape the kernels were specialised for
-static int jit_lat_pix(const Impl& I) { return I.dm.nin <= 8 ? 512 : 256; }
+// rounds per wave of the latent pair kernel: lat_rounds<S>() (the shape's most; the specialised kernels'
+// shape has nin inputs), one where two would leave the launch under 2048 blocks
+static int lat_rounds_for(const Impl& I, int most, int K) {
+    if (most > 1 && (size_t)((I.npix + 511) / 512) * (size_t)K < 2048) return 1;
+    return most;
+}
 
 bool lat_pair_on_matrix_cores(const Impl& I) { return pop_on_matrix_cores(I); }
 
 template <class S, int Act>
 static void launch_lat_mfma(Impl& I, int K, float sigma, unsigned mask) {
     auto kern = I.dm.clamp_out ? k_lat_pair_mfma<S, Act, true> : k_lat_pair_mfma<S, Act, false>;
-    constexpr int kLatPix = lat_pix<S>();
-    hipLaunchKernelGGL(kern, dim3((unsigned)((I.npix + kLatPix - 1) / kLatPix), K), dim3(256), 0, I.stream, I.dm, I.w, I.zdec,
-                       I.eps_lat, I.tgt, sigma, mask, I.dpix);
+    const int rounds = lat_rounds_for(I, lat_rounds<S>(), K), pix = 256 * rounds;
+    hipLaunchKernelGGL(kern, dim3((unsigned)((I.npix + pix - 1) / pix), K), dim3(256), 0, I.stream, I.dm, I.w, I.zdec,
+                       I.eps_lat, I.tgt, sigma, mask, I.dpix, rounds);
 }
 
 void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask) {
@@ -129,10 +133,10 @@ void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask) {
     }
     if (I.jit) {
         const int act = I.dm.leak == 0.0f ? kActZero : kActFold;
-        const int lp = jit_lat_pix(I);
+        const int rounds = lat_rounds_for(I, I.dm.nin <= 8 ? 2 : 1, K), pix = 256 * rounds;
         jit_launch(k_lat_pair_mfma<ShapeMaterial, kActZero, false>, I, "k_lat_pair_mfma",
-                   std::to_string(act) + (I.dm.clamp_out ? ", true" : ", false"), dim3((unsigned)((I.npix + lp - 1) / lp), K), dim3(256), 0,
-                   I.dm, I.w, I.zdec, I.eps_lat, I.tgt, sigma, mask, I.dpix);
+                   std::to_string(act) + (I.dm.clamp_out ? ", true" : ", false"), dim3((unsigned)((I.npix + pix - 1) / pix), K), dim3(256), 0,
+                   I.dm, I.w, I.zdec, I.eps_lat, I.tgt, sigma, mask, I.dpix, rounds);
         NTC_CHECK(hipGetLastError());
         return;
     }
