@@ -84,15 +84,15 @@ std::vector<std::string> expressions(const std::string& shape, const DevModel& m
         return v;
     }
     const std::string c = m.clamp_out ? "true" : "false";
-    const bool zero = m.leak == 0.0f, unit = m.leak >= 0.0f && m.leak <= 1.0f;
+    const bool unit = m.leak >= 0.0f && m.leak <= 1.0f;
     if (unit) {
-        const int a_fd = zero ? kActZero : kActMax, a_es = zero ? kActZero : kActFold;
+        const int a_fd = kActMax, a_es = kActFold;
         v.push_back(e("k_pop_mfma", std::to_string(a_fd) + ", " + c + ", 0"));
         v.push_back(e("k_pop_mfma", std::to_string(a_es) + ", " + c + ", 1"));
         v.push_back(e("k_pop_mfma", std::to_string(a_es) + ", " + c + ", 2"));
         v.push_back(e("k_lat_pair_mfma", std::to_string(a_es) + ", " + c));
     }
-    v.push_back(e("k_qat_mfma", std::to_string(zero ? kActZero : (unit ? kActFold : kActAny))));
+    v.push_back(e("k_qat_mfma", std::to_string(unit ? kActFold : kActAny)));
     return v;
 }
 

@@ -9,10 +9,9 @@
 // On this chip an FP32 matrix instruction and a VALU instruction do not run concurrently on a
 // SIMD (a 16x16x4 f32 step costs 32 cycles, a VALU instruction 4, and their mixes take the sum),
 // so everything around the matrix operations is counted in instructions: the activation is one
-// instruction (kActZero's v_max_f32, or kActFold's fused multiply-add on hidden layers whose weights
-// were scaled by (1 + leak) / 2 when the member's weights were staged; this file is compiled with
-// relaxed NaN handling and the IEEE mode bit off, so a maximum needs no canonicalising copies); a
-// hidden layer's outputs feed the next layer in the order
+// instruction (kActFold's fused multiply-add on hidden layers whose weights were scaled by
+// (1 + leak) / 2 when the member's weights were staged, which propagates a NaN as the reference's
+// activation does); a hidden layer's outputs feed the next layer in the order
 // the matrix instruction leaves them (no transpose; each unit's sum takes its inputs in another
 // order than the reference's ascending one); the sigmoid is the hardware exp2 and reciprocal, its
 // -log2(e) folded into the output layer; a lane's channel terms cw d d are fused multiply-adds in float
@@ -244,9 +243,11 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
 // cw (d d) over its channels (a lane's four in ascending order, then the lane groups pairwise: within
 // a few ulp of the reference's ascending chain), and dpix = (e+ - e-) * inv_px.
 // rounds of 64 pixels per wave, at most: 2 (512 pixels per block), or 1 for wide inputs; the launch may
-// take fewer (`rounds`) to spread a small image over more blocks
+// take fewer (`rounds`) to spread a small image over more blocks. One rule for the kernel and its
+// launchers (the host checks a launch's rounds against it: the kernel stops at this count).
+__host__ __device__ constexpr int lat_rounds_of(int nin) { return nin <= 8 ? 2 : 1; }
 template <class S>
-constexpr int lat_rounds() { return MfmaShape<S>::kIn <= 8 ? 2 : 1; }
+constexpr int lat_rounds() { return lat_rounds_of(MfmaShape<S>::kIn); }
 
 
 template <class S, int Act, bool Clamp>
@@ -416,7 +417,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
 #pragma unroll
                     for (int v = 0; v < 2; v++) {
                         const float d = out_of<S>(valu_out_g<S>(W, x[v]), m.clamp_out != 0) - t4[t][0];
-                        lv[v] = __fmul_rn(__fmul_rn(cw[0], d), d);
+                        lv[v] = __fmul_rn(cw[0], __fmul_rn(d, d));   // cw (d d), main.cpp:2119
                     }
                 } else {
                     f4v o[2];
@@ -427,7 +428,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
 #pragma unroll
                         for (int r = 0; r < 4; r++) {
                             const float d = out_of<S>(o[v][r], m.clamp_out != 0) - t4[t][r];
-                            lv[v] = __builtin_fmaf(__fmul_rn(cw[r], d), d, lv[v]);
+                            lv[v] = __builtin_fmaf(cw[r], __fmul_rn(d, d), lv[v]);
                         }
                     }
                 }

@@ -14,7 +14,7 @@ bool qat_on_matrix_cores(const Impl& I) {
     return ok;
 }
 
-// the population and latent-pair evaluations on the matrix cores take 0 <= leak <= 1 (kActZero, kActFold)
+// the population and latent-pair evaluations on the matrix cores take 0 <= leak <= 1 (kActFold, kActMax)
 bool pop_on_matrix_cores(const Impl& I) {
     if (I.valu_only || !(I.dm.leak >= 0.0f && I.dm.leak <= 1.0f)) return false;
     if (I.jit) return jit_mfma(I);
@@ -58,8 +58,8 @@ static void check_pop_launch(const Impl& I, int pairs, int chunk, int chunks) {
 template <int From>
 static void launch_pop_matrix(Impl& I, const PopSource& src, int pairs, int M, int chunk, int chunks) {
     if (I.jit) {   // the same choice of activation as below
-        const int act = I.dm.leak == 0.0f ? kActZero : (From == kSets ? kActMax : kActFold);
-        jit_launch(k_pop_mfma<ShapeMaterial, kActZero, false, From>, I, "k_pop_mfma",
+        const int act = From == kSets ? kActMax : kActFold;
+        jit_launch(k_pop_mfma<ShapeMaterial, kActFold, false, From>, I, "k_pop_mfma",
                    std::to_string(act) + (I.dm.clamp_out ? ", true, " : ", false, ") + std::to_string(From), dim3(pairs, chunks),
                    dim3(64 * kPopWaves), 0, I.dm, src, M, I.Mcap, chunk, chunks, I.feat, I.btgt, I.part);
         NTC_CHECK(hipGetLastError());
@@ -70,8 +70,7 @@ static void launch_pop_matrix(Impl& I, const PopSource& src, int pairs, int M, i
         if constexpr (MfmaShape<S>::kOk) {
             // central differences compare members one weight apart (w_j +- h): their activations are the
             // reference's bit for bit; the ES members (w +- sigma eps) take the one-instruction folded form
-            if (I.dm.leak == 0.0f) launch_pop_mfma<S, kActZero, From>(I, src, pairs, M, chunk, chunks);
-            else if constexpr (From == kSets) launch_pop_mfma<S, kActMax, From>(I, src, pairs, M, chunk, chunks);
+            if constexpr (From == kSets) launch_pop_mfma<S, kActMax, From>(I, src, pairs, M, chunk, chunks);
             else launch_pop_mfma<S, kActFold, From>(I, src, pairs, M, chunk, chunks);
         }
     });
@@ -108,9 +107,15 @@ void launch_pop_eval_es(Impl& I, int it, float sigma, int N, int M, int chunk, i
     else launch_pop_matrix<kDraw>(I, src, N, M, chunk, chunks);
 }
 
-// rounds per wave of the latent pair kernel: lat_rounds<S>() (the shape's most; the specialised kernels'
-// shape has nin inputs), one where two would leave the launch under 2048 blocks
+// rounds per wave of the latent pair kernel: lat_rounds_of(nin) (the shape's most; the compiled shape has
+// nin inputs), one where two would leave the launch under 2048 blocks. A count above the compiled kernel's
+// would leave pixels of every block unevaluated: refused.
 static int lat_rounds_for(const Impl& I, int most, int K) {
+    if (most < 1 || most > lat_rounds_of(I.dm.nin)) {
+        fprintf(stderr, "ntc_hip backend: latent pair launch with %d rounds for a %d-input model (at most %d)\n", most, I.dm.nin,
+                lat_rounds_of(I.dm.nin));
+        exit(1);
+    }
     if (most > 1 && (size_t)((I.npix + 511) / 512) * (size_t)K < 2048) return 1;
     return most;
 }
@@ -120,6 +125,7 @@ bool lat_pair_on_matrix_cores(const Impl& I) { return pop_on_matrix_cores(I); }
 template <class S, int Act>
 static void launch_lat_mfma(Impl& I, int K, float sigma, unsigned mask) {
     auto kern = I.dm.clamp_out ? k_lat_pair_mfma<S, Act, true> : k_lat_pair_mfma<S, Act, false>;
+    static_assert(lat_rounds<S>() >= 1, "a latent pair kernel takes at least one round");
     const int rounds = lat_rounds_for(I, lat_rounds<S>(), K), pix = 256 * rounds;
     hipLaunchKernelGGL(kern, dim3((unsigned)((I.npix + pix - 1) / pix), K), dim3(256), 0, I.stream, I.dm, I.w, I.zdec,
                        I.eps_lat, I.tgt, sigma, mask, I.dpix, rounds);
@@ -132,9 +138,9 @@ void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask) {
         return;
     }
     if (I.jit) {
-        const int act = I.dm.leak == 0.0f ? kActZero : kActFold;
-        const int rounds = lat_rounds_for(I, I.dm.nin <= 8 ? 2 : 1, K), pix = 256 * rounds;
-        jit_launch(k_lat_pair_mfma<ShapeMaterial, kActZero, false>, I, "k_lat_pair_mfma",
+        const int act = kActFold;
+        const int rounds = lat_rounds_for(I, lat_rounds_of(I.dm.nin), K), pix = 256 * rounds;
+        jit_launch(k_lat_pair_mfma<ShapeMaterial, kActFold, false>, I, "k_lat_pair_mfma",
                    std::to_string(act) + (I.dm.clamp_out ? ", true" : ", false"), dim3((unsigned)((I.npix + pix - 1) / pix), K), dim3(256), 0,
                    I.dm, I.w, I.zdec, I.eps_lat, I.tgt, sigma, mask, I.dpix, rounds);
         NTC_CHECK(hipGetLastError());
@@ -143,8 +149,7 @@ void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask) {
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         if constexpr (MfmaShape<S>::kOk) {
-            if (I.dm.leak == 0.0f) launch_lat_mfma<S, kActZero>(I, K, sigma, mask);
-            else launch_lat_mfma<S, kActFold>(I, K, sigma, mask);
+            launch_lat_mfma<S, kActFold>(I, K, sigma, mask);
         }
     });
     NTC_CHECK(hipGetLastError());
@@ -153,8 +158,8 @@ void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask) {
 void launch_qat_mfma(Impl& I) {
     if (I.jit) {
         const float leak = I.dm.leak;
-        const int act = leak == 0.0f ? kActZero : (leak > 0.0f && leak <= 1.0f ? kActFold : kActAny);
-        jit_launch(k_qat_mfma<ShapeMaterial, kActZero>, I, "k_qat_mfma", std::to_string(act), dim3((unsigned)((I.npix + 255) / 256)),
+        const int act = leak >= 0.0f && leak <= 1.0f ? kActFold : kActAny;
+        jit_launch(k_qat_mfma<ShapeMaterial, kActFold>, I, "k_qat_mfma", std::to_string(act), dim3((unsigned)((I.npix + 255) / 256)),
                    dim3(256), 0, I.dm, I.w, I.zdec, I.tgt, I.qat_bits, I.qat_grid);
         NTC_CHECK(hipGetLastError());
         return;
@@ -164,8 +169,7 @@ void launch_qat_mfma(Impl& I) {
         if constexpr (MfmaShape<S>::kOk)
         {
             const float leak = I.dm.leak;
-            auto kern = leak == 0.0f ? k_qat_mfma<S, kActZero>
-                                     : (leak > 0.0f && leak <= 1.0f ? k_qat_mfma<S, kActFold> : k_qat_mfma<S, kActAny>);
+            auto kern = leak >= 0.0f && leak <= 1.0f ? k_qat_mfma<S, kActFold> : k_qat_mfma<S, kActAny>;
             hipLaunchKernelGGL(kern, dim3((unsigned)((I.npix + 255) / 256)), dim3(256), 0, I.stream, I.dm, I.w, I.zdec, I.tgt,
                                I.qat_bits, I.qat_grid);
         }

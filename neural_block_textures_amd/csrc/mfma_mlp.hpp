@@ -243,21 +243,25 @@ __device__ __forceinline__ void tiles_of(const float (&f)[S::kMaxIn], float (&b)
     }
 }
 
-// How a kernel applies the activation of main.cpp:560, x > 0 ? x : leak x, to the matrix results.
+// How a kernel applies the activation of main.cpp:560, x > 0 ? x : leak x, to the matrix results. Every
+// form propagates a NaN pre-activation as the reference's does (NaN > 0 is false and leak NaN is NaN),
+// so a diverged member shows up as a NaN loss and a NaN update, never as a finite loss.
 enum ActMode : int {
     kActAny = 0,    // any leak: a compare and a select
     kActMax = 1,    // 0 <= leak <= 1: max(x, leak x), bit for bit (also for signed zeros), one multiply and one maximum
-    kActZero = 2,   // leak = 0: max(x, -0), one instruction (x > 0: x, otherwise a zero)
-    kActFold = 3,   // 0 < leak <= 1, with every hidden layer's weights and biases scaled by b = (1 + leak) / 2
+                    // (a NaN x makes both operands NaN, so the maximum is NaN)
+    kActFold = 3,   // 0 <= leak <= 1, with every hidden layer's weights and biases scaled by b = (1 + leak) / 2
                     // (scale_hidden): x' = b x and act = x' + c |x'| with c = (1 - leak) / (1 + leak), one fused
                     // multiply-add with an absolute-value operand - x for x > 0, leak x otherwise, within two
-                    // roundings of the reference's value
+                    // roundings of the reference's value; for leak 0 (b = 1/2, c = 1) the value is the
+                    // reference's exactly (scaling by 1/2 commutes with every rounding of the matrix chain;
+                    // weights of magnitude below 2^-125 aside), except that a negative x gives +0 where the
+                    // reference gives -0, which changes no sum it enters
 };
 // k: leak (kActAny, kActMax) or c (kActFold)
 template <int Act>
 __device__ __forceinline__ float act(float x, float k) {
     if constexpr (Act == kActMax) return fmaxf(x, k * x);
-    else if constexpr (Act == kActZero) return fmaxf(x, -0.0f);
     else if constexpr (Act == kActFold) return __builtin_fmaf(k, __builtin_fabsf(x), x);
     else return x > 0.0f ? x : k * x;
 }

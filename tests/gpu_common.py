@@ -1,13 +1,15 @@
 """Layouts and helpers of the GPU parity tests (HIP path through the C ABI against the oracle)."""
 from __future__ import annotations
 
+import ctypes as C
 import os
 import sys
 
 import numpy as np
 
 from neural_block_textures_amd import synth
-from neural_block_textures_amd.trainer import PK_LV1LOCAL, PK_UV, Layout, Trainer
+from neural_block_textures_amd.trainer import PK_LV1LOCAL, PK_UV, DctDesc, Layout, Trainer
+from oracle.oracle import OrDct, OrLevel
 
 # One layout per compiled MLP shape, at sizes the oracle finishes in seconds, plus one that runs
 # through the runtime-shaped kernels (3 levels, lv1local, clamp output, ratios not powers of 2).
@@ -87,3 +89,61 @@ def trainer(layout: Layout, z, p, tgt, *, max_pairs=64, max_batch=4096, seed=5, 
 def rel(a, b):
     a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
     return np.abs(a - b) / np.maximum(np.abs(b), 1e-300)
+
+
+def dct_tables(orc):
+    b, zz, ak = np.zeros(64, np.float32), np.zeros(64, np.int32), np.zeros(16, np.float32)
+    orc.lib.or_dct_tables(b.ctypes.data, zz.ctypes.data, ak.ctypes.data)
+    return b, zz
+
+
+class HostDct:
+    """The host side of a DCT-coded level 0: codes, symbols, steps, bits (the oracle computes them)."""
+
+    def __init__(self, orc, lay, q, dc_step=4, deadzone=0, lam=0.0, lo16=4, rate="both"):
+        self.orc = orc
+        W, H, C0, _ = lay.levels[0]
+        self.L0 = OrLevel(W, H, C0, 1, 0)
+        self.C, self.BW, self.BH = C0, W // 8, H // 8
+        self.n = self.BW * self.BH * C0
+        self.steps = np.zeros(C0 * 1024, np.int32)
+        for c in range(C0):
+            orc._dct_build_steps(q[c], dc_step, self.steps[c * 1024:].ctypes.data)
+        self.code = np.zeros(self.n, np.uint8)
+        self.sym = np.zeros(self.n * 64, np.int16)
+        self.rate_es = lam > 0 and rate != "trunc"
+        self.rate_trunc = lam > 0 and rate != "es"
+        gk = lambda k: (14 / 64) * 2 ** (0.6 * k)
+        self.lam_t16 = np.array([np.float32(lam / (gk(k) * gk(k) * 16.0)) if self.rate_trunc else 0.0
+                                 for k in range(16)], np.float32)
+        self.rate_scale = np.float32(lam / (16.0 * 65025.0 * lay.W * lay.H)) if self.rate_es else np.float32(0)
+        self.d = OrDct()
+        self.d.C, self.d.BW, self.d.BH, self.d.dc_step, self.d.deadzone, self.d.lo_w16 = C0, self.BW, self.BH, dc_step, deadzone, lo16
+        for k in range(16):
+            self.d.lam_t16[k] = self.lam_t16[k]
+        self.d.step = self.steps.ctypes.data_as(C.POINTER(C.c_int))
+        self.d.code = self.code.ctypes.data_as(C.POINTER(C.c_uint8))
+        self.d.sym = self.sym.ctypes.data_as(C.POINTER(C.c_int16))
+        self.dc_step, self.deadzone, self.lo16 = dc_step, deadzone, lo16
+
+    def desc(self):
+        d = DctDesc()
+        d.live, d.C, d.BW, d.BH, d.N, d.dc_step = 1, self.C, self.BW, self.BH, 8, self.dc_step
+        d.rate_es, d.rate_trunc, d.rate_scale = int(self.rate_es), int(self.rate_trunc), self.rate_scale
+        for k in range(16):
+            d.lam_t16[k] = self.lam_t16[k]
+        d.lo_w16, d.deadzone = self.lo16, self.deadzone
+        return d
+
+    def probe(self, lay, p, zdec):
+        self.orc._dct_probe_codes(C.byref(__import__("oracle.oracle", fromlist=["model_of"]).model_of(lay)),
+                                  p.ctypes.data, zdec.ctypes.data, C.byref(self.d), self.code.ctypes.data)
+
+    def snap(self, z):
+        """dct_snap_level0 on a copy: (clamped shadow, plane, bits, counts); symbols land in self.sym"""
+        n0 = self.L0.W * self.L0.H * self.C
+        zs, zq = z[:n0].copy(), np.zeros(n0, np.float32)
+        bits, cnt = np.zeros(self.n, np.int32), np.zeros(3, np.int64)
+        self.orc._dct_snap_level0(C.byref(self.d), C.byref(self.L0), zs.ctypes.data, zq.ctypes.data, bits.ctypes.data,
+                                  cnt.ctypes.data)
+        return zs, zq, bits, cnt

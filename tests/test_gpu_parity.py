@@ -256,3 +256,53 @@ def test_specialised_shape_in_use(orc, name):
     if name == "jit_widths":
         assert "|20,12|" in tr.banner()
     assert tr.on_matrix_cores("pop_eval") == (name == "jit_mfma_28")
+
+
+@pytest.mark.parametrize("name", ["rgb_16x2", "material", "large", "material_valu", "runtime"])
+def test_nan_member_propagates(orc, name):
+    """A diverged model (one NaN weight in the second hidden layer) gives NaN member losses, a NaN update, a
+    NaN decode and NaN per-pixel latent differences, as the reference's activation propagates a NaN
+    (main.cpp:560) - on the matrix-core kernels (leak 0 and leak > 0) and on the VALU ones."""
+    lay = LAYOUTS[name]
+    say("nan", name)
+    z, p, tgt = data(lay, 9)
+    h = lay.hidden[0]
+    p = p.copy()
+    p[lay.nin * h + h + 3] = np.nan
+    tr = trainer(lay, z, p, tgt, max_pairs=8, max_batch=512)
+    tr.mlp_step(1, 0.02, 0.0, 8, 512)
+    lp, lm = tr.debug_last_losses()
+    assert np.isnan(lp).all() and np.isnan(lm).all()
+    assert np.isnan(orc.loss_subset(lay, p, z, tgt, tr.debug_last_batch()))
+    assert np.isnan(tr.debug_last_wgrad()).all()
+    assert np.isnan(tr.decode_full()).all()
+    tr.lat_step(1, 0.05, 0.0, 2)
+    assert np.isnan(tr.debug_last_dpix()).all()
+    tr.close()
+
+
+@pytest.mark.parametrize("name,K", [("material", 512), ("rgb_16x2", 256)])
+def test_latent_step_two_rounds(orc, name, K):
+    """Enough pairs that ceil(W H / 512) K >= 2048: the latent pair kernel takes two 64-pixel rounds per wave
+    (512-pixel blocks), the launch the full-size workloads use (models with at most 8 inputs). The per-pixel
+    differences and the gradient against the oracle at the reference's bar (1e-3 of RMS, main.cpp:3088),
+    the gather exactly as the oracle's scatter of the device's own differences, Adam bit for bit."""
+    lay = LAYOUTS[name]
+    assert lay.nin <= 8 and -(-lay.W * lay.H // 512) * K >= 2048
+    say("latent two rounds", name, K)
+    z, p, tgt = data(lay, 5)
+    seed, sigma, lr = 7, np.float32(0.05), 0.02
+    tr = trainer(lay, z, p, tgt, seed=seed)
+    tr.lat_step(1, sigma, lr, K)
+    mask = (1 << len(lay.levels)) - 1
+    g_o, dpix_o, _, _ = orc.lat_grad(lay, p, z, z, tgt, seed, 0, sigma, K, mask, want_dpix=True)
+    dpix = tr.debug_last_dpix()
+    d_rms = np.sqrt((dpix_o.astype(np.float64) ** 2).mean())
+    assert np.abs(dpix.ravel() - dpix_o).max() < 1e-3 * d_rms
+    g = tr.debug_last_zgrad()
+    assert np.abs(g - g_o).max() < 1e-3 * np.sqrt((g_o.astype(np.float64) ** 2).mean())
+    eps = np.concatenate([orc.gauss_fill(seed, 1, 0, k, 0, lay.nz) for k in range(K)])
+    assert np.array_equal(g, orc.lat_scatter(lay, eps, dpix, K, mask, sigma))
+    zz, m, v = z.copy(), np.zeros_like(z), np.zeros_like(z)
+    orc.adam(zz, g, m, v, lr, 1)
+    assert np.array_equal(tr.download_model()[0], zz)

@@ -4,6 +4,7 @@ size-independent properties (an unperturbed population has exactly zero loss dif
 equal member losses; member losses of sampled pairs match the oracle on the device's own
 minibatch; frozen levels get exactly zero gradient; every --qat value stays on its grid)."""
 import ctypes as C
+import time
 
 import numpy as np
 import pytest
@@ -11,8 +12,8 @@ import pytest
 from neural_block_textures_amd import synth
 from neural_block_textures_amd.configs import workloads
 from neural_block_textures_amd.trainer import Layout
-from oracle.oracle import OrTrainCfg, OrTrainState, model_of
-from tests.gpu_common import rel, say, trainer
+from oracle.oracle import OrTrainCfg, OrTrainState, have_reference, model_of, oracle, reference
+from tests.gpu_common import HostDct, dct_tables, rel, say, trainer
 
 pytestmark = pytest.mark.gpu
 
@@ -79,37 +80,87 @@ def full_trainer(name, **kw):
     maps = synth.material(w.seed, lay.W, lay.H) if lay.T == 4 else [synth.rgb_texture(w.seed, lay.W, lay.H)]
     tgt = synth.target_from_maps(maps)
     z, p = synth.init_model(lay, w.seed, qat_bits=w.qat_bits)
+    if w.dct_q:
+        basis, zz = dct_tables(_orc())
+        kw.update(dct={"C": lay.levels[0][2], "q": w.dct_q, "dc_step": 4}, dct_basis=basis, dct_zigzag=zz)
     tr = trainer(lay, z, p, tgt, max_pairs=w.mlp_pairs, max_batch=w.mlp_batch, seed=w.seed, qat_bits=w.qat_bits,
                  qat_grid=synth.qat_grid() if w.qat_bits else None, **kw)
     return w, lay, tr, z, p, tgt
 
 
-@pytest.mark.parametrize("name", ["rgb512_two_level", "material512", "material2048"])
+def _orc():
+    return oracle()
+
+
+def live_dct(orc, w, lay, tr, z, p, tgt):
+    """the workload's --dct-q level switched live as the reference's DCT switch does it (main.cpp:4099-4120):
+    scale codes from the decoder sensitivity probe (the device's, checked against the oracle's), the host
+    snap of the shadow, set_dct; then one rate-pass latent step with lr 0 and the device snap, all exact
+    against the oracle at the full size"""
+    H = HostDct(orc, lay, w.dct_q, deadzone=0, lam=0.5, lo16=4, rate="both")
+    n0 = lay.levels[0][0] * lay.levels[0][1] * lay.levels[0][2]
+    zd, _ = tr.download_model()
+    assert np.array_equal(zd[:n0], np.clip(z[:n0], -1, 1))
+    code_d, _ = tr.dct_probe()
+    H.probe(lay, p, tr.download_zq())
+    differ = int((code_d != H.code).sum())
+    say(f"{w.name}: device probe codes differing from the oracle's: {differ} of {H.n}")
+    assert differ <= max(2, H.n // 100) and np.all(np.abs(code_d.astype(int) - H.code.astype(int)) <= 1)
+    H.code[:] = code_d
+    zs, zq, bits, cnt = H.snap(zd)
+    tr.set_dct(H.desc(), H.code, H.sym, H.steps)
+    sym_d, c_d = tr.download_dct()
+    assert np.array_equal(sym_d, H.sym) and np.array_equal(c_d, H.code)
+    assert np.array_equal(tr.download_zq()[:n0], zq)
+    K = w.lat_pairs
+    tr.lat_step(1, w.lat_sigma, 0.0, K)               # the rate pass of every pair; lr 0 leaves the shadow
+    zd2, _ = tr.download_model()
+    assert np.array_equal(zd2, zd)
+    bits_d, dbits_d, nt_d, nz_d, hits_d, evals_d = tr.download_dct_rate()
+    zdec = tr.download_zq()
+    g_o, _, dbits_o, hits_o = orc.lat_grad(lay, p, zdec, zd2, tgt, w.seed, 0, w.lat_sigma, K, 3, dct=H.d,
+                                           rate_scale=float(H.rate_scale))
+    say(f"{w.name}: rate pass bit differences nonzero on {hits_d} of {H.n * K} (block, channel, pair)")
+    assert np.array_equal(dbits_d, dbits_o) and hits_d == hits_o and evals_d == H.n * K
+    g = tr.debug_last_zgrad()
+    assert np.abs(g - g_o).max() < 1e-3 * np.sqrt((g_o.astype(np.float64) ** 2).mean())
+    zs2, zq2, bits2, cnt2 = H.snap(zd2)
+    sym_d, _ = tr.download_dct()
+    assert np.array_equal(sym_d, H.sym) and np.array_equal(tr.download_zq()[:n0], zq2)
+    assert np.array_equal(bits_d, bits2) and (nt_d, nz_d) == (cnt2[0], cnt2[1])
+    say(f"{w.name}: snap of {H.n} blocks exact: {int(bits2.sum())} proxy bits/16, {nt_d} ACs truncated of {nz_d}")
+
+
+@pytest.mark.parametrize("name", ["rgb256", "rgb512_two_level", "material512", "dct512", "material2048"])
 def test_full_size_properties(orc, name):
     say("full size", name)
     w, lay, tr, z, p, tgt = full_trainer(name)
+    if w.dct_q:
+        live_dct(orc, w, lay, tr, z, p, tgt)
+    zdec = tr.download_zq()                             # what every decode reads (the snapped plane with --dct-q)
     N, M = w.mlp_pairs, w.mlp_batch
     tr.mlp_step(1, w.mlp_sigma, 0.0, N, M)              # lr 0: Adam leaves every weight bit-identical
     assert np.array_equal(tr.download_model()[1], p)
     dl = tr.debug_last_dl()
     lp, lm = tr.debug_last_losses()
     idx = tr.debug_last_batch()
+    assert np.array_equal(idx, orc.draw_batch(w.seed, 1, M, lay.W * lay.H))
     assert dl.size == N and np.isfinite(lp).all() and np.isfinite(lm).all()
     assert np.array_equal(dl, lp - lm) or np.abs(dl - (lp - lm)).max() <= 1e-15 * np.abs(lp).max()
-    if M <= 65536:
-        s = np.float64(np.float32(w.mlp_sigma))
-        for i in (0, N // 2, N - 1):                    # sampled pairs on the device's own minibatch
-            eps = orc.gauss_fill(w.seed, 2, 1, i, 0, p.size).astype(np.float64)
-            # w +- sigma eps as one rounding (sigma * eps is exact in double)
-            wp = (p.astype(np.float64) + s * eps).astype(np.float32)
-            wm = (p.astype(np.float64) - s * eps).astype(np.float32)
-            assert rel(lp[i], orc.loss_subset(lay, wp, z, tgt, idx)) < 1e-5
-            assert rel(lm[i], orc.loss_subset(lay, wm, z, tgt, idx)) < 1e-5
+    s = np.float64(np.float32(w.mlp_sigma))
+    worst = 0.0
+    for i in ((0, N // 2, N - 1) if M <= 65536 else (0, N - 1)):   # sampled pairs on the device's own minibatch
+        eps = orc.gauss_fill(w.seed, 2, 1, i, 0, p.size).astype(np.float64)
+        # w +- sigma eps as one rounding (sigma * eps is exact in double)
+        wp = (p.astype(np.float64) + s * eps).astype(np.float32)
+        wm = (p.astype(np.float64) - s * eps).astype(np.float32)
+        worst = max(worst, rel(lp[i], orc.loss_subset(lay, wp, zdec, tgt, idx)), rel(lm[i], orc.loss_subset(lay, wm, zdec, tgt, idx)))
+    say(f"{name}: sampled member losses within {worst:.2e} relative of the oracle")
+    assert worst < 1e-5
     # the unperturbed pair of a central-difference step is the loss of w on the step's minibatch
     tr.mlp_step_fd(2, np.float32(w.fd_h), 0.0, M)
     l0, _ = tr.mlp_stats()
-    if M <= 65536:
-        assert rel(l0, orc.loss_subset(lay, p, z, tgt, tr.debug_last_batch())) < 1e-6
+    assert rel(l0, orc.loss_subset(lay, p, zdec, tgt, tr.debug_last_batch())) < 1e-6
     assert np.isfinite(tr.debug_last_dl()).all()
     tr.mlp_step(3, w.mlp_sigma, w.mlp_lr, N, M)
     assert np.isfinite(tr.download_model()[1]).all()
@@ -128,3 +179,90 @@ def test_full_size_properties(orc, name):
         assert g[:n0].any()
     img = tr.decode_full()
     assert np.isfinite(img).all() and img.min() >= 0 and img.max() <= 1
+
+
+def mse_psnr(orc, img, tgt, lay):
+    """the reference's printed figure: mse_of (both images rounded to 8 bits, main.cpp:1764-1788), 10 log10(255^2 / mse)"""
+    tex, weighted = np.zeros(4), np.zeros(1)
+    cw = [float(x) for x in (lay.weights or [1.0] * lay.T)]
+    wv = np.array(cw, np.float32)
+    orc._mse_of(img.ctypes.data, tgt.ctypes.data, lay.W, lay.H, lay.nout, wv.ctypes.data, float(np.float32(wv.sum())), 0, 0,
+                tex.ctypes.data, weighted.ctypes.data)
+    return float(weighted[0]) * 65025.0, 10 * np.log10(255.0 ** 2 / (float(weighted[0]) * 65025.0))
+
+
+@pytest.mark.skipif(not have_reference(fast=True), reason="the reference's CPU loop is built only where the reference tree is")
+def test_rgb256_fixed_seed_psnr(orc):
+    """rgb256 (the CPU-reference plumbing run) trained for its full 200 iterations at its fixed seed on the
+    device and by the reference's own CPU training loop (main.cpp compiled with its -O3 -ffast-math flags,
+    MlpTrainer / LatentTrainer in main.cpp:4121-4148's order, --rng hash), from the same initial model: the
+    final PSNRs must agree within 0.05 dB (the reference's own cross-backend check, README.md:964-970)."""
+    w, lay, tr, z, p, tgt = full_trainer("rgb256")
+    ref = reference(fast=True)
+    cfg = OrTrainCfg()
+    cfg.seed, cfg.mlp_pairs, cfg.mlp_batch, cfg.mlp_sigma, cfg.mlp_lr = w.seed, w.mlp_pairs, w.mlp_batch, w.mlp_sigma, w.mlp_lr
+    cfg.lat_pairs, cfg.lat_sigma, cfg.lat_lr, cfg.fd_from, cfg.fd_h = w.lat_pairs, w.lat_sigma, w.lat_lr, w.iters + 1, w.fd_h
+    mc = model_of(lay)
+    h = ref.lib.ref_train_create(C.byref(mc), C.byref(cfg), z.ctypes.data, p.ctypes.data, tgt.ctypes.data)
+    t0 = time.time()
+    try:
+        for it in range(1, w.iters + 1):
+            ref.lib.ref_train_iter(h, it, w.iters)
+            if it % 50 == 0:
+                say(f"rgb256 reference CPU loop: iteration {it} ({time.time() - t0:.1f} s)")
+        zr, pr = np.empty_like(z), np.empty_like(p)
+        ref.lib.ref_train_get(h, zr.ctypes.data, pr.ctypes.data)
+    finally:
+        ref.lib.ref_train_destroy(h)
+    t1 = time.time()
+    for it in range(1, w.iters + 1):
+        tr.mlp_step(it, w.mlp_sigma, w.mlp_lr, w.mlp_pairs, w.mlp_batch)
+        tr.lat_step(it, w.lat_sigma, w.lat_lr, w.lat_pairs)
+    img = tr.decode_full()
+    t2 = time.time()
+    mse_0, ps_0 = mse_psnr(orc, orc.decode_full(lay, p, z), tgt, lay)
+    mse_c, ps_c = mse_psnr(orc, orc.decode_full(lay, pr, zr), tgt, lay)
+    mse_g, ps_g = mse_psnr(orc, img, tgt, lay)
+    say(f"rgb256 {w.iters} iterations, seed {w.seed}: start psnr {ps_0:.3f} dB; reference CPU loop mse {mse_c:.3f} psnr "
+        f"{ps_c:.3f} dB ({t1 - t0:.1f} s); device mse {mse_g:.3f} psnr {ps_g:.3f} dB ({t2 - t1:.2f} s); "
+        f"delta {ps_g - ps_c:+.4f} dB")
+    assert ps_c > ps_0 + 1.0                            # training moved
+    assert abs(ps_g - ps_c) <= 0.05
+
+
+def test_material512_selectors_full_size(orc):
+    """One selector search (--qat 2,2, qat_search main.cpp:2088-2139) at material512's full size (262144 texels x
+    2 channels, 12 outputs), after a few training iterations on the device, against the oracle's search of the
+    same model. Every texel channel whose choice differs is counted and printed; at each one the reference's
+    cell losses (loss_subset of the one pixel, the double sum of float terms) of the two choices must agree to
+    a rounding tie (the reference's own check accepts ties, main.cpp:3143-3144)."""
+    w, lay, tr, z, p, tgt = full_trainer("material512")
+    for it in range(1, 6):
+        tr.mlp_step(it, w.mlp_sigma, w.mlp_lr, w.mlp_pairs, w.mlp_batch)
+        tr.lat_step(it, w.lat_sigma, w.lat_lr, w.lat_pairs)
+        tr.qat_search()
+    zd, pd = tr.download_model()
+    tr.qat_search()
+    z_dev = tr.download_model()[0]
+    z_or = zd.copy()
+    grid = synth.qat_grid()
+    orc.qat_search(lay, pd, z_or, tgt, w.qat_bits, grid)
+    W0, H0, C0, _ = lay.levels[0]
+    n0 = W0 * H0 * C0
+    a, b, before = z_dev[:n0].reshape(-1, C0), z_or[:n0].reshape(-1, C0), zd[:n0].reshape(-1, C0)
+    diff = np.nonzero((a != b).any(axis=1))[0]
+    changed = int((b != before).any(axis=1).sum())
+    worst = 0.0
+    for t in diff:
+        c = int(np.nonzero(a[t] != b[t])[0][0])            # the first channel whose choice differs
+        losses = []
+        for v in (a[t, c], b[t, c]):
+            zz = zd.copy()
+            zz[t * C0:(t + 1) * C0] = np.concatenate([b[t, :c], [v], before[t, c + 1:]])
+            losses.append(orc.loss_subset(lay, pd, zz, tgt, np.array([t], np.int32)))
+        gap = abs(losses[0] - losses[1]) / max(abs(losses[1]), 1e-30)
+        worst = max(worst, gap)
+    say(f"material512 selector search: {diff.size} of {W0 * H0} texels ({2 * W0 * H0} channel choices) differ from the "
+        f"oracle's; the oracle changed {changed} texels; largest relative cell-loss gap at a difference {worst:.2e}")
+    assert diff.size <= max(2, W0 * H0 // 1000)
+    assert worst < 1e-5

@@ -4,8 +4,9 @@ mathematics fixes (splitmix64's published outputs, Box-Muller moments, closed fo
 import ctypes as C
 
 import numpy as np
+import pytest
 
-from oracle.oracle import Model, model_of
+from oracle.oracle import Model, have_reference, model_of, reference
 
 JPEG_ZIGZAG = [0, 1, 8, 16, 9, 2, 3, 10, 17, 24, 32, 25, 18, 11, 4, 5, 12, 19, 26, 33, 40, 48, 41, 34, 27, 20, 13, 6, 7,
                14, 21, 28, 35, 42, 49, 56, 57, 50, 43, 36, 29, 22, 15, 23, 30, 37, 44, 51, 58, 59, 52, 45, 38, 31, 39, 46,
@@ -269,3 +270,28 @@ def test_es_gradient_follows_the_loss(orc):
     gfd = orc.fd_grad(dlf, hh)
     cos = float(ges @ gfd / (np.linalg.norm(ges) * np.linalg.norm(gfd)))
     assert cos > 0.85
+
+
+@pytest.mark.parametrize("leak", [0.0, 0.01])
+def test_nan_hidden_unit_propagates(orc, leak):
+    """A diverged model (one NaN hidden-layer weight) gives a NaN loss, a NaN per-pixel error and a NaN
+    ES update in the reference: its activation x > 0 ? x : leak x maps a NaN pre-activation to
+    leak NaN = NaN (main.cpp:560), which then reaches every unit of the next layer. The oracle does the
+    same; the device kernels are held to this behaviour (a maximum-based activation would drop the NaN
+    and report a finite loss)."""
+    m = Model(12, 10, [(4, 3, 4, 0)], [8, 8], T=1, pos=[0], leak=leak)
+    rng = np.random.default_rng(2)
+    z = rng.normal(0, 0.3, m.nz).astype(np.float32)
+    p = rng.normal(0, 0.5, m.nparams).astype(np.float32)
+    tgt = rng.random(12 * 10 * 3).astype(np.float32)
+    idx = np.arange(120, dtype=np.int32)
+    p[m.nin * 8 + 8 + 3] = np.nan            # a weight of the second hidden layer (unit 0, input 3)
+    assert np.isnan(orc.loss_subset(m, p, z, tgt, idx))
+    assert np.isnan(orc.decode_err(m, p, z, tgt)).all()
+    dl, _, lp, lm = orc.mlp_es_eval(m, p, z, tgt, 1, 1, 0.01, 4, idx)
+    assert np.isnan(lp).all() and np.isnan(lm).all()
+    assert np.isnan(orc.mlp_es_grad(p.size, 4, 1, 1, 0.01, dl)).all()
+    if have_reference():
+        ref = reference()
+        assert np.isnan(ref.loss_subset(m, p, z, tgt, idx))
+        assert np.isnan(ref.decode_err(m, p, z, tgt)).all()
