@@ -188,7 +188,8 @@ def mse_psnr(orc, img, tgt, lay):
     wv = np.array(cw, np.float32)
     orc._mse_of(img.ctypes.data, tgt.ctypes.data, lay.W, lay.H, lay.nout, wv.ctypes.data, float(np.float32(wv.sum())), 0, 0,
                 tex.ctypes.data, weighted.ctypes.data)
-    return float(weighted[0]) * 65025.0, 10 * np.log10(255.0 ** 2 / (float(weighted[0]) * 65025.0))
+    mse = float(weighted[0])                        # in 8-bit units
+    return mse, 10 * np.log10(255.0 ** 2 / mse)
 
 
 @pytest.mark.skipif(not have_reference(fast=True), reason="the reference's CPU loop is built only where the reference tree is")

@@ -295,3 +295,18 @@ def test_nan_hidden_unit_propagates(orc, leak):
         ref = reference()
         assert np.isnan(ref.loss_subset(m, p, z, tgt, idx))
         assert np.isnan(ref.decode_err(m, p, z, tgt)).all()
+
+
+def test_nan_output_with_clamp_is_zero(orc):
+    """With --clamp the reference's output min(1, max(0, s + 0.5)) maps a NaN pre-activation to 0
+    (std::max(0, NaN) returns its first argument, main.cpp:624): the loss stays finite."""
+    m = Model(12, 10, [(4, 3, 4, 0)], [8, 8], T=1, pos=[0], leak=0.02, clamp_out=True)
+    rng = np.random.default_rng(3)
+    z = rng.normal(0, 0.3, m.nz).astype(np.float32)
+    p = rng.normal(0, 0.5, m.nparams).astype(np.float32)
+    tgt = rng.random(12 * 10 * 3).astype(np.float32)
+    p[m.nin * 8 + 8 + 3] = np.nan
+    assert not orc.decode_full(m, p, z).any()
+    assert np.isfinite(orc.loss_subset(m, p, z, tgt, np.arange(120, dtype=np.int32)))
+    if have_reference():
+        assert not reference().decode_full(m, p, z).any()
