@@ -109,6 +109,14 @@ void ntc_trainer_dct_refit(ntc_trainer* t, uint8_t* code);
  * No counterpart in the reference's backend (its print path downloads the model and decodes on the
  * host, main.cpp:4155-4174). */
 void ntc_trainer_decode_error(ntc_trainer* t, const float* z_host, int ew, int eh, double* tex_mse, double* weighted);
+/* ntc_trainer_decode_error with no allocation at call time (no hipMalloc / hipFree, no allocating library
+ * call): the same figures from the same kernels, with the per-block partial sums kept in a static per-GPU
+ * scratch array of 512 KiB and added on the device. No counterpart in the reference: it is for callers that
+ * cannot allocate (code under HIP graph capture, a serving or progress-print loop that must not synchronize
+ * the device through hipMalloc / hipFree). The extent ew x eh may hold at most 2^24 pixels (4096 x 4096);
+ * a larger one prints an error and exits, as every other misuse. Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (from several host threads or trainers) race. */
+void ntc_trainer_decode_error_noalloc(ntc_trainer* t, const float* z_host, int ew, int eh, double* tex_mse, double* weighted);
 /* The decode of the current model rounded to 8 bits as the reference's save_png and ntc_decode write it
  * (lround of the [0, 1]-clamped value times 255): W*H*nout bytes, interleaved per pixel. No counterpart in
  * the reference's backend (its decoder is the host program ntc_decode.cpp). */

@@ -88,6 +88,9 @@ void ntc_trainer_decode_rgb8(ntc_trainer* t, uint8_t* out) { t->t.decode_rgb8(ou
 void ntc_trainer_decode_error(ntc_trainer* t, const float* z_host, int ew, int eh, double* tex_mse, double* weighted) {
     t->t.decode_error(z_host, ew, eh, tex_mse, weighted);
 }
+void ntc_trainer_decode_error_noalloc(ntc_trainer* t, const float* z_host, int ew, int eh, double* tex_mse, double* weighted) {
+    ntc_hip::decode_error_noalloc_impl(*t->t.im, z_host, ew, eh, tex_mse, weighted);
+}
 
 void ntc_trainer_mlp_step(ntc_trainer* t, int it, float sigma, float lr, int N, int M) { t->t.mlp_step(it, sigma, lr, N, M); }
 void ntc_trainer_mlp_step_fd(ntc_trainer* t, int it, float h, float lr, int M) { t->t.mlp_step_fd(it, h, lr, M); }

@@ -263,6 +263,7 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
     I.dev_name = prop.name; I.arch = prop.gcnArchName; I.cus = prop.multiProcessorCount;
     NTC_CHECK(hipRuntimeGetVersion(&I.rt_ver));
     if (!noise_fix_for_device(I.device, I.noise, why)) return false;
+    if (!noalloc_scratch_setup(I.device, why)) return false;
     NTC_CHECK(hipStreamCreateWithFlags(&I.stream, hipStreamNonBlocking));
 
     // ---- model description

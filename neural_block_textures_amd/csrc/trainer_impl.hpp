@@ -193,6 +193,10 @@ void launch_pack_u8(Impl& I, uint8_t* out);
 void decode_rgb8_impl(Impl& I, uint8_t* out);
 // decode the decode buffer on the device and return mse_of's per-texture and weighted figures
 void decode_error_impl(Impl& I, const float* z_host, int ew, int eh, double* tex_mse, double* weighted);
+// noalloc.hip: decode_error with its partial sums in a static per-GPU scratch array (no allocation at call
+// time); the array's device address is looked up once per GPU at init
+bool noalloc_scratch_setup(int device, std::string& why);
+void decode_error_noalloc_impl(Impl& I, const float* z_host, int ew, int eh, double* tex_mse, double* weighted);
 void dct_probe_impl(Impl& I, uint8_t* code, float* gain);
 void dct_refit_impl(Impl& I, uint8_t* code);
 void launch_dct_rate_pairs(Impl& I, int K, float sigma);

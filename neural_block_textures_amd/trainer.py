@@ -109,6 +109,7 @@ def library() -> C.CDLL:
             "ntc_trainer_dct_probe": (None, [P, P, P]),
             "ntc_trainer_dct_refit": (None, [P, P]),
             "ntc_trainer_decode_error": (None, [P, P, C.c_int, C.c_int, P, P]),
+            "ntc_trainer_decode_error_noalloc": (None, [P, P, C.c_int, C.c_int, P, P]),
             "ntc_trainer_decode_rgb8": (None, [P, P]),
             "ntc_trainer_debug_gauss": (None, [P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, C.c_size_t, P]),
             "ntc_trainer_debug_noise_factors": (None, [P, C.c_uint32, C.c_size_t, P, P]),
@@ -336,6 +337,16 @@ class Trainer:
         wt = C.c_double()
         zh = None if z is None else _f32(z, self.nz)
         self._lib.ntc_trainer_decode_error(self._h, _ptr(zh), ew, eh, tex.ctypes.data, C.addressof(wt))
+        return tex[:T], wt.value
+
+    def decode_error_noalloc(self, ew=0, eh=0, z=None):
+        """decode_error with no device allocation at call time (its partial sums in the library's static
+        per-GPU scratch; at most 2^24 pixels in the extent)"""
+        T = max(1, self.layout.nout // 3) if self.layout else 4
+        tex = np.zeros(4, np.float64)
+        wt = C.c_double()
+        zh = None if z is None else _f32(z, self.nz)
+        self._lib.ntc_trainer_decode_error_noalloc(self._h, _ptr(zh), ew, eh, tex.ctypes.data, C.addressof(wt))
         return tex[:T], wt.value
 
     # ---- steps
