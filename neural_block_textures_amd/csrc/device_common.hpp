@@ -20,6 +20,12 @@ using __hip_internal::uint8_t; using __hip_internal::uint16_t; using __hip_inter
 namespace ntc_hip {
 
 constexpr int kMaxLevels = 3, kMaxPos = 16, kMaxOut = 12, kMaxHidden = 8, kMaxWidth = 64;
+// The minibatch arrays of a trainer (structure of arrays, Mcap slots per row): the feature array has
+// minibatch_rows(nin) rows, those past nin zero (the matrix kernels read whole 4-input k-steps), and both
+// arrays carry kMinibatchSlack floats past their last row (more than the 7 tile strides of 32 slots a
+// population pass can read past the end of its chunk).
+constexpr int kMinibatchSlack = 256;
+__host__ __device__ constexpr int minibatch_rows(int nin) { return 4 * ((nin + 3) / 4); }
 
 // ---------------------------------------------------------------- model description
 struct DevLevel {

@@ -110,6 +110,10 @@ struct MfmaWeights {
     f4v co;
     float wo[valu_out<S>() ? 4 : 1][Q::kKsH];   // the output layer on the VALU: output c's weight of the input this
     float bo[valu_out<S>() ? 4 : 1];            // lane group feeds at k-step ks; output c's bias in lane group 0
+    // the pixel-per-lane output layer (mfma_out_own): the A operand of 4x4x1 step (ks, r) - in lane l, the
+    // weight of output l % 4 for the input lane group r feeds at k-step ks - and the biases of outputs 0 .. 3
+    float wo4[valu_out<S>() ? Q::kKsH : 1][4];
+    f4v c4;
 };
 
 // Gathers a member's flat parameter vector (per layer W[out][in] row-major, then b[out]) into
@@ -166,7 +170,16 @@ __device__ __forceinline__ void mfma_load_from(MfmaWeights<S>& W, const Get& w, 
                 W.wo[c][ks] = (c < NO && in < H) ? w(p + c * H + in) : 0.0f;
             }
             W.bo[c] = (c < NO && g == 0) ? w(p + NO * H + c) : 0.0f;
+            W.c4[c] = c < NO ? w(p + NO * H + c) : 0.0f;
         }
+        const int oc = lane & 3;
+#pragma unroll
+        for (int ks = 0; ks < Q::kKsH; ks++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int in = hidden_input<Q, Exact>(ks, r);
+                W.wo4[ks][r] = (oc < NO && in < H) ? w(p + oc * H + in) : 0.0f;
+            }
     } else {
 #pragma unroll
         for (int ks = 0; ks < Q::kKsH; ks++) {
@@ -203,7 +216,12 @@ __device__ __forceinline__ void scale_output(MfmaWeights<S>& W, float sc) {
 #pragma unroll
             for (int ks = 0; ks < MfmaShape<S>::kKsH; ks++) W.wo[c][ks] *= sc;
             W.bo[c] *= sc;
+            W.c4[c] *= sc;
         }
+#pragma unroll
+        for (int ks = 0; ks < MfmaShape<S>::kKsH; ks++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) W.wo4[ks][r] *= sc;
     } else {
 #pragma unroll
         for (int ks = 0; ks < MfmaShape<S>::kKsH; ks++) W.ao[ks] *= sc;
@@ -213,6 +231,10 @@ __device__ __forceinline__ void scale_output(MfmaWeights<S>& W, float sc) {
 }
 
 __device__ __forceinline__ f4v mfma4(float a, float b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+
+// v_mfma_f32_4x4x1_16b_f32: 16 independent 4 x 4 x 1 products, block b = lanes 4b .. 4b + 3:
+// D[lane 4b + j][register i] = C[lane 4b + j][register i] + A[lane 4b + i] B[lane 4b + j] (measured on gfx950)
+__device__ __forceinline__ f4v mfma4x4(float a, float b, f4v c) { return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0); }
 
 // element (lane group g, register r) -> (lane group r, register g)
 __device__ __forceinline__ void transpose4(const f4v& v, float* y) {
@@ -366,6 +388,37 @@ __device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const floa
     for (int ks = 0; ks < Q::kKsH; ks++)
 #pragma unroll
         for (int u = 0; u < U; u++) o[u] = mfma4(W.ao[ks], x[u][ks], o[u]);
+}
+
+// The output layer of four tiles for at most 4 outputs with the pixels in the lanes: x = the last hidden
+// layer of tiles 0 .. 3 as mfma_hidden leaves it (lane (g, j), register ks of tile u = input
+// hidden_input(ks, g) of pixel j). One 4 x 4 transpose across (lane group, tile) per k-step gives lane
+// (g, j) every input of pixel j of tile g (register r: input hidden_input(ks, r)); then each input is one
+// 4x4x1 step whose A operand holds output l % 4's weight of it, so the block of lanes 4b .. 4b + 3 adds
+// w[i][in] x[in] of its four pixels into output i: lane (g, j) ends with the pre-activations of outputs
+// 0 .. 3 of its own pixel (bias first, then the inputs in k-step order; outputs past nout are zero).
+// 16 4x4x1 steps (8 cycles each) and 16 lane swaps per 16-unit tile set, where the VALU layer spends
+// 4 x (3 x 4 fused multiply-adds + its reduce-scatter) and one sigmoid per lane and tile.
+template <class S>
+__device__ __forceinline__ f4v mfma_out_own(const MfmaWeights<S>& W, const float (&x)[4][MfmaShape<S>::kKsH]) {
+    static_assert(valu_out<S>(), "at most 4 outputs");
+    // two independent chains (inputs of registers 0, 1 and 2, 3), added at the end
+    f4v o = W.c4, o2 = { 0.0f, 0.0f, 0.0f, 0.0f };
+#pragma unroll
+    for (int ks = 0; ks < MfmaShape<S>::kKsH; ks++) {
+        f4v v;
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = x[u][ks];
+        float y[4];
+        transpose4(v, y);
+        o = mfma4x4(W.wo4[ks][0], y[0], o);
+        o2 = mfma4x4(W.wo4[ks][2], y[2], o2);
+        o = mfma4x4(W.wo4[ks][1], y[1], o);
+        o2 = mfma4x4(W.wo4[ks][3], y[3], o2);
+    }
+#pragma unroll
+    for (int r = 0; r < MfmaShape<S>::kNout; r++) o[r] += o2[r];
+    return o;
 }
 
 // The output layer on the VALU for at most 4 outputs: lane (g, j) forms the partial sums of every

@@ -336,8 +336,12 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
     dev_alloc(&I.w, I.P); dev_alloc(&I.wgrad, I.P); dev_alloc(&I.wm, I.P); dev_alloc(&I.wv, I.P);
     dev_alloc(&I.tgt, I.npix * d.nout); dev_alloc(&I.img, I.npix * d.nout);
     I.Mcap = d.max_batch;
-    // 64 floats of slack: the matrix-core population evaluation reads whole 16-slot tiles
-    dev_alloc(&I.feat, (size_t)I.Mcap * d.nin + 64); dev_alloc(&I.btgt, (size_t)I.Mcap * d.nout + 64); dev_alloc(&I.bidx, (size_t)I.Mcap);
+    // the matrix-core population evaluation reads whole 16-slot tiles and 4-input k-steps: zero feature rows
+    // up to minibatch_rows(nin) and kMinibatchSlack floats past the last row of each array
+    const size_t nfeat = (size_t)I.Mcap * minibatch_rows(d.nin) + kMinibatchSlack;
+    dev_alloc(&I.feat, nfeat); dev_alloc(&I.btgt, (size_t)I.Mcap * d.nout + kMinibatchSlack); dev_alloc(&I.bidx, (size_t)I.Mcap);
+    NTC_CHECK(hipMemset(I.feat, 0, nfeat * sizeof(float)));
+    NTC_CHECK(hipMemset(I.btgt, 0, ((size_t)I.Mcap * d.nout + kMinibatchSlack) * sizeof(float)));
     I.pairs_cap = d.max_pairs;
     dev_alloc(&I.eps_mlp, (size_t)I.pairs_cap * I.P);
     I.gpart_cap = (size_t)((I.pairs_cap + 127) / 128) * I.P;
