@@ -186,7 +186,20 @@ def cpu_baseline(w, z, p, tgt, seconds: float, pairs=None, dct_codes=None):
         sample = (f"{its} ES iteration(s) of {w.name} with {pairs} of its {w.mlp_pairs} pairs (population evaluation scaled "
                   f"down, everything else at full size), {el:.1f} s")
     return {"value": ev * its / el, "unit": "member·pixel evals/s", "cores": threads, "kind": kind, "sample": sample,
-            "es_iters_per_s": its / el, "cpu": platform.processor() or platform.machine()}
+            "es_iters_per_s": its / el, "cpu": cpu_model(), "nproc": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None}
+
+
+def cpu_model() -> str:
+    """the host CPU's model name (/proc/cpuinfo), else the architecture"""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def cpu_refit_ms(w, r):
