@@ -190,6 +190,29 @@ def cpu_baseline(w, z, p, tgt, seconds: float, pairs=None, dct_codes=None):
             "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None}
 
 
+def gauss_draw(w, reps: int):
+    """The device draw of all N x P Gaussians of one ES step of the workload (Trainer.debug_gauss, the population
+    kernel's per-element draw), reps times, timed with HIP events on the trainer's stream."""
+    import numpy as np
+
+    from neural_block_textures_amd import synth
+    from neural_block_textures_amd.trainer import Trainer
+    lay = w.layout
+    z, p = synth.init_model(lay, w.seed, qat_bits=w.qat_bits)
+    tr = Trainer()
+    kw = dict(qat_bits=w.qat_bits, qat_grid=synth.qat_grid()) if w.qat_bits else {}
+    tr.init(Trainer.model_desc(lay, max_pairs=8, max_batch=256, seed=w.seed, **kw), z, p,
+            np.zeros(lay.W * lay.H * lay.nout, np.float32), lay)
+    n = w.mlp_pairs * lay.nparams
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g = tr.debug_gauss(2, 1, 0, 0, n)   # includes the download of the n values
+    el = time.perf_counter() - t0
+    print(json.dumps({"gauss_draw": {"workload": w.name, "gaussians": n, "reps": reps, "host_ms_per_draw_with_download": 1e3 * el / reps,
+                                     "mean": float(g.mean()), "std": float(g.std())}}), flush=True)
+    tr.close()
+
+
 def cpu_model() -> str:
     """the host CPU's model name (/proc/cpuinfo), else the architecture"""
     try:
@@ -401,6 +424,8 @@ def main():
     ap.add_argument("--all-configs", metavar="OUT_MD", help="run the five workloads and write a table")
     ap.add_argument("--valu", action="store_true",
                     help="every stage on the VALU kernels (the same work; measures the matrix-core choice against the alternative)")
+    ap.add_argument("--gauss-draw", type=int, default=0, metavar="REPS",
+                    help="time REPS device draws of one ES step's N x P Gaussians of the workload (what a regenerating update redraws)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="FLOATS",
                     help="only run a plain device copy of FLOATS floats three times (the reference for memory counters)")
     args = ap.parse_args()
@@ -429,6 +454,9 @@ def main():
         return
     if args.all_configs:
         all_configs(args.all_configs, args.cpu_seconds)
+        return
+    if args.gauss_draw:
+        gauss_draw(workloads()[args.workload], args.gauss_draw)
         return
 
     w = workloads()[args.workload]
