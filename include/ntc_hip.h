@@ -117,6 +117,27 @@ void ntc_trainer_decode_error(ntc_trainer* t, const float* z_host, int ew, int e
  * a larger one prints an error and exits, as every other misuse. Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (from several host threads or trainers) race. */
 void ntc_trainer_decode_error_noalloc(ntc_trainer* t, const float* z_host, int ew, int eh, double* tex_mse, double* weighted);
+/* The figures of the reference's progress line (main.cpp:4155-4212) computed on the device, without downloading
+ * the model (the reference's --cuda print path downloads the latent and the weights at every print):
+ *   bitrate_stats (main.cpp:2273-2352) as a progress print runs it, the order-0 figure standing in for the
+ *   (up, left) context estimate (main.cpp:4171), at --qbits qbits; q_*: mse_of (main.cpp:1764-1788, extent ew x eh,
+ *   0 = the whole image) of the decode of the quantized latent it returns; lat_*: latent_stats (main.cpp:2211-2216)
+ *   of each level of the shadow; dct_*: with a live --dct-q level 0, dct_analyze (main.cpp:1080-1208) with the code
+ *   grid's context estimate, as the line's token group calls it (main.cpp:4180-4190). No counterpart in the
+ *   reference's backend. The bitrate figures equal the host computation bit for bit, except that a live DCT
+ *   plane's token bits (and dct_analyze's per-class sums) add the same terms per histogram bin instead of per
+ *   token (within 1e-13 relative). */
+typedef struct ntc_print_stats {
+    double bpp_fp32, bpp_q8, bpp_q8_ent, bpp_q8_ctx, bpp_ctx_level0, bpp_est, bits_mlp, bits_raw_latent, bits_header;
+    double q_tex_mse[4], q_weighted_mse;
+    float lat_mean[NTC_MAX_LEVELS], lat_sd[NTC_MAX_LEVELS], lat_max[NTC_MAX_LEVELS];
+    int dct_live;
+    double dct_raw[7], dct_h0[7], dct_ctx[7];   /* dc, run, magnitude, sign, end of block, scale code, header */
+    double dct_raw_total, dct_h0_total, dct_ctx_total;
+    long long dct_nblk, dct_ntok_nz, dct_ntok_eob, dct_nmag_over;
+    double dct_nz_mean, dct_lnz_mean, dct_eob_only_frac;
+} ntc_print_stats;
+void ntc_trainer_print_stats(ntc_trainer* t, int qbits, int ew, int eh, ntc_print_stats* out);
 /* The decode of the current model rounded to 8 bits as the reference's save_png and ntc_decode write it
  * (lround of the [0, 1]-clamped value times 255): W*H*nout bytes, interleaved per pixel. No counterpart in
  * the reference's backend (its decoder is the host program ntc_decode.cpp). */
@@ -177,6 +198,14 @@ int ntc_jit_compile_check(const ntc_model_desc* d, const char* arch, double* sec
 /* the device's Gaussian draws for indices index0 .. index0 + n - 1 of one (seed, stream, step, pair) */
 void ntc_trainer_debug_gauss(ntc_trainer* t, uint32_t stream, uint32_t step, uint32_t pair, uint64_t index0, size_t n,
                              float* out);
+/* The integer histograms behind the last ntc_trainer_print_stats: bitrate (returned count) = for each level l (a live
+ * --dct-q level 0 skipped) and channel c, 2^bits(l, c) quantization-index bins, then for l >= 1 as many bins of the
+ * DPCM residual of bpp_est; lohi[l * 64 + c][2] = the least and greatest value of the channel (its post-hoc scale);
+ * dct (*n_dct values) = per channel run[65] mag[257] ctx_run[64 x 65] ctx_mag[64 x 257] ctxr[64] ctxm[64] dcres[4097]
+ * code[16] code_tri[16 x 16 x 16] code_pair[16 x 16] nrun neob nsign, then sum_nz sum_lnz n_lnz eob_only nmag_over.
+ * Copies at most the capacities given (lohi: 3 x 64 x 2 floats). */
+size_t ntc_trainer_debug_print_counts(const ntc_trainer* t, long long* bitrate, size_t cap_b, float* lohi, long long* dct,
+                                      size_t cap_d, size_t* n_dct);
 /* runs a plain device copy of n floats (n a multiple of 4) reps times on the trainer's stream:
  * the known-size reference that converts a profile's memory counters into bytes */
 void ntc_trainer_debug_copy_calibration(ntc_trainer* t, size_t n, int reps);

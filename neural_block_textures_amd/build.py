@@ -20,8 +20,8 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libntc_hip.so")
-SOURCES = ["kernels_pop.hip", "kernels_mlp.hip", "kernels_latent.hip", "kernels_quant.hip", "noalloc.hip", "trainer.cpp", "noise_fix.cpp",
-           "capi.cpp", "jit.cpp"]
+SOURCES = ["kernels_pop.hip", "kernels_mlp.hip", "kernels_latent.hip", "kernels_quant.hip", "kernels_stats.hip", "noalloc.hip", "trainer.cpp",
+           "noise_fix.cpp", "capi.cpp", "jit.cpp"]
 ARCH = "gfx950"
 # The matrix-core population evaluation takes maxima of values that are never NaN for a finite
 # model (the reference's own build assumes no NaNs either, -ffast-math): with the IEEE mode bit

@@ -88,6 +88,18 @@ void ntc_trainer_decode_rgb8(ntc_trainer* t, uint8_t* out) { t->t.decode_rgb8(ou
 void ntc_trainer_decode_error(ntc_trainer* t, const float* z_host, int ew, int eh, double* tex_mse, double* weighted) {
     t->t.decode_error(z_host, ew, eh, tex_mse, weighted);
 }
+void ntc_trainer_print_stats(ntc_trainer* t, int qbits, int ew, int eh, ntc_print_stats* out) {
+    ntc_hip::print_stats_impl(*t->t.im, qbits, ew, eh, out);
+}
+size_t ntc_trainer_debug_print_counts(const ntc_trainer* t, long long* bitrate, size_t cap_b, float* lohi, long long* dct,
+                                      size_t cap_d, size_t* n_dct) {
+    const auto& I = *t->t.im;
+    if (bitrate) memcpy(bitrate, I.st_counts.data(), std::min(cap_b, I.st_counts.size()) * sizeof(long long));
+    if (lohi) memcpy(lohi, I.st_lohi.data(), std::min<size_t>(3 * 64 * 2, I.st_lohi.size()) * sizeof(float));
+    if (dct) memcpy(dct, I.st_dct_counts.data(), std::min(cap_d, I.st_dct_counts.size()) * sizeof(long long));
+    if (n_dct) *n_dct = I.st_dct_counts.size();
+    return I.st_counts.size();
+}
 void ntc_trainer_decode_error_noalloc(ntc_trainer* t, const float* z_host, int ew, int eh, double* tex_mse, double* weighted) {
     ntc_hip::decode_error_noalloc_impl(*t->t.im, z_host, ew, eh, tex_mse, weighted);
 }
@@ -160,6 +172,7 @@ size_t ntc_abi_sizeof(const char* name) {
     if (n == "ntc_qes_desc") return sizeof(ntc_qes_desc);
     if (n == "ntc_dct_desc") return sizeof(ntc_dct_desc);
     if (n == "ntc_level_desc") return sizeof(ntc_level_desc);
+    if (n == "ntc_print_stats") return sizeof(ntc_print_stats);
     return 0;
 }
 long long ntc_trainer_nparams(const ntc_trainer* t) { return t->t.im->P; }

@@ -423,6 +423,22 @@ __device__ __forceinline__ float pixel_err_f(const DevModel& m, const float (&o)
     return e;
 }
 
+// qes_index (main.cpp:448-453): the --qes grid index, round half to even, clamped in float before the cast
+__device__ __forceinline__ int qes_index(float v, float lo, float range, int levels) {
+    const float r = rintf(((v - lo) / range) * (float)levels);   // round half to even
+    if (!(r == r)) return 0;
+    return r <= 0.0f ? 0 : (r >= (float)levels ? levels : (int)r);
+}
+// q8_index / q8_value (main.cpp:478-482): the post-hoc grid of a continuous level, strict float
+__device__ __forceinline__ int q8_index(float z, float lo, float range, int levels) {
+    const float x = __fmul_rn(__fdiv_rn(__fsub_rn(z, lo), range), (float)levels);
+    const float r = roundf(x);                                   // lround: half away from zero
+    return r <= 0.0f ? 0 : (r >= (float)levels ? levels : (int)r);
+}
+__device__ __forceinline__ float q8_value(int k, float lo, float range, int levels) {
+    return __fadd_rn(lo, __fmul_rn(__fdiv_rn((float)k, (float)levels), range));
+}
+
 // qat_index (main.cpp:2060-2064): lround of the grid coordinate, clamped
 __device__ __forceinline__ int qat_index(float v, int bits) {
     const int levels = (1 << bits) - 1;

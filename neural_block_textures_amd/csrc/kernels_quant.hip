@@ -15,12 +15,7 @@
 namespace ntc_hip {
 
 
-// ---------------------------------------------------------------- --qes
-__device__ __forceinline__ int qes_index(float v, float lo, float range, int levels) {
-    const float r = rintf(((v - lo) / range) * (float)levels);   // round half to even
-    if (!(r == r)) return 0;
-    return r <= 0.0f ? 0 : (r >= (float)levels ? levels : (int)r);
-}
+// ---------------------------------------------------------------- --qes (qes_index: device_common.hpp)
 
 // zq = snap(z) per level (a level without --qes bits is copied); once frozen the shadow is first
 // clamped to [lo, hi] (std::min(std::max(v, lo), hi) semantics) and written back.

@@ -185,6 +185,7 @@ Trainer::~Trainer() {
         dev_free(I.wsets); dev_free(I.eps_mlp); dev_free(I.gpart); dev_free(I.part); dev_free(I.dl); dev_free(I.lsum); dev_free(I.hh);
         dev_free(I.eps_lat); dev_free(I.dpix); dev_free(I.ranges); dev_free(I.qat_grid); dev_free(I.qat_bits);
         dev_free(I.qes_dev); dev_free(I.qgrid);
+        dev_free(I.zpost); dev_free(I.st_part); dev_free(I.st_keys); dev_free(I.st_hist); dev_free(I.st_dct); dev_free(I.st_sse);
         dev_free(I.dct_sym); dev_free(I.dct_code); dev_free(I.dct_step); dev_free(I.dct_bits); dev_free(I.dct_dbits); dev_free(I.dct_tn); dev_free(I.dct_probe_code); dev_free(I.dct_gain);
         (void)hipStreamDestroy(I.stream);
     }
@@ -312,6 +313,7 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
         QesDesc q0; memset(&q0, 0, sizeof(q0));
         for (int l = 0; l < d.nlev; l++) q0.bits[l] = d.qes_bits[l];
         NTC_CHECK(hipMemcpy(I.qes_dev, &q0, sizeof(q0), hipMemcpyHostToDevice));
+        I.qes_h = q0;
         if (I.qes) dev_alloc(&I.qgrid, (size_t)MAX_LEVELS * MAX_QES_CH * 4096);
         I.zdec = I.zq;
     } else {
@@ -402,6 +404,7 @@ void Trainer::set_qes(const QesDesc& q, const float* grid, size_t grid_n) {
     Impl& I = *im;
     if (!I.qes) die("set_qes without a --qes level in the model description");
     if (grid_n > (size_t)MAX_LEVELS * MAX_QES_CH * 4096) die("--qes grid table too large");
+    I.qes_h = q;
     NTC_CHECK(hipMemcpyAsync(I.qes_dev, &q, sizeof(q), hipMemcpyHostToDevice, I.stream));
     if (grid_n) NTC_CHECK(hipMemcpyAsync(I.qgrid, grid, grid_n * sizeof(float), hipMemcpyHostToDevice, I.stream));
     snap_latent_impl(I);

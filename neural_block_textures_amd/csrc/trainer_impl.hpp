@@ -22,6 +22,7 @@
 
 #include "device_common.hpp"
 #include "ntc_cuda.h"
+#include "ntc_hip.h"
 
 #define NTC_CHECK(x)                                                                                          \
     do {                                                                                                      \
@@ -86,6 +87,7 @@ struct ntc_cuda::Trainer::Impl {
 
     bool qes = false;
     ntc_cuda::QesDesc* qes_dev = nullptr;
+    ntc_cuda::QesDesc qes_h{};     // the host's copy of the last set_qes (which levels are live, at what depth)
     float* qgrid = nullptr;
 
     bool dct = false, dct_live = false, dct_rate_es = false, dct_rate_trunc = false;
@@ -99,6 +101,16 @@ struct ntc_cuda::Trainer::Impl {
     float* dct_gain = nullptr;           // and block gains (n)
     int dct_evals = 0, dct_last_K = 0;
     int lat_last_K = 0;            // pairs of the last latent ES step (the K x W*H rows of dpix it wrote)
+
+    // print_stats (kernels_stats.hip): the quantized latent, the histograms and partial sums (grown on first use),
+    // and the host's copy of the last histograms (ntc_trainer_debug_print_counts)
+    float* zpost = nullptr; size_t zpost_cap = 0;
+    double* st_part = nullptr; size_t st_part_cap = 0;
+    unsigned *st_keys = nullptr, *st_hist = nullptr, *st_dct = nullptr;
+    size_t st_keys_cap = 0, st_hist_cap = 0, st_dct_cap = 0;
+    unsigned long long* st_sse = nullptr; size_t st_sse_cap = 0;
+    std::vector<long long> st_counts, st_dct_counts;
+    std::vector<float> st_lohi;
 
     int mlp_t = 0, lat_t = 0, lat_step_no = 0;
     int last_N = 0, last_M = 0, last_chunk = 1;
@@ -197,6 +209,8 @@ void decode_error_impl(Impl& I, const float* z_host, int ew, int eh, double* tex
 // time); the array's device address is looked up once per GPU at init
 bool noalloc_scratch_setup(int device, std::string& why);
 void decode_error_noalloc_impl(Impl& I, const float* z_host, int ew, int eh, double* tex_mse, double* weighted);
+// kernels_stats.hip: the progress line's figures from device histograms
+void print_stats_impl(Impl& I, int qbits, int ew, int eh, ntc_print_stats* out);
 void dct_probe_impl(Impl& I, uint8_t* code, float* gain);
 void dct_refit_impl(Impl& I, uint8_t* code);
 void launch_dct_rate_pairs(Impl& I, int K, float sigma);

@@ -59,6 +59,20 @@ class DctDesc(C.Structure):
 _lib = None
 
 
+class PrintStats(C.Structure):
+    """ntc_print_stats: the progress line's figures (bitrate_stats, the quantized latent's error, latent_stats,
+    dct_analyze)"""
+    _fields_ = [(n, C.c_double) for n in ("bpp_fp32", "bpp_q8", "bpp_q8_ent", "bpp_q8_ctx", "bpp_ctx_level0", "bpp_est",
+                                          "bits_mlp", "bits_raw_latent", "bits_header")] + \
+               [("q_tex_mse", C.c_double * 4), ("q_weighted_mse", C.c_double), ("lat_mean", C.c_float * MAX_LEVELS),
+                ("lat_sd", C.c_float * MAX_LEVELS), ("lat_max", C.c_float * MAX_LEVELS), ("dct_live", C.c_int),
+                ("dct_raw", C.c_double * 7), ("dct_h0", C.c_double * 7), ("dct_ctx", C.c_double * 7),
+                ("dct_raw_total", C.c_double), ("dct_h0_total", C.c_double), ("dct_ctx_total", C.c_double),
+                ("dct_nblk", C.c_longlong), ("dct_ntok_nz", C.c_longlong), ("dct_ntok_eob", C.c_longlong),
+                ("dct_nmag_over", C.c_longlong), ("dct_nz_mean", C.c_double), ("dct_lnz_mean", C.c_double),
+                ("dct_eob_only_frac", C.c_double)]
+
+
 def library() -> C.CDLL:
     """The HIP backend. Raises if it is not built: there is no fallback path."""
     global _lib
@@ -110,6 +124,8 @@ def library() -> C.CDLL:
             "ntc_trainer_dct_refit": (None, [P, P]),
             "ntc_trainer_decode_error": (None, [P, P, C.c_int, C.c_int, P, P]),
             "ntc_trainer_decode_error_noalloc": (None, [P, P, C.c_int, C.c_int, P, P]),
+            "ntc_trainer_print_stats": (None, [P, C.c_int, C.c_int, C.c_int, C.POINTER(PrintStats)]),
+            "ntc_trainer_debug_print_counts": (C.c_size_t, [P, P, C.c_size_t, P, P, C.c_size_t, P]),
             "ntc_trainer_decode_rgb8": (None, [P, P]),
             "ntc_trainer_debug_gauss": (None, [P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, C.c_size_t, P]),
             "ntc_trainer_debug_noise_factors": (None, [P, C.c_uint32, C.c_size_t, P, P]),
@@ -348,6 +364,21 @@ class Trainer:
         zh = None if z is None else _f32(z, self.nz)
         self._lib.ntc_trainer_decode_error_noalloc(self._h, _ptr(zh), ew, eh, tex.ctypes.data, C.addressof(wt))
         return tex[:T], wt.value
+
+    def print_stats(self, qbits=8, ew=0, eh=0) -> PrintStats:
+        """the reference's progress-line figures from the device (bitrate_stats as a progress print runs it, the
+        quantized latent's 8-bit error, latent_stats, dct_analyze of a live --dct-q plane); no model download"""
+        out = PrintStats()
+        self._lib.ntc_trainer_print_stats(self._h, qbits, ew, eh, C.byref(out))
+        return out
+
+    def debug_print_counts(self):
+        """(bitrate histograms, lohi [3 x 64 x 2], dct histograms) of the last print_stats"""
+        nd = C.c_size_t()
+        nb = self._lib.ntc_trainer_debug_print_counts(self._h, None, 0, None, None, 0, C.byref(nd))
+        hb, lohi, hd = np.zeros(max(nb, 1), np.int64), np.zeros(3 * 64 * 2, np.float32), np.zeros(max(nd.value, 1), np.int64)
+        self._lib.ntc_trainer_debug_print_counts(self._h, hb.ctypes.data, nb, lohi.ctypes.data, hd.ctypes.data, nd.value, None)
+        return hb[:nb], lohi, hd[:nd.value]
 
     # ---- steps
     def mlp_step(self, it, sigma, lr, N, M):

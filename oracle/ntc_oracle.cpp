@@ -924,3 +924,264 @@ extern "C" void or_mse_of(const float* a, const float* b, int W, int H, int nc, 
     *weighted = ws / (3.0 * wsum * npix);
 }
 
+
+// ---------------------------------------------------------------- the progress print's statistics
+namespace {
+double cl0(double cnt, double tot) { return cnt != 0.0 && tot != 0.0 ? -std::log2(cnt / tot) : 0.0; }   // main.cpp:1130
+// bits of channel c of level l as bitrate_stats charges it (main.cpp:2285-2288, 2297); *kind: 0 continuous, 1 discrete (qat), 2 --qes
+int level_bits(const OrModel& m, const OrPrintIn& in, int l, int c, int* kind) {
+    const bool fixed = l == 0 && in.qat > 0;
+    const bool qes = in.qes_live && in.qes_bits[l] > 0;
+    *kind = fixed ? 1 : (qes ? 2 : 0);
+    if (fixed) return in.qat_ch[c];
+    if (qes) return in.qes_bits[l];
+    return (in.qes_on && in.qes_bits[l] > 0) ? in.qes_bits[l] : in.qbits;
+}
+// the quantization index of z[i] (channel c of level l) and its value
+int level_index(const OrPrintIn& in, int kind, int l, int c, int bits, float lo, float range, float zi, float zdi, float* q) {
+    const int levels = (1 << bits) - 1;
+    if (kind == 1) { *q = zi; return qat_index(zi, bits); }
+    if (kind == 2) { *q = zdi; return qes_index(zi, in.qes_lo[l * 64 + c], in.qes_range[l * 64 + c], levels); }
+    const int k = or_q8_index(zi, lo, range, levels);
+    *q = or_q8_value(k, lo, range, levels);
+    return k;
+}
+int dpcm_pred(const int* idx, int W, int x, int y) {   // main.cpp:2336-2337
+    const int lf = x ? idx[(size_t)y * W + x - 1] : -1, up = y ? idx[(size_t)(y - 1) * W + x] : -1;
+    return (lf >= 0 && up >= 0) ? (lf + up) / 2 : (lf >= 0 ? lf : (up >= 0 ? up : 0));
+}
+}   // namespace
+
+extern "C" {
+
+// dct_analyze, main.cpp:1080-1208: the figures of the progress line (per-class bits, token counts, nz / lnz / eob-only)
+void or_dct_analyze(const OrDct* d, int dc_raw_bits, int ctx, OrDctStats* out) {
+    const int* zz = dct_tables().zigzag;
+    OrDctStats S; memset(&S, 0, sizeof(S));
+    const size_t nb = (size_t)d->BW * d->BH, nbc = nb * (size_t)d->C;
+    S.nblk = (long long)nb;
+    long long sum_nz = 0, sum_lnz = 0, n_lnz = 0, eob_only = 0;
+    for (int c = 0; c < d->C; c++) {
+        std::vector<size_t> run_cnt(65, 0), mag_cnt(257, 0), ctxr_cnt(64, 0), ctxm_cnt(64, 0);
+        std::vector<size_t> ctx_run((size_t)64 * 65, 0), ctx_mag((size_t)64 * 257, 0), dcres_cnt(4097, 0);
+        size_t nrun = 0, neob = 0;
+        std::vector<int> dcs(nb, 0);
+        for (size_t b = 0; b < nb; b++) {   // pass 1: counts
+            const int16_t* sym = d->sym + (b * d->C + c) * 64;
+            const int dc = sym[0];
+            dcs[b] = dc;
+            const int bx = (int)(b % d->BW), by = (int)(b / d->BW);
+            const int pred = bx > 0 ? dcs[b - 1] : (by > 0 ? dcs[b - d->BW] : 0);
+            dcres_cnt[(size_t)std::max(0, std::min(4096, dc - pred + 2048))]++;
+            int run = 0, prev = 0, nz = 0, lnz = 0;
+            for (int p = 1; p < 64; p++) {
+                const int q = sym[zz[p]];
+                if (q == 0) { run++; continue; }
+                const int mag = std::min(256, std::abs(q)); if (std::abs(q) > 256) S.nmag_over++;
+                run_cnt[run]++; mag_cnt[mag]++; ctx_run[(size_t)prev * 65 + run]++; ctx_mag[(size_t)prev * 257 + mag]++; ctxr_cnt[prev]++; ctxm_cnt[prev]++;
+                nrun++; nz++; lnz = p; prev = p; run = 0;
+            }
+            if (lnz < 63) { run_cnt[64]++; ctx_run[(size_t)prev * 65 + 64]++; ctxr_cnt[prev]++; neob++; }
+            sum_nz += nz;
+            if (nz) { sum_lnz += lnz; n_lnz++; } else eob_only++;
+        }
+        S.ntok_nz += (long long)nrun; S.ntok_eob += (long long)neob;
+        const size_t nruntok = nrun + neob;
+        for (size_t b = 0; b < nb; b++) {   // pass 2: charge every token
+            const int16_t* sym = d->sym + (b * d->C + c) * 64;
+            const int bx = (int)(b % d->BW), by = (int)(b / d->BW);
+            const int pred = bx > 0 ? dcs[b - 1] : (by > 0 ? dcs[b - d->BW] : 0);
+            const double dcbits = cl0((double)dcres_cnt[(size_t)std::max(0, std::min(4096, sym[0] - pred + 2048))], (double)nb);
+            S.raw[0] += dc_raw_bits; S.h0[0] += dcbits; S.ctx[0] += dcbits;
+            int run = 0, prev = 0, lnz = 0;
+            for (int p = 1; p < 64; p++) {
+                const int q = sym[zz[p]];
+                if (q == 0) { run++; continue; }
+                const int mag = std::min(256, std::abs(q));
+                const double r0 = cl0((double)run_cnt[run], (double)nruntok), m0 = cl0((double)mag_cnt[mag], (double)nrun);
+                const double rc = cl0((double)ctx_run[(size_t)prev * 65 + run], (double)ctxr_cnt[prev]);
+                const double mc = cl0((double)ctx_mag[(size_t)prev * 257 + mag], (double)ctxm_cnt[prev]);
+                S.raw[1] += 7; S.raw[2] += 8; S.raw[3] += 1;
+                S.h0[1] += r0; S.h0[2] += m0; S.h0[3] += 1;
+                S.ctx[1] += rc; S.ctx[2] += mc; S.ctx[3] += 1;
+                lnz = p; prev = p; run = 0;
+            }
+            if (lnz < 63) {
+                S.raw[4] += 7; S.h0[4] += cl0((double)run_cnt[64], (double)nruntok); S.ctx[4] += cl0((double)ctx_run[(size_t)prev * 65 + 64], (double)ctxr_cnt[prev]);
+            }
+        }
+        // scale codes: 4 bits raw, order-0, and the (up, left) context estimate of the BW x BH code grid (main.cpp:1162-1166,
+        // context_entropy_bits main.cpp:2242-2258: H(X, U, L) - H(U, L), out-of-grid neighbours as code 0)
+        size_t chist[16] = { 0 };
+        for (size_t b = 0; b < nb; b++) chist[d->code[b * d->C + c]]++;
+        double ch0 = 0; for (int k = 0; k < 16; k++) if (chist[k]) ch0 += (double)chist[k] * cl0((double)chist[k], (double)nb);
+        double cctx = ch0;
+        if (ctx) {
+            std::vector<size_t> tri(4096, 0), pair(256, 0);
+            for (int y = 0; y < d->BH; y++)
+                for (int x = 0; x < d->BW; x++) {
+                    const int s = d->code[((size_t)y * d->BW + x) * d->C + c];
+                    const int u = y ? d->code[((size_t)(y - 1) * d->BW + x) * d->C + c] : 0;
+                    const int l = x ? d->code[((size_t)y * d->BW + x - 1) * d->C + c] : 0;
+                    tri[(size_t)u * 256 + l * 16 + s]++; pair[(size_t)u * 16 + l]++;
+                }
+            double hxul = 0, hul = 0;
+            for (size_t i = 0; i < tri.size(); i++) if (tri[i]) hxul -= (double)tri[i] * std::log2((double)tri[i] / (double)nb);
+            for (size_t i = 0; i < pair.size(); i++) if (pair[i]) hul -= (double)pair[i] * std::log2((double)pair[i] / (double)nb);
+            cctx = hxul - hul;
+        }
+        S.code_raw += 4.0 * (double)nb; S.code_h0 += ch0; S.code_ctx += cctx;
+        S.header += 3 * 32.0;
+    }
+    S.raw[5] = S.code_raw; S.h0[5] = S.code_h0; S.ctx[5] = S.code_ctx;
+    S.raw[6] = S.h0[6] = S.ctx[6] = S.header;
+    for (int k = 0; k < 7; k++) { S.raw_total += S.raw[k]; S.h0_total += S.h0[k]; S.ctx_total += S.ctx[k]; }
+    S.nz_mean = nbc ? (double)sum_nz / (double)nbc : 0;
+    S.lnz_mean = n_lnz ? (double)sum_lnz / (double)n_lnz : 0;
+    S.eob_only_frac = nbc ? (double)eob_only / (double)nbc : 0;
+    *out = S;
+}
+
+// bitrate_stats, main.cpp:2273-2352 as a progress print runs it (order-0 in place of the context estimate)
+void or_bitrate_stats(const OrModel* mp, const OrPrintIn* in, long long P, const float* z, const float* zdec, OrBitrate* out, float* zq) {
+    const OrModel& m = *mp;
+    OrBitrate s; memset(&s, 0, sizeof(s));
+    const double npix = (double)m.W * m.H;
+    const long long nz = nzof(m);
+    s.bits_mlp = (double)P * 16.0;
+    s.bpp_fp32 = ((double)nz * 32.0 + (double)P * 32.0) / npix;
+    double ent = 0, header = 0, raw = 0, ctxb = 0, est = 0;
+    for (int l = 0; l < m.nlev; l++) {
+        const OrLevel& L = m.lv[l];
+        const size_t nl = (size_t)L.W * L.H * L.C;
+        const double ntex = (double)L.W * L.H;
+        float* q = zq + L.off;
+        if (l == 0 && in->dct_live) {
+            OrDctStats b; or_dct_analyze(in->dct, in->dc_raw_bits, 0, &b);
+            raw += b.raw_total - b.header; ent += b.h0_total - b.header; ctxb += b.ctx_total - b.header; est += b.h0_total - b.header;
+            s.bpp_ctx_level0 += (b.ctx_total - b.header) / npix;
+            header += b.header;
+            memcpy(q, zdec + L.off, nl * sizeof(float));
+            continue;
+        }
+        int kind0; (void)level_bits(m, *in, l, 0, &kind0);
+        if (kind0 == 0) raw += (double)nl * (double)level_bits(m, *in, l, 0, &kind0);
+        for (int c = 0; c < L.C; c++) {
+            int kind; const int bits = level_bits(m, *in, l, c, &kind);
+            const int levels = (1 << bits) - 1;
+            if (kind != 0) raw += ntex * (double)bits;
+            float lo = 1e30f, hi = -1e30f;
+            if (kind == 0) for (size_t i = c; i < nl; i += L.C) { lo = std::min(lo, z[L.off + i]); hi = std::max(hi, z[L.off + i]); }
+            const float range = std::max(hi - lo, 1e-6f);
+            std::vector<int> hist(levels + 1, 0), idx((size_t)L.W * L.H);
+            for (size_t i = c, t = 0; i < nl; i += L.C, t++) {
+                const int qi = level_index(*in, kind, l, c, bits, lo, range, z[L.off + i], zdec[L.off + i], &q[i]);
+                hist[qi]++; idx[t] = qi;
+            }
+            double h0 = 0;
+            for (int v = 0; v <= levels; v++) if (hist[v]) h0 -= hist[v] * std::log2(hist[v] / ntex);
+            ent += h0;
+            if (l == 0) { ctxb += h0; s.bpp_ctx_level0 += h0 / npix; est += h0; }
+            else {
+                ctxb += h0;
+                std::vector<int> rh(levels + 1, 0);
+                for (int y = 0; y < L.H; y++)
+                    for (int x = 0; x < L.W; x++) rh[(idx[(size_t)y * L.W + x] - dpcm_pred(idx.data(), L.W, x, y)) & levels]++;
+                double hr = 0;
+                for (int v = 0; v <= levels; v++) if (rh[v]) hr -= rh[v] * std::log2(rh[v] / ntex);
+                est += hr;
+            }
+        }
+        if (kind0 != 1) header += L.C * 2 * 32.0;
+    }
+    s.bpp_q8 = (raw + header + s.bits_mlp) / npix;
+    s.bpp_q8_ent = (ent + header + s.bits_mlp) / npix;
+    s.bpp_q8_ctx = (ctxb + header + s.bits_mlp) / npix;
+    s.bpp_est = (est + header + s.bits_mlp) / npix;
+    s.bits_raw_latent = raw; s.bits_header = header;
+    *out = s;
+}
+
+// latent_stats, main.cpp:2211-2216
+void or_latent_stats(const OrModel* m, int l, const float* z, float* mean, float* sd, float* mx) {
+    const OrLevel& L = m->lv[l];
+    const size_t n = (size_t)L.W * L.H * L.C;
+    double s = 0, s2 = 0; float x = 0;
+    for (size_t i = 0; i < n; i++) { const float v = z[L.off + i]; s += v; s2 += (double)v * v; x = std::max(x, std::fabs(v)); }
+    *mean = (float)(s / n);
+    *sd = (float)std::sqrt(std::max(0.0, s2 / n - (s / n) * (s / n)));
+    *mx = x;
+}
+
+void or_print_counts_size(const OrModel* mp, const OrPrintIn* in, long long* n_bitrate, long long* n_dct) {
+    long long nb = 0;
+    for (int l = 0; l < mp->nlev; l++) {
+        if (l == 0 && in->dct_live) continue;
+        for (int c = 0; c < mp->lv[l].C; c++) { int kind; nb += (long long)(1 << level_bits(*mp, *in, l, c, &kind)) * (l >= 1 ? 2 : 1); }
+    }
+    *n_bitrate = nb;
+    *n_dct = in->dct_live ? (long long)in->dct->C * OR_DCT_COUNTS_PER_CH + OR_DCT_COUNTS_TAIL : 0;
+}
+
+void or_print_counts(const OrModel* mp, const OrPrintIn* in, const float* z, const float* zdec, long long* bitrate, float* lohi,
+                     long long* dct) {
+    const OrModel& m = *mp;
+    long long nb_, nd_; or_print_counts_size(mp, in, &nb_, &nd_);
+    memset(bitrate, 0, (size_t)nb_ * sizeof(long long));
+    long long* h = bitrate;
+    for (int l = 0; l < m.nlev; l++) {
+        const OrLevel& L = m.lv[l];
+        if (l == 0 && in->dct_live) continue;
+        const size_t nl = (size_t)L.W * L.H * L.C;
+        for (int c = 0; c < L.C; c++) {
+            int kind; const int bits = level_bits(m, *in, l, c, &kind);
+            const int nbin = 1 << bits;
+            float lo = 1e30f, hi = -1e30f;
+            if (kind == 0) for (size_t i = c; i < nl; i += L.C) { lo = std::min(lo, z[L.off + i]); hi = std::max(hi, z[L.off + i]); }
+            lohi[(l * 64 + c) * 2] = lo; lohi[(l * 64 + c) * 2 + 1] = hi;
+            const float range = std::max(hi - lo, 1e-6f);
+            std::vector<int> idx((size_t)L.W * L.H);
+            for (size_t i = c, t = 0; i < nl; i += L.C, t++) { float q; idx[t] = level_index(*in, kind, l, c, bits, lo, range, z[L.off + i], zdec[L.off + i], &q); h[idx[t]]++; }
+            h += nbin;
+            if (l >= 1) {
+                for (int y = 0; y < L.H; y++)
+                    for (int x = 0; x < L.W; x++) h[(idx[(size_t)y * L.W + x] - dpcm_pred(idx.data(), L.W, x, y)) & (nbin - 1)]++;
+                h += nbin;
+            }
+        }
+    }
+    if (!in->dct_live) return;
+    const OrDct* d = in->dct;
+    const int* zz = dct_tables().zigzag;
+    memset(dct, 0, (size_t)nd_ * sizeof(long long));
+    const size_t nb = (size_t)d->BW * d->BH;
+    long long* tail = dct + (size_t)d->C * OR_DCT_COUNTS_PER_CH;
+    for (int c = 0; c < d->C; c++) {
+        long long* runh = dct + (size_t)c * OR_DCT_COUNTS_PER_CH;
+        long long *mag = runh + 65, *cr = mag + 257, *cm = cr + 64 * 65, *ctxr = cm + 64 * 257, *ctxm = ctxr + 64, *dcres = ctxm + 64;
+        long long *code = dcres + 4097, *tri = code + 16, *pair = tri + 4096, *sc = pair + 256;   // sc: nrun neob nsign
+        for (size_t b = 0; b < nb; b++) {
+            const int16_t* sym = d->sym + (b * d->C + c) * 64;
+            const int bx = (int)(b % d->BW), by = (int)(b / d->BW);
+            const int pred = bx > 0 ? d->sym[((b - 1) * d->C + c) * 64] : (by > 0 ? d->sym[((b - d->BW) * d->C + c) * 64] : 0);
+            dcres[std::max(0, std::min(4096, sym[0] - pred + 2048))]++;
+            int run = 0, prev = 0, nz = 0, lnz = 0;
+            for (int p = 1; p < 64; p++) {
+                const int q = sym[zz[p]];
+                if (q == 0) { run++; continue; }
+                const int mg = std::min(256, std::abs(q)); if (std::abs(q) > 256) tail[4]++;
+                runh[run]++; mag[mg]++; cr[prev * 65 + run]++; cm[prev * 257 + mg]++; ctxr[prev]++; ctxm[prev]++;
+                sc[0]++; sc[2]++; nz++; lnz = p; prev = p; run = 0;
+            }
+            if (lnz < 63) { runh[64]++; cr[prev * 65 + 64]++; ctxr[prev]++; sc[1]++; }
+            tail[0] += nz;
+            if (nz) { tail[1] += lnz; tail[2]++; } else tail[3]++;
+            const int k = d->code[b * d->C + c];
+            code[k]++;
+            const int u = by ? d->code[(b - d->BW) * d->C + c] : 0, lf = bx ? d->code[(b - 1) * d->C + c] : 0;
+            tri[u * 256 + lf * 16 + k]++; pair[u * 16 + lf]++;
+        }
+    }
+}
+
+}   // extern "C"

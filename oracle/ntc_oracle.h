@@ -178,3 +178,53 @@ double or_train_iter(const OrModel* m, const OrTrainCfg* c, OrTrainState* s, con
 #ifdef __cplusplus
 }
 #endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+/* ---- the progress print's statistics (main.cpp:4155-4212): bitrate_stats (main.cpp:2220-2352, with the
+ * order-0 figure standing in for the context estimate as on a progress print), dct_analyze (main.cpp:1049-1208)
+ * and latent_stats (main.cpp:2211-2216). */
+typedef struct OrPrintIn {
+    int qbits;                        /* --qbits: the post-hoc depth of a continuous level */
+    int qat; int qat_ch[16];          /* qat > 0: level 0 discrete, qat_ch bits per channel */
+    int qes_on;                       /* the model has --qes levels (qes_bits); a continuous one is quantized at its depth */
+    int qes_live;                     /* --qes levels trained quantized: indices by qes_index with qes_lo / qes_range */
+    int qes_bits[OR_MAX_LEVELS];
+    const float* qes_lo;              /* [level][64] */
+    const float* qes_range;           /* [level][64] */
+    int dct_live; const OrDct* dct; int dc_raw_bits;
+    int dct_ctx;                      /* dct_analyze with the code grid's context estimate (g_ctx_stats) */
+} OrPrintIn;
+typedef struct OrBitrate {
+    double bpp_fp32, bpp_q8, bpp_q8_ent, bpp_q8_ctx, bpp_ctx_level0, bpp_est, bits_mlp, bits_raw_latent, bits_header;
+} OrBitrate;
+typedef struct OrDctStats {
+    double raw[7], h0[7], ctx[7];     /* dc, run, mag, sign, eob, code, header */
+    double raw_total, h0_total, ctx_total, code_raw, code_h0, code_ctx, header;
+    long long nblk, ntok_nz, ntok_eob, nmag_over;
+    double nz_mean, lnz_mean, eob_only_frac;
+} OrDctStats;
+/* bitrate_stats: figures, and zq = the quantized latent it returns (nz floats); P = MLP parameters */
+void or_bitrate_stats(const OrModel* m, const OrPrintIn* in, long long P, const float* z, const float* zdec, OrBitrate* out, float* zq);
+/* dct_analyze of all channels */
+void or_dct_analyze(const OrDct* d, int dc_raw_bits, int ctx, OrDctStats* out);
+/* latent_stats of level l of z */
+void or_latent_stats(const OrModel* m, int l, const float* z, float* mean, float* sd, float* mx);
+
+/* The integer histograms the figures above are sums over (the device path fills the same layout):
+ *   bitrate: for each level l (a live DCT level 0 skipped), each channel c, with nb = 2^bits(l, c): nb index bins, then for
+ *            l >= 1 nb bins of the DPCM residual (cur - pred) & (nb - 1) of bpp_est; lohi[l][c][2] = the channel's min and
+ *            max (continuous levels; the post-hoc scale)
+ *   dct, per channel: run[65] mag[257] ctx_run[64 x 65] ctx_mag[64 x 257] ctxr[64] ctxm[64] dcres[4097] code[16]
+ *            code_tri[16 x 16 x 16] (up, left, code) code_pair[16 x 16] (up, left) nrun neob nsign; then over all channels
+ *            sum_nz sum_lnz n_lnz eob_only nmag_over
+ * or_print_counts_size returns both sizes; or_print_counts fills them (lohi: 3 x 64 x 2 floats). */
+#define OR_DCT_COUNTS_PER_CH (65 + 257 + 64 * 65 + 64 * 257 + 64 + 64 + 4097 + 16 + 4096 + 256 + 3)
+#define OR_DCT_COUNTS_TAIL 5
+void or_print_counts_size(const OrModel* m, const OrPrintIn* in, long long* n_bitrate, long long* n_dct);
+void or_print_counts(const OrModel* m, const OrPrintIn* in, const float* z, const float* zdec, long long* bitrate, float* lohi,
+                     long long* dct);
+#ifdef __cplusplus
+}
+#endif

@@ -50,6 +50,28 @@ class OrTrainState(C.Structure):
                 ("zv", C.POINTER(C.c_float)), ("zt", C.c_int), ("lat_step_no", C.c_int)]
 
 
+class OrPrintIn(C.Structure):
+    _fields_ = [("qbits", C.c_int), ("qat", C.c_int), ("qat_ch", C.c_int * 16), ("qes_on", C.c_int), ("qes_live", C.c_int),
+                ("qes_bits", C.c_int * MAX_LEVELS), ("qes_lo", C.POINTER(C.c_float)), ("qes_range", C.POINTER(C.c_float)),
+                ("dct_live", C.c_int), ("dct", C.POINTER(OrDct)), ("dc_raw_bits", C.c_int), ("dct_ctx", C.c_int)]
+
+
+class OrBitrate(C.Structure):
+    _fields_ = [(n, C.c_double) for n in ("bpp_fp32", "bpp_q8", "bpp_q8_ent", "bpp_q8_ctx", "bpp_ctx_level0", "bpp_est",
+                                          "bits_mlp", "bits_raw_latent", "bits_header")]
+
+
+class OrDctStats(C.Structure):
+    _fields_ = [("raw", C.c_double * 7), ("h0", C.c_double * 7), ("ctx", C.c_double * 7)] + \
+               [(n, C.c_double) for n in ("raw_total", "h0_total", "ctx_total", "code_raw", "code_h0", "code_ctx", "header")] + \
+               [(n, C.c_longlong) for n in ("nblk", "ntok_nz", "ntok_eob", "nmag_over")] + \
+               [(n, C.c_double) for n in ("nz_mean", "lnz_mean", "eob_only_frac")]
+
+
+DCT_COUNTS_PER_CH = 65 + 257 + 64 * 65 + 64 * 257 + 64 + 64 + 4097 + 16 + 4096 + 256 + 3
+DCT_COUNTS_TAIL = 5
+
+
 @dataclass
 class Model:
     """A decoder layout: image size, latent levels (W, H, C, nearest), positional kinds, MLP."""
@@ -211,6 +233,13 @@ class Lib:
             fn.restype = res
             fn.argtypes = args
             setattr(self, "_" + name, fn)
+        for fn in ("bitrate_stats", "dct_analyze", "latent_stats", "print_counts_size", "print_counts"):
+            f = getattr(self.lib, prefix + fn, None)
+            if f is not None:
+                f.restype = None
+                f.argtypes = {"bitrate_stats": [_P, _P, C.c_longlong, _P, _P, _P, _P], "dct_analyze": [_P, C.c_int, C.c_int, _P],
+                              "latent_stats": [_P, C.c_int, _P, _P, _P, _P], "print_counts_size": [_P, _P, _P, _P],
+                              "print_counts": [_P, _P, _P, _P, _P, _P, _P]}[fn]
         if prefix == "or_":
             self.lib.or_train_iter.restype = C.c_double
             self.lib.or_train_iter.argtypes = [_P, _P, _P, _P, C.c_int, C.c_int]
@@ -353,6 +382,59 @@ class Lib:
         bits[: len(ch_bits)] = ch_bits
         self._qat_search(C.byref(model_of(m)), p.ctypes.data, z.ctypes.data, tgt.ctypes.data, bits.ctypes.data,
                          np.ascontiguousarray(grid, np.float32).ctypes.data)
+
+
+    # ---- the progress print's statistics (bitrate_stats, dct_analyze, latent_stats; the histograms behind them)
+    def bitrate_stats(self, m, pin, P, z, zdec):
+        """(OrBitrate, the quantized latent zq)"""
+        mc = model_of(m)
+        out, zq = OrBitrate(), np.zeros(z.size, np.float32)
+        getattr(self.lib, self.prefix + "bitrate_stats")(C.byref(mc), C.byref(pin), int(P), z.ctypes.data, zdec.ctypes.data,
+                                                          C.byref(out), zq.ctypes.data)
+        return out, zq
+
+    def dct_analyze(self, d, dc_raw_bits, ctx):
+        out = OrDctStats()
+        getattr(self.lib, self.prefix + "dct_analyze")(C.byref(d), dc_raw_bits, int(ctx), C.byref(out))
+        return out
+
+    def latent_stats(self, m, level, z):
+        a, b, c = C.c_float(), C.c_float(), C.c_float()
+        getattr(self.lib, self.prefix + "latent_stats")(C.byref(model_of(m)), level, z.ctypes.data, C.byref(a), C.byref(b),
+                                                         C.byref(c))
+        return a.value, b.value, c.value
+
+    def print_counts(self, m, pin, z, zdec):
+        """(bitrate histograms, lohi [3][64][2], dct histograms) in the layout ntc_oracle.h documents"""
+        mc = model_of(m)
+        nb, nd = C.c_longlong(), C.c_longlong()
+        self.lib.or_print_counts_size(C.byref(mc), C.byref(pin), C.byref(nb), C.byref(nd))
+        hb, lohi, hd = np.zeros(max(nb.value, 1), np.int64), np.zeros(3 * 64 * 2, np.float32), np.zeros(max(nd.value, 1), np.int64)
+        self.lib.or_print_counts(C.byref(mc), C.byref(pin), z.ctypes.data, zdec.ctypes.data, hb.ctypes.data, lohi.ctypes.data,
+                                 hd.ctypes.data)
+        return hb[: nb.value], lohi, hd[: nd.value]
+
+
+def print_in(qbits=8, qat_ch=None, qes_bits=None, qes_on=False, qes_live=False, qes_lo=None, qes_range=None, dct=None,
+             dc_raw_bits=8, dct_ctx=False):
+    """an OrPrintIn (the arrays it points at are kept alive on the returned object)"""
+    pin = OrPrintIn()
+    pin.qbits = qbits
+    if qat_ch:
+        pin.qat = max(qat_ch)
+        for c, b in enumerate(qat_ch):
+            pin.qat_ch[c] = b
+    pin.qes_on, pin.qes_live = int(qes_on), int(qes_live)
+    for l, b in enumerate(qes_bits or []):
+        pin.qes_bits[l] = b
+    lo = np.zeros(3 * 64, np.float32) if qes_lo is None else np.ascontiguousarray(qes_lo, np.float32)
+    rg = np.ones(3 * 64, np.float32) if qes_range is None else np.ascontiguousarray(qes_range, np.float32)
+    pin.qes_lo, pin.qes_range = _f(lo), _f(rg)
+    pin._keep = (lo, rg, dct)
+    if dct is not None:
+        pin.dct_live, pin.dct, pin.dc_raw_bits = 1, C.pointer(dct), dc_raw_bits
+    pin.dct_ctx = int(dct_ctx)
+    return pin
 
 
 def oracle() -> Lib:

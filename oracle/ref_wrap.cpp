@@ -256,6 +256,66 @@ void ref_mse_of(const float* a, const float* b, int W, int H, int nc, const floa
     *weighted = m.weighted;
 }
 
+// ---- the progress print's statistics: the reference's own bitrate_stats (with g_ctx_stats off, as a progress
+// print runs it, main.cpp:4171), dct_analyze (g_ctx_stats as asked) and latent_stats
+namespace {
+void print_decoder(RefModel& R, const OrModel* m, const OrPrintIn* in, const float* z, const float* zdec, long long P) {
+    std::vector<float> p((size_t)P, 0.0f);
+    fill_decoder(R, *m, z, p.data(), nullptr);
+    Decoder& D = R.D;
+    if (in->qat > 0) {
+        qat_init_grid();
+        D.qat_ch.assign(in->qat_ch, in->qat_ch + m->lv[0].C);
+        D.qat_bits = *std::max_element(D.qat_ch.begin(), D.qat_ch.end());
+    }
+    D.qes_on = in->qes_on != 0;
+    D.qes_live = in->qes_live != 0;
+    for (int l = 0; l < m->nlev; l++) {
+        D.qes[l].bits = in->qes_bits[l];
+        if (in->qes_live && in->qes_bits[l] > 0) {
+            const int C = m->lv[l].C;
+            D.qes[l].lo.assign(in->qes_lo + l * 64, in->qes_lo + l * 64 + C);
+            D.qes[l].range.assign(in->qes_range + l * 64, in->qes_range + l * 64 + C);
+            D.qes[l].hi.assign(C, 0.0f);
+        }
+    }
+    if (in->dct_live) {
+        D.dct = dct_level_of(in->dct);
+        D.dct.dc_raw_bits = in->dc_raw_bits;
+    }
+    D.zq.assign(zdec, zdec + D.lat.z.size());
+}
+}   // namespace
+void ref_bitrate_stats(const OrModel* m, const OrPrintIn* in, long long P, const float* z, const float* zdec, OrBitrate* out, float* zq) {
+    RefModel R; print_decoder(R, m, in, z, zdec, P);
+    std::vector<float> q;
+    g_ctx_stats = false;
+    const BitrateStats b = bitrate_stats(R.D, in->qbits, q);
+    g_ctx_stats = true;
+    out->bpp_fp32 = b.bpp_fp32; out->bpp_q8 = b.bpp_q8; out->bpp_q8_ent = b.bpp_q8_ent; out->bpp_q8_ctx = b.bpp_q8_ctx;
+    out->bpp_ctx_level0 = b.bpp_ctx_level0; out->bpp_est = b.bpp_est; out->bits_mlp = b.bits_mlp;
+    out->bits_raw_latent = b.bits_raw_latent; out->bits_header = b.bits_header;
+    memcpy(zq, q.data(), q.size() * sizeof(float));
+}
+void ref_dct_analyze(const OrDct* d, int dc_raw_bits, int ctx, OrDctStats* out) {
+    DctLevel Q = dct_level_of(d);
+    Q.dc_raw_bits = dc_raw_bits;
+    g_ctx_stats = ctx != 0;
+    const DctStats S = dct_analyze(Q);
+    g_ctx_stats = true;
+    memset(out, 0, sizeof(*out));
+    for (int k = 0; k < 7; k++) { out->raw[k] = S.raw[k]; out->h0[k] = S.h0[k]; out->ctx[k] = S.ctx[k]; }
+    out->raw_total = S.raw_total; out->h0_total = S.h0_total; out->ctx_total = S.ctx_total;
+    out->code_raw = S.code_raw; out->code_h0 = S.code_h0; out->code_ctx = S.code_ctx; out->header = S.header;
+    out->nblk = (long long)S.nblk; out->ntok_nz = (long long)S.ntok_nz; out->ntok_eob = (long long)S.ntok_eob;
+    out->nmag_over = (long long)S.nmag_over;
+    out->nz_mean = S.nz_mean; out->lnz_mean = S.lnz_mean; out->eob_only_frac = S.eob_only_frac;
+}
+void ref_latent_stats(const OrModel* m, int l, const float* z, float* mean, float* sd, float* mx) {
+    RefModel R; fill_decoder(R, *m, z, nullptr, nullptr);
+    latent_stats(R.D.lat.lv[l], R.D.lat.level(l), *mean, *sd, *mx);
+}
+
 // ---- fp16 and post-hoc quantization
 int ref_ntcb_selfcheck() { return ntcb_selfcheck() ? 1 : 0; }
 uint16_t ref_f32_to_f16(float f, int* overflow) { bool ov = false; const uint16_t h = ntcb_f32_to_f16(f, &ov); *overflow = ov ? 1 : 0; return h; }

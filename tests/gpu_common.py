@@ -8,7 +8,7 @@ import sys
 import numpy as np
 
 from neural_block_textures_amd import synth
-from neural_block_textures_amd.trainer import PK_LV1LOCAL, PK_UV, DctDesc, Layout, Trainer
+from neural_block_textures_amd.trainer import PK_LV1LOCAL, PK_UV, DctDesc, Layout, QesDesc, Trainer
 from oracle.oracle import OrDct, OrLevel
 
 # One layout per compiled MLP shape, at sizes the oracle finishes in seconds, plus one that runs
@@ -147,3 +147,45 @@ class HostDct:
         self.orc._dct_snap_level0(C.byref(self.d), C.byref(self.L0), zs.ctypes.data, zq.ctypes.data, bits.ctypes.data,
                                   cnt.ctypes.data)
         return zs, zq, bits, cnt
+
+
+def qes_tables(orc, lay, z, bits_per_level):
+    q = QesDesc()
+    grid_all = []
+    off = 0
+    for l, bits in enumerate(bits_per_level):
+        w, h, c, nr = lay.levels[l]
+        if bits:
+            L = OrLevel(w, h, c, int(nr), 0)
+            lo, hi, rg = (np.zeros(c, np.float32) for _ in range(3))
+            grid = np.zeros(c << bits, np.float32)
+            orc._qes_fit(C.byref(L), z[off:].ctypes.data, bits, lo.ctypes.data, hi.ctypes.data, rg.ctypes.data,
+                         grid.ctypes.data)
+            q.bits[l] = bits
+            for ch in range(c):
+                q.lo[l][ch], q.hi[l][ch], q.range[l][ch] = lo[ch], hi[ch], rg[ch]
+                q.grid_off[l][ch] = sum(g.size for g in grid_all) + ch * (1 << bits)
+            grid_all.append(grid)
+        off += w * h * c
+    q.live, q.frozen = 1, 1
+    return q, np.concatenate(grid_all)
+
+
+def host_snap(orc, lay, q, grid, z):
+    """Decoder::qes_refresh on a copy of the shadow: (clamped shadow, snapped copy)"""
+    z = z.copy()
+    zq = z.copy()
+    off = 0
+    for l, (w, h, c, nr) in enumerate(lay.levels):
+        n = w * h * c
+        if q.bits[l]:
+            L = OrLevel(w, h, c, int(nr), 0)
+            lo = np.array(q.lo[l][:c], np.float32); hi = np.array(q.hi[l][:c], np.float32)
+            rg = np.array(q.range[l][:c], np.float32)
+            g = grid[q.grid_off[l][0]:q.grid_off[l][0] + (c << q.bits[l])].copy()
+            zl, zql = z[off:off + n].copy(), np.zeros(n, np.float32)
+            orc._qes_snap_level(C.byref(L), int(q.bits[l]), lo.ctypes.data, hi.ctypes.data, rg.ctypes.data,
+                                g.ctypes.data, zl.ctypes.data, zql.ctypes.data, 1)
+            z[off:off + n], zq[off:off + n] = zl, zql
+        off += n
+    return z, zq

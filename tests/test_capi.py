@@ -39,7 +39,8 @@ def test_cpp_trainer_symbols_for_main_cpp():
 
 
 @pytest.mark.parametrize("name,cls", [("ntc_model_desc", T.ModelDesc), ("ntc_qes_desc", T.QesDesc),
-                                      ("ntc_dct_desc", T.DctDesc), ("ntc_level_desc", T.LevelDesc)])
+                                      ("ntc_dct_desc", T.DctDesc), ("ntc_level_desc", T.LevelDesc),
+                                      ("ntc_print_stats", T.PrintStats)])
 def test_struct_layouts(name, cls):
     assert T.library().ntc_abi_sizeof(name.encode()) == C.sizeof(cls)
 

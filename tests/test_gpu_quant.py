@@ -1,58 +1,14 @@
 """--qes and --dct-q on the device against the oracle, exact (the reference's --cuda-check items 6
 and 7, main.cpp:3152-3216): the snapped copy, the symbols, the plane, the scale codes, the proxy
 bits, the truncation counts, the rate-pass bit differences and hit count."""
-import ctypes as C
 
 import numpy as np
 import pytest
 
-from neural_block_textures_amd.trainer import Layout, QesDesc
-from oracle.oracle import OrLevel
-from tests.gpu_common import LAYOUTS, HostDct, data, dct_tables, say, trainer
+from neural_block_textures_amd.trainer import Layout
+from tests.gpu_common import LAYOUTS, HostDct, data, dct_tables, host_snap, qes_tables, say, trainer
 
 pytestmark = pytest.mark.gpu
-
-
-def qes_tables(orc, lay, z, bits_per_level):
-    q = QesDesc()
-    grid_all = []
-    off = 0
-    for l, bits in enumerate(bits_per_level):
-        w, h, c, nr = lay.levels[l]
-        if bits:
-            L = OrLevel(w, h, c, int(nr), 0)
-            lo, hi, rg = (np.zeros(c, np.float32) for _ in range(3))
-            grid = np.zeros(c << bits, np.float32)
-            orc._qes_fit(C.byref(L), z[off:].ctypes.data, bits, lo.ctypes.data, hi.ctypes.data, rg.ctypes.data,
-                         grid.ctypes.data)
-            q.bits[l] = bits
-            for ch in range(c):
-                q.lo[l][ch], q.hi[l][ch], q.range[l][ch] = lo[ch], hi[ch], rg[ch]
-                q.grid_off[l][ch] = sum(g.size for g in grid_all) + ch * (1 << bits)
-            grid_all.append(grid)
-        off += w * h * c
-    q.live, q.frozen = 1, 1
-    return q, np.concatenate(grid_all)
-
-
-def host_snap(orc, lay, q, grid, z):
-    """Decoder::qes_refresh on a copy of the shadow: (clamped shadow, snapped copy)"""
-    z = z.copy()
-    zq = z.copy()
-    off = 0
-    for l, (w, h, c, nr) in enumerate(lay.levels):
-        n = w * h * c
-        if q.bits[l]:
-            L = OrLevel(w, h, c, int(nr), 0)
-            lo = np.array(q.lo[l][:c], np.float32); hi = np.array(q.hi[l][:c], np.float32)
-            rg = np.array(q.range[l][:c], np.float32)
-            g = grid[q.grid_off[l][0]:q.grid_off[l][0] + (c << q.bits[l])].copy()
-            zl, zql = z[off:off + n].copy(), np.zeros(n, np.float32)
-            orc._qes_snap_level(C.byref(L), int(q.bits[l]), lo.ctypes.data, hi.ctypes.data, rg.ctypes.data,
-                                g.ctypes.data, zl.ctypes.data, zql.ctypes.data, 1)
-            z[off:off + n], zq[off:off + n] = zl, zql
-        off += n
-    return z, zq
 
 
 @pytest.mark.parametrize("name,bits", [("two_level", [0, 5]), ("rgb_24x2", [6]), ("runtime", [0, 3, 12]), ("jit_widths", [0, 3, 12])])

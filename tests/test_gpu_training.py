@@ -129,6 +129,7 @@ def live_dct(orc, w, lay, tr, z, p, tgt):
     assert np.array_equal(sym_d, H.sym) and np.array_equal(tr.download_zq()[:n0], zq2)
     assert np.array_equal(bits_d, bits2) and (nt_d, nz_d) == (cnt2[0], cnt2[1])
     say(f"{w.name}: snap of {H.n} blocks exact: {int(bits2.sum())} proxy bits/16, {nt_d} ACs truncated of {nz_d}")
+    return H
 
 
 @pytest.mark.parametrize("name", ["rgb256", "rgb512_two_level", "material512", "dct512", "material2048"])
