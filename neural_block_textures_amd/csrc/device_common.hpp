@@ -297,6 +297,14 @@ __device__ __forceinline__ void features_pm(const DevModel& m, const float* z, c
 // a read-only view of global memory; uniform addresses in it become scalar loads
 typedef __attribute__((address_space(4))) float CFloat;
 
+// Thread and workgroup ids read straight from the hardware. Kernels built with IEEE mode off cannot inline
+// the device library's id helpers (built with it on): blockIdx / threadIdx then become calls that return
+// VGPRs, every block-uniform index derived from them is treated as divergent (VALU address arithmetic,
+// divergent branches, waterfall loops over buffer descriptors). The builtins keep workgroup ids in SGPRs.
+__device__ __forceinline__ int tid_x() { return (int)__builtin_amdgcn_workitem_id_x(); }
+__device__ __forceinline__ int bid_x() { return (int)__builtin_amdgcn_workgroup_id_x(); }
+__device__ __forceinline__ int bid_y() { return (int)__builtin_amdgcn_workgroup_id_y(); }
+
 // A pointer every lane holds the same value of, moved to SGPRs (a value that flowed through a
 // loop with a per-lane trip count is otherwise treated as divergent).
 __device__ __forceinline__ const float* uniform_ptr(const float* p) {
@@ -457,7 +465,7 @@ __device__ __forceinline__ double wave_sum(double v) {
 template <int BLOCK>
 __device__ __forceinline__ double block_sum(double v, double* lds /* BLOCK / 64 */) {
     v = wave_sum(v);
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int lane = tid_x() & 63, wid = tid_x() >> 6;
     if (lane == 0) lds[wid] = v;
     __syncthreads();
     double r = 0.0;

@@ -138,15 +138,15 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     constexpr bool Es = From != kSets;
     __shared__ double red[kPopWaves];
     __shared__ float wpm_s[Es ? 2 * Q::kP : 1];   // ES: the + member's weights, then the - member's
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int pair = blockIdx.x, ch = blockIdx.y, sgn = wave & 1, half = wave >> 1;
+    const int lane = tid_x() & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
+    const int pair = bid_x(), ch = bid_y(), sgn = wave & 1, half = wave >> 1;
     const int i16 = lane & 15, g = lane >> 4;
     MfmaWeights<S> W;
     if constexpr (Es) {
         const uint64_t head = noise_head(src.seed, NS_MLP, src.step, (uint32_t)pair);
         float* eg = src.eps + (size_t)pair * Q::kP;
-        for (int k = threadIdx.x; k < Q::kP; k += 64 * kPopWaves) {
+        for (int k = tid_x(); k < Q::kP; k += 64 * kPopWaves) {
             float e;
             if constexpr (From == kDraw) {
                 e = gauss_at(src.nt, head, (uint64_t)k);
@@ -279,7 +279,7 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     e = wave_sum(e);
     if (lane == 0) red[wave] = e;
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid_x() == 0) {
         part[(size_t)(2 * pair) * chunks + ch] = red[0] + red[2];
         part[(size_t)(2 * pair + 1) * chunks + ch] = red[1] + red[3];
     }
@@ -310,8 +310,8 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     constexpr int NO = Q::kNout, kRounds = lat_rounds<S>();
     // at most 4 outputs: the output layer on the VALU leaves output g of pixel j in lane (g, j)
     constexpr bool kVOut = valu_out<S>();
-    const int k = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
+    const int k = bid_y();
+    const int lane = tid_x() & 63, wave = tid_x() >> 6, i16 = lane & 15, g = lane >> 4;
     const float* e = eps + (size_t)k * m.nz;
     float* out = dpix + (size_t)k * m.npix;
     MfmaWeights<S> W;
@@ -346,7 +346,7 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     };
     for (int rd = 0; rd < kRounds; rd++) {
         if (rd >= rounds) break;
-        const int base = blockIdx.x * 256 * rounds + 64 * rounds * wave + 64 * rd;   // tile t: pixels base + 16 t + j
+        const int base = bid_x() * 256 * rounds + 64 * rounds * wave + 64 * rd;   // tile t: pixels base + 16 t + j
         float tn[4];
         load_t(base, tn);
         float bp[4][Q::kKs1], bm[4][Q::kKs1];
@@ -415,7 +415,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                                                  const float* __restrict__ grid) {
     using Q = MfmaShape<S>;
     constexpr int NO = Q::kNout, C0 = S::kC0;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
+    const int lane = tid_x() & 63, wave = tid_x() >> 6, i16 = lane & 15, g = lane >> 4;
     MfmaWeights<S> W;
     mfma_load<S, false>(W, w, lane);
     if (!m.clamp_out) scale_output<S>(W, kNegLog2e);
@@ -429,7 +429,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
     } else {
         lane_cw<NO>(m.cw, g, cw);
     }
-    const int base = blockIdx.x * 256 + wave * 64;   // tile t: pixels base + 16 t + j
+    const int base = bid_x() * 256 + wave * 64;   // tile t: pixels base + 16 t + j
     float f[S::kMaxIn];
     {
         const int pr = min(base + lane, m.npix - 1);
