@@ -238,62 +238,6 @@ __device__ __forceinline__ void features(const DevModel& m, const Src& src, int 
     }
 }
 
-// The features of one pixel for both members of a latent pair at once (fixed shapes): every tap
-// and texel load is shared, each member's texel value is its own fused zb +- sg eps (a level outside
-// `mask` is unperturbed), and each member's blend is the single-member blend - so fp and fm equal
-// features<S> with PerturbedLatent{ z, eps, sg, mask } and { z, eps, -sg, mask }.
-template <int CMAX>
-__device__ __forceinline__ void sample_level_pm(const DevLevel& L, bool pert, const float* z, const float* e, float sg, const Tap& t,
-                                                float* fp, float* fm) {
-    auto val = [&](long long i, float& vp, float& vm) {
-        const float zb = z[i];
-        if (pert) { const float ee = e[i]; vp = __builtin_fmaf(sg, ee, zb); vm = __builtin_fmaf(-sg, ee, zb); }
-        else { vp = zb; vm = zb; }
-    };
-    const long long a = L.off + ((long long)t.y0 * L.W + t.x0) * L.C;
-    if (L.nearest) {
-#pragma unroll
-        for (int c = 0; c < CMAX; c++) val(a + c, fp[c], fm[c]);
-        return;
-    }
-    const long long b = L.off + ((long long)t.y0 * L.W + t.x1) * L.C;
-    const long long cc = L.off + ((long long)t.y1 * L.W + t.x0) * L.C;
-    const long long d = L.off + ((long long)t.y1 * L.W + t.x1) * L.C;
-    const Blend w = blend_of(t);
-#pragma unroll
-    for (int c = 0; c < CMAX; c++) {
-        float ap, am, bp, bm, cp, cm, dp, dm;
-        val(a + c, ap, am); val(b + c, bp, bm); val(cc + c, cp, cm); val(d + c, dp, dm);
-        fp[c] = blend(w, ap, bp, cp, dp);
-        fm[c] = blend(w, am, bm, cm, dm);
-    }
-}
-
-template <class S>
-__device__ __forceinline__ void features_pm(const DevModel& m, const float* z, const float* e, float sg, unsigned mask, int px, int py,
-                                            float (&fp)[S::kMaxIn], float (&fm)[S::kMaxIn]) {
-    static_assert(S::kFixed, "fixed shapes only");
-    const float u = pixel_u(px, m.W), v = pixel_u(py, m.H);
-    const Tap t0 = tap_of(m.lv[0].W, m.lv[0].H, m.lv[0].nearest != 0, u, v);
-    Tap t1 = t0;
-    sample_level_pm<S::kC0>(m.lv[0], mask & 1u, z, e, sg, t0, fp, fm);
-    if constexpr (S::kC1 > 0) {
-        t1 = tap_of(m.lv[1].W, m.lv[1].H, m.lv[1].nearest != 0, u, v);
-        sample_level_pm<S::kC1>(m.lv[1], (mask >> 1) & 1u, z, e, sg, t1, fp + S::kC0, fm + S::kC0);
-    }
-    if constexpr (S::kC2 > 0) {
-        const Tap t2 = tap_of(m.lv[2].W, m.lv[2].H, m.lv[2].nearest != 0, u, v);
-        sample_level_pm<S::kC2>(m.lv[2], (mask >> 2) & 1u, z, e, sg, t2, fp + S::kC0 + S::kC1, fm + S::kC0 + S::kC1);
-    }
-    constexpr int k0 = S::kC0 + S::kC1 + S::kC2;
-#pragma unroll
-    for (int q = 0; q < S::kNpos; q++) {
-        const bool uv = m.pos[q] == 0;
-        fp[k0 + 2 * q] = fm[k0 + 2 * q] = __builtin_fmaf(uv ? u : t1.fx, 2.0f, -1.0f);
-        fp[k0 + 2 * q + 1] = fm[k0 + 2 * q + 1] = __builtin_fmaf(uv ? v : t1.fy, 2.0f, -1.0f);
-    }
-}
-
 // a read-only view of global memory; uniform addresses in it become scalar loads
 typedef __attribute__((address_space(4))) float CFloat;
 
@@ -304,6 +248,15 @@ typedef __attribute__((address_space(4))) float CFloat;
 __device__ __forceinline__ int tid_x() { return (int)__builtin_amdgcn_workitem_id_x(); }
 __device__ __forceinline__ int bid_x() { return (int)__builtin_amdgcn_workgroup_id_x(); }
 __device__ __forceinline__ int bid_y() { return (int)__builtin_amdgcn_workgroup_id_y(); }
+
+// A raw buffer over `bytes` bytes at p: a load takes a 32-bit byte offset per lane (VGPR) and one per wave
+// (SGPR), and one past the end returns 0 instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const float* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float buffer_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
 
 // A pointer every lane holds the same value of, moved to SGPRs (a value that flowed through a
 // loop with a per-lane trip count is otherwise treated as divergent).

@@ -40,16 +40,10 @@ constexpr bool pop_own() { return valu_out<S>() && MfmaShape<S>::kHt == 1; }
 template <class S>
 constexpr int pop_u() { return pop_own<S>() ? 4 : 2; }
 
-// A raw buffer over the minibatch arrays: loads take a loop-invariant 32-bit lane offset (VGPR) and
-// the tile's byte offset (SGPR), so no address arithmetic per load. num_records = the allocation
-// (every read stays inside it: minibatch_rows(nin) feature rows, those past nin zero, and
+// The minibatch arrays are read through raw buffers (buffer_of): loads take a loop-invariant 32-bit lane
+// offset (VGPR) and the tile's byte offset (SGPR), so no address arithmetic per load. num_records = the
+// allocation (every read stays inside it: minibatch_rows(nin) feature rows, those past nin zero, and
 // kMinibatchSlack floats past the last row of each array).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const float* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ float buffer_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
-}
 
 // The targets a lane needs per tile: the pixel-per-lane output layer leaves every output of the lane's
 // own pixel in the lane (its nout targets, once per pass); models with at most 4 outputs otherwise take
@@ -301,6 +295,87 @@ __host__ __device__ constexpr int lat_rounds_of(int nin) { return nin <= 8 ? 2 :
 template <class S>
 constexpr int lat_rounds() { return lat_rounds_of(MfmaShape<S>::kIn); }
 
+// The features of one pixel for both members of a latent pair at once (fixed shapes): every tap and texel
+// load is shared, each member's texel value is its own fused zb +- sg eps (a level outside `mask` is
+// unperturbed), and each member's blend is the single-member blend - so fp and fm equal features<S> with
+// PerturbedLatent{ z, eps, sg, mask } and { z, eps, -sg, mask }. Texels are read through raw buffers with
+// 32-bit byte offsets (a latent holds fewer than 2^30 floats). The code has no branch per texel: a level
+// outside `mask` takes its Gaussians too, scaled by 0 (fma(0, eps, zb) = zb for the finite Gaussians, up to
+// the sign of a zero texel, which no output can see: the layers' sums and the activation treat +0 and -0
+// alike). A branch per texel (or stores under a branch) makes the compiler keep the features in scratch.
+template <int C>
+__device__ __forceinline__ void sample_level_pm(const DevLevel& L, bool pert, __amdgpu_buffer_rsrc_t rz, __amdgpu_buffer_rsrc_t re,
+                                                float sg, const Tap& t, float* fp, float* fm) {
+    const uint32_t off = (uint32_t)L.off, LW = (uint32_t)L.W, LC = (uint32_t)L.C;
+    const float sp = pert ? sg : 0.0f;
+    const uint32_t a = 4u * (off + ((uint32_t)t.y0 * LW + (uint32_t)t.x0) * LC);
+    if (L.nearest) {
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+            const float zb = buffer_f32(rz, a + 4u * c, 0u), ee = buffer_f32(re, a + 4u * c, 0u);
+            fp[c] = __builtin_fmaf(sp, ee, zb);
+            fm[c] = __builtin_fmaf(-sp, ee, zb);
+        }
+        return;
+    }
+    const uint32_t tap[4] = { a, 4u * (off + ((uint32_t)t.y0 * LW + (uint32_t)t.x1) * LC),
+                              4u * (off + ((uint32_t)t.y1 * LW + (uint32_t)t.x0) * LC),
+                              4u * (off + ((uint32_t)t.y1 * LW + (uint32_t)t.x1) * LC) };
+    const Blend w = blend_of(t);
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        float vp[4], vm[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float zb = buffer_f32(rz, tap[q] + 4u * c, 0u), ee = buffer_f32(re, tap[q] + 4u * c, 0u);
+            vp[q] = __builtin_fmaf(sp, ee, zb);
+            vm[q] = __builtin_fmaf(-sp, ee, zb);
+        }
+        fp[c] = blend(w, vp[0], vp[1], vp[2], vp[3]);
+        fm[c] = blend(w, vm[0], vm[1], vm[2], vm[3]);
+    }
+}
+
+template <class S>
+__device__ __forceinline__ void features_pm(const DevModel& m, __amdgpu_buffer_rsrc_t rz, __amdgpu_buffer_rsrc_t re, float sg, unsigned mask,
+                                            int px, int py, float (&fp)[S::kMaxIn], float (&fm)[S::kMaxIn]) {
+    static_assert(S::kFixed, "fixed shapes only");
+    const float u = pixel_u(px, m.W), v = pixel_u(py, m.H);
+    const Tap t0 = tap_of(m.lv[0].W, m.lv[0].H, m.lv[0].nearest != 0, u, v);
+    Tap t1 = t0;
+    sample_level_pm<S::kC0>(m.lv[0], mask & 1u, rz, re, sg, t0, fp, fm);
+    if constexpr (S::kC1 > 0) {
+        t1 = tap_of(m.lv[1].W, m.lv[1].H, m.lv[1].nearest != 0, u, v);
+        sample_level_pm<S::kC1>(m.lv[1], (mask >> 1) & 1u, rz, re, sg, t1, fp + S::kC0, fm + S::kC0);
+    }
+    if constexpr (S::kC2 > 0) {
+        const Tap t2 = tap_of(m.lv[2].W, m.lv[2].H, m.lv[2].nearest != 0, u, v);
+        sample_level_pm<S::kC2>(m.lv[2], (mask >> 2) & 1u, rz, re, sg, t2, fp + S::kC0 + S::kC1, fm + S::kC0 + S::kC1);
+    }
+    constexpr int k0 = S::kC0 + S::kC1 + S::kC2;
+#pragma unroll
+    for (int q = 0; q < S::kNpos; q++) {
+        const bool uv = m.pos[q] == 0;
+        fp[k0 + 2 * q] = fm[k0 + 2 * q] = __builtin_fmaf(uv ? u : t1.fx, 2.0f, -1.0f);
+        fp[k0 + 2 * q + 1] = fm[k0 + 2 * q + 1] = __builtin_fmaf(uv ? v : t1.fy, 2.0f, -1.0f);
+    }
+}
+
+// The column and row of pixel base + lane for a wave's 64 pixels from base (a multiple of 64): when the
+// image's width is a multiple of 64 they share one row (a scalar division), else each lane divides (pixels
+// past the last clamped to it).
+__device__ __forceinline__ void round_pixel(const DevModel& m, int base, int lane, int& px, int& py) {
+    if (m.W % 64 == 0 && base < m.npix) {
+        const int row = base / m.W;
+        px = base - row * m.W + lane;
+        py = row;
+    } else {
+        const int pr = min(base + lane, m.npix - 1);
+        px = pr % m.W;
+        py = pr / m.W;
+    }
+}
+
 
 template <class S, int Act, bool Clamp>
 __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* __restrict__ w, const float* __restrict__ zdec,
@@ -311,8 +386,8 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     // at most 4 outputs: the output layer on the VALU leaves output g of pixel j in lane (g, j)
     constexpr bool kVOut = valu_out<S>();
     const int k = bid_y();
-    const int lane = tid_x() & 63, wave = tid_x() >> 6, i16 = lane & 15, g = lane >> 4;
-    const float* e = eps + (size_t)k * m.nz;
+    const int lane = tid_x() & 63, wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6), i16 = lane & 15, g = lane >> 4;
+    const __amdgpu_buffer_rsrc_t rz = buffer_of(zdec, 4u * (uint32_t)m.nz), re = buffer_of(eps + (size_t)k * m.nz, 4u * (uint32_t)m.nz);
     float* out = dpix + (size_t)k * m.npix;
     MfmaWeights<S> W;
     mfma_load<S, false>(W, w, lane);
@@ -351,9 +426,10 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
         load_t(base, tn);
         float bp[4][Q::kKs1], bm[4][Q::kKs1];
         {
-            const int pr = min(base + lane, m.npix - 1);
+            int px, py;
+            round_pixel(m, base, lane, px, py);
             float fp[S::kMaxIn], fm[S::kMaxIn];
-            features_pm<S>(m, zdec, e, sg, mask, pr % m.W, pr / m.W, fp, fm);
+            features_pm<S>(m, rz, re, sg, mask, px, py, fp, fm);
             tiles_of<S>(fp, bp);
             tiles_of<S>(fm, bm);
         }
@@ -415,7 +491,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                                                  const float* __restrict__ grid) {
     using Q = MfmaShape<S>;
     constexpr int NO = Q::kNout, C0 = S::kC0;
-    const int lane = tid_x() & 63, wave = tid_x() >> 6, i16 = lane & 15, g = lane >> 4;
+    const int lane = tid_x() & 63, wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6), i16 = lane & 15, g = lane >> 4;
     MfmaWeights<S> W;
     mfma_load<S, false>(W, w, lane);
     if (!m.clamp_out) scale_output<S>(W, kNegLog2e);

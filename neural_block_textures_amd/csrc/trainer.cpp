@@ -221,6 +221,7 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
             if (d.lv[l].off != off) { why = "latent levels must be concatenated in order"; return false; }
             off += (size_t)d.lv[l].W * d.lv[l].H * d.lv[l].C;
         }
+        if (off >= ((size_t)1 << 30)) { why = "latents of at most 2^30 values (32-bit element offsets)"; return false; }
     }
     for (int l = 0; l < d.nhidden; l++) if (d.hidden[l] < 1) { why = "empty hidden layer"; return false; }
     I.qes = false;

@@ -205,8 +205,11 @@ def test_qat_search_and_frozen_level(orc, name):
     g = tr.debug_last_zgrad()
     assert not g[:n0].any()
     mask = ((1 << len(lay.levels)) - 1) & ~1
-    g_o, _, _, _ = orc.lat_grad(lay, p, z, z, tgt, 5, 0, 0.05, 2, mask)
+    g_o, dpix_o, _, _ = orc.lat_grad(lay, p, z, z, tgt, 5, 0, 0.05, 2, mask, want_dpix=True)
     assert np.abs(g - g_o).max() < 1e-3 * np.sqrt((g_o.astype(np.float64) ** 2).mean())
+    # the per-pixel differences with level 0 outside the perturbation mask (its texels taken unperturbed)
+    dpix = tr.debug_last_dpix()
+    assert np.abs(dpix.ravel() - dpix_o).max() < 1e-3 * np.sqrt((dpix_o.astype(np.float64) ** 2).mean())
     tr.qat_search()
     zg = tr.download_model()[0]
     zc = z.copy()
