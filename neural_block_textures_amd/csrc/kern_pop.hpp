@@ -136,6 +136,29 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
     const int pair = bid_x(), ch = bid_y(), sgn = wave & 1, half = wave >> 1;
     const int i16 = lane & 15, g = lane >> 4;
+    constexpr int NT = pop_nt<S>();
+    constexpr bool kOwn = pop_own<S>();
+    constexpr bool kVOut = valu_out<S>();
+    // lane byte offsets of the feature rows 4 ks + g (rows past nin are the array's zero rows) and target
+    // rows 4 g + r, or g (rows past the last one are clamped to it: their channel weights cw are zero); the
+    // pixel-per-lane layer: target row r of pixel i16 of tile g
+    uint32_t fo[Q::kKs1], to[NT];
+#pragma unroll
+    for (int ks = 0; ks < Q::kKs1; ks++) fo[ks] = 4u * ((uint32_t)(4 * ks + g) * (uint32_t)Mcap + (uint32_t)i16);
+#pragma unroll
+    for (int r = 0; r < NT; r++)
+        to[r] = kOwn ? 4u * ((uint32_t)r * (uint32_t)Mcap + 32u * (uint32_t)g + (uint32_t)i16)
+                     : 4u * ((uint32_t)min(kVOut ? g : 4 * g + r, Q::kNout - 1) * (uint32_t)Mcap + (uint32_t)i16);
+    const int s0 = ch * chunk, s1 = min(M, s0 + chunk);
+    const int tiles = (s1 - s0 + 15) >> 4;
+    const int mine = (tiles - half + 1) >> 1;   // this wave's tiles: 2 j + half, j < mine
+    static_assert(minibatch_rows(Q::kIn) == 4 * Q::kKs1, "the feature rows the first layer's k-steps read");
+    const __amdgpu_buffer_rsrc_t rf = buffer_of(feat, 4u * ((uint32_t)minibatch_rows(Q::kIn) * (uint32_t)Mcap + (uint32_t)kMinibatchSlack));
+    const __amdgpu_buffer_rsrc_t rt = buffer_of(btgt, 4u * ((uint32_t)Q::kNout * (uint32_t)Mcap + (uint32_t)kMinibatchSlack));
+    constexpr int U = pop_u<S>();
+    // the first tiles' inputs load while the member's weights are staged
+    PopTileIn<S> in0, in1;
+    pop_load<S>(in0, rf, rt, 4u * (uint32_t)(s0 + 16 * half), fo, to);
     MfmaWeights<S> W;
     if constexpr (Es) {
         const uint64_t head = noise_head(src.seed, NS_MLP, src.step, (uint32_t)pair);
@@ -160,9 +183,6 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
     const float ak = act_k(Act, m.leak);
-    constexpr bool kVOut = valu_out<S>();
-    constexpr int NT = pop_nt<S>();
-    constexpr bool kOwn = pop_own<S>();
     // the channel weight of each of this lane's outputs (pixel-per-lane layer: output r; D layout: rows
     // 4 g + r; VALU output layer: output g), zero past the last output
     float cw[NT];
@@ -173,24 +193,7 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
         for (int c = 0; c < Q::kNout; c++)
             if ((kOwn ? r : (kVOut ? g : 4 * g + r)) == c) cw[r] = m.cw[c];
     }
-    // lane byte offsets of the feature rows 4 ks + g (rows past nin are the array's zero rows) and target
-    // rows 4 g + r, or g (rows past the last one are clamped to it: their channel weights cw are zero); the
-    // pixel-per-lane layer: target row r of pixel i16 of tile g
-    uint32_t fo[Q::kKs1], to[NT];
-#pragma unroll
-    for (int ks = 0; ks < Q::kKs1; ks++) fo[ks] = 4u * ((uint32_t)(4 * ks + g) * (uint32_t)Mcap + (uint32_t)i16);
-#pragma unroll
-    for (int r = 0; r < NT; r++)
-        to[r] = kOwn ? 4u * ((uint32_t)r * (uint32_t)Mcap + 32u * (uint32_t)g + (uint32_t)i16)
-                     : 4u * ((uint32_t)min(kVOut ? g : 4 * g + r, Q::kNout - 1) * (uint32_t)Mcap + (uint32_t)i16);
-    const int s0 = ch * chunk, s1 = min(M, s0 + chunk);
-    const int tiles = (s1 - s0 + 15) >> 4;
-    const int mine = (tiles - half + 1) >> 1;   // this wave's tiles: 2 j + half, j < mine
     double e = 0.0;
-    static_assert(minibatch_rows(Q::kIn) == 4 * Q::kKs1, "the feature rows the first layer's k-steps read");
-    const __amdgpu_buffer_rsrc_t rf = buffer_of(feat, 4u * ((uint32_t)minibatch_rows(Q::kIn) * (uint32_t)Mcap + (uint32_t)kMinibatchSlack));
-    const __amdgpu_buffer_rsrc_t rt = buffer_of(btgt, 4u * ((uint32_t)Q::kNout * (uint32_t)Mcap + (uint32_t)kMinibatchSlack));
-    constexpr int U = pop_u<S>();
     // One pass: tiles j .. j + U - 1 from c, while tiles j + U .. load into n. The loop alternates
     // two input sets, so no registers are copied between passes. The loads are issued on every pass
     // (the last one reloads its own tiles) so that the wait for them falls in the next pass.
@@ -256,8 +259,6 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
             }
         }
     };
-    PopTileIn<S> in0, in1;
-    pop_load<S>(in0, rf, rt, 4u * (uint32_t)(s0 + 16 * half), fo, to);
     // this wave's tiles that lie wholly inside the chunk (tile t: slots s0 + 16 (2 t + half) + 0 .. 15)
     const int nwhole = min(mine, max(0, (s1 - s0 - 16 * half + 16) >> 5));
     int j = 0;
