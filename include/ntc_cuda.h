@@ -15,6 +15,8 @@
 #include <string>
 #include <vector>
 
+struct ntc_print_stats;   // the progress line's figures (include/ntc_hip.h)
+
 namespace ntc_cuda {
 
 // Envelope (cuda/ntc_cuda.h:14-20)
@@ -116,6 +118,9 @@ public:
     void decode_error(const float* z_host, int ew, int eh, double* tex_mse, double* weighted);
     // The decode rounded to 8 bits as save_png writes it: W * H * nout bytes.
     void decode_rgb8(uint8_t* out);
+    // The figures of a progress line on the device (bitrate_stats at --qbits qbits, the error of its quantized
+    // latent over ew x eh, latent_stats, dct_analyze; main.cpp:4155-4212), without downloading the model.
+    void print_stats(int qbits, int ew, int eh, ::ntc_print_stats* out);
 
     struct Impl;
     Impl* im;

@@ -608,6 +608,9 @@ void Trainer::decode_error(const float* z_host, int ew, int eh, double* tex_mse,
     ntc_hip::decode_error_impl(*im, z_host, ew, eh, tex_mse, weighted);
 }
 void Trainer::decode_rgb8(uint8_t* out) { ntc_hip::decode_rgb8_impl(*im, out); }
+void Trainer::print_stats(int qbits, int ew, int eh, ::ntc_print_stats* out) {
+    ntc_hip::print_stats_impl(*im, qbits, ew, eh, out);
+}
 
 void Trainer::debug_last_batch(std::vector<int>& bidx) const {
     Impl& I = *im;
