@@ -301,21 +301,21 @@ constexpr int lat_rounds() { return lat_rounds_of(MfmaShape<S>::kIn); }
 // unperturbed), and each member's blend is the single-member blend - so fp and fm equal features<S> with
 // PerturbedLatent{ z, eps, sg, mask } and { z, eps, -sg, mask }. Texels are read through raw buffers with
 // 32-bit byte offsets (a latent holds fewer than 2^30 floats). The code has no branch per texel: a level
-// outside `mask` takes its Gaussians too, scaled by 0 (fma(0, eps, zb) = zb for the finite Gaussians, up to
-// the sign of a zero texel, which no output can see: the layers' sums and the activation treat +0 and -0
-// alike). A branch per texel (or stores under a branch) makes the compiler keep the features in scratch.
+// outside `mask` reads its Gaussians through an empty buffer (rn: every load returns 0 without touching
+// memory), so fma(+-sg, 0, zb) = zb, up to the sign of a zero texel, which no output can see (the layers'
+// sums and the activation treat +0 and -0 alike). A branch per texel (or stores under a branch) makes the
+// compiler keep the features in scratch.
 template <int C>
-__device__ __forceinline__ void sample_level_pm(const DevLevel& L, bool pert, __amdgpu_buffer_rsrc_t rz, __amdgpu_buffer_rsrc_t re,
+__device__ __forceinline__ void sample_level_pm(const DevLevel& L, __amdgpu_buffer_rsrc_t rz, __amdgpu_buffer_rsrc_t re,
                                                 float sg, const Tap& t, float* fp, float* fm) {
     const uint32_t off = (uint32_t)L.off, LW = (uint32_t)L.W, LC = (uint32_t)L.C;
-    const float sp = pert ? sg : 0.0f;
     const uint32_t a = 4u * (off + ((uint32_t)t.y0 * LW + (uint32_t)t.x0) * LC);
     if (L.nearest) {
 #pragma unroll
         for (int c = 0; c < C; c++) {
             const float zb = buffer_f32(rz, a + 4u * c, 0u), ee = buffer_f32(re, a + 4u * c, 0u);
-            fp[c] = __builtin_fmaf(sp, ee, zb);
-            fm[c] = __builtin_fmaf(-sp, ee, zb);
+            fp[c] = __builtin_fmaf(sg, ee, zb);
+            fm[c] = __builtin_fmaf(-sg, ee, zb);
         }
         return;
     }
@@ -329,8 +329,8 @@ __device__ __forceinline__ void sample_level_pm(const DevLevel& L, bool pert, __
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const float zb = buffer_f32(rz, tap[q] + 4u * c, 0u), ee = buffer_f32(re, tap[q] + 4u * c, 0u);
-            vp[q] = __builtin_fmaf(sp, ee, zb);
-            vm[q] = __builtin_fmaf(-sp, ee, zb);
+            vp[q] = __builtin_fmaf(sg, ee, zb);
+            vm[q] = __builtin_fmaf(-sg, ee, zb);
         }
         fp[c] = blend(w, vp[0], vp[1], vp[2], vp[3]);
         fm[c] = blend(w, vm[0], vm[1], vm[2], vm[3]);
@@ -338,20 +338,21 @@ __device__ __forceinline__ void sample_level_pm(const DevLevel& L, bool pert, __
 }
 
 template <class S>
-__device__ __forceinline__ void features_pm(const DevModel& m, __amdgpu_buffer_rsrc_t rz, __amdgpu_buffer_rsrc_t re, float sg, unsigned mask,
+__device__ __forceinline__ void features_pm(const DevModel& m, __amdgpu_buffer_rsrc_t rz, __amdgpu_buffer_rsrc_t re, __amdgpu_buffer_rsrc_t rn,
+                                            float sg, unsigned mask,
                                             int px, int py, float (&fp)[S::kMaxIn], float (&fm)[S::kMaxIn]) {
     static_assert(S::kFixed, "fixed shapes only");
     const float u = pixel_u(px, m.W), v = pixel_u(py, m.H);
     const Tap t0 = tap_of(m.lv[0].W, m.lv[0].H, m.lv[0].nearest != 0, u, v);
     Tap t1 = t0;
-    sample_level_pm<S::kC0>(m.lv[0], mask & 1u, rz, re, sg, t0, fp, fm);
+    sample_level_pm<S::kC0>(m.lv[0], rz, (mask & 1u) ? re : rn, sg, t0, fp, fm);
     if constexpr (S::kC1 > 0) {
         t1 = tap_of(m.lv[1].W, m.lv[1].H, m.lv[1].nearest != 0, u, v);
-        sample_level_pm<S::kC1>(m.lv[1], (mask >> 1) & 1u, rz, re, sg, t1, fp + S::kC0, fm + S::kC0);
+        sample_level_pm<S::kC1>(m.lv[1], rz, ((mask >> 1) & 1u) ? re : rn, sg, t1, fp + S::kC0, fm + S::kC0);
     }
     if constexpr (S::kC2 > 0) {
         const Tap t2 = tap_of(m.lv[2].W, m.lv[2].H, m.lv[2].nearest != 0, u, v);
-        sample_level_pm<S::kC2>(m.lv[2], (mask >> 2) & 1u, rz, re, sg, t2, fp + S::kC0 + S::kC1, fm + S::kC0 + S::kC1);
+        sample_level_pm<S::kC2>(m.lv[2], rz, ((mask >> 2) & 1u) ? re : rn, sg, t2, fp + S::kC0 + S::kC1, fm + S::kC0 + S::kC1);
     }
     constexpr int k0 = S::kC0 + S::kC1 + S::kC2;
 #pragma unroll
@@ -388,7 +389,8 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     constexpr bool kVOut = valu_out<S>();
     const int k = bid_y();
     const int lane = tid_x() & 63, wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6), i16 = lane & 15, g = lane >> 4;
-    const __amdgpu_buffer_rsrc_t rz = buffer_of(zdec, 4u * (uint32_t)m.nz), re = buffer_of(eps + (size_t)k * m.nz, 4u * (uint32_t)m.nz);
+    const __amdgpu_buffer_rsrc_t rz = buffer_of(zdec, 4u * (uint32_t)m.nz), re = buffer_of(eps + (size_t)k * m.nz, 4u * (uint32_t)m.nz),
+                                 rn = buffer_of(eps, 0u);   // a level outside the mask: no Gaussians (every load 0)
     float* out = dpix + (size_t)k * m.npix;
     MfmaWeights<S> W;
     mfma_load<S, false>(W, w, lane);
@@ -430,7 +432,7 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
             int px, py;
             round_pixel(m, base, lane, px, py);
             float fp[S::kMaxIn], fm[S::kMaxIn];
-            features_pm<S>(m, rz, re, sg, mask, px, py, fp, fm);
+            features_pm<S>(m, rz, re, rn, sg, mask, px, py, fp, fm);
             tiles_of<S>(fp, bp);
             tiles_of<S>(fm, bm);
         }
