@@ -428,6 +428,8 @@ def main():
                     help="time REPS device draws of one ES step's N x P Gaussians of the workload (what a regenerating update redraws)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="FLOATS",
                     help="only run a plain device copy of FLOATS floats three times (the reference for memory counters)")
+    ap.add_argument("--mlp-batch", type=int, default=0, metavar="M",
+                    help="analysis only: the workload with an M-slot minibatch instead of its own (the line's config records it)")
     args = ap.parse_args()
     MATRIX_CORES[0] = not args.valu
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -460,6 +462,8 @@ def main():
         return
 
     w = workloads()[args.workload]
+    if args.mlp_batch:
+        w.mlp_batch = args.mlp_batch
     lay = w.layout
     log(f"bench: {w.name} {lay.W}x{lay.H}x{lay.T} levels {lay.levels} mlp {lay.nin}->{lay.hidden}->{lay.nout} "
         f"pairs {w.mlp_pairs} batch {w.mlp_batch}")
