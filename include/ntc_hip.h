@@ -191,6 +191,10 @@ int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage);
  * kernels' parity and speed are then measured against them); on = 1 (the default): the matrix cores
  * take every stage whose shape they pay off for */
 void ntc_trainer_set_matrix_cores(ntc_trainer* t, int on);
+/* pairs > 0: every latent step of this trainer runs its pairs in groups of at most `pairs` (the Gaussians and
+ * per-pixel differences of one group at a time; the results are the same bit for bit); 0 (the default): groups
+ * as large as 1 GiB of those buffers holds. ntc_trainer_debug_last_dpix then returns the last group's pairs. */
+void ntc_trainer_set_lat_group(ntc_trainer* t, int pairs);
 /* Compiles, with hipRTC and without loading it (no device needed), the kernel set that a trainer
  * specialises at init for a model whose shape the library does not list (its hidden layers all one
  * width); arch e.g. "gfx950". Returns 1, or 0 with the compiler's log in why. seconds: the compile time. */

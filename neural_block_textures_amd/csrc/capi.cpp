@@ -197,6 +197,7 @@ int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage) {
 }
 
 void ntc_trainer_set_matrix_cores(ntc_trainer* t, int on) { t->t.im->valu_only = on == 0; }
+void ntc_trainer_set_lat_group(ntc_trainer* t, int pairs) { t->t.im->lat_group = pairs > 0 ? pairs : 0; }
 
 int ntc_jit_compile_check(const ntc_model_desc* d, const char* arch, double* seconds, char* why, size_t why_cap) {
     ntc_hip::DevModel m{};

@@ -19,17 +19,17 @@ __device__ __forceinline__ int level_of(const DevModel& m, long long i) {
     return l;
 }
 
-// eps[k][i] = gauss(seed, NS_LAT, step, k, i) for the ES-perturbed levels (the other levels' entries are
-// never read and are left as they are); the pair-0 threads also clear the latent gradient. Grid: latent
-// entries x pairs (blockIdx.y = pair k).
-__global__ void __launch_bounds__(kTPB) k_lat_eps(NoiseFix nt, DevModel m, uint64_t seed, uint32_t step, unsigned mask,
+// eps[k][i] = gauss(seed, NS_LAT, step, k0 + k, i) for the ES-perturbed levels (the other levels' entries are
+// never read and are left as they are): the group of pairs k0 .. k0 + gridDim.y - 1 of a latent step; the
+// first group's pair-0 threads also clear the latent gradient. Grid: latent entries x pairs (blockIdx.y = k).
+__global__ void __launch_bounds__(kTPB) k_lat_eps(NoiseFix nt, DevModel m, uint64_t seed, uint32_t step, unsigned mask, int k0,
                                                  float* __restrict__ eps, float* __restrict__ zgrad) {
     const long long i = (long long)blockIdx.x * kTPB + threadIdx.x;
     if (i >= m.nz) return;
     const int k = blockIdx.y;
-    if (k == 0) zgrad[i] = 0.0f;
+    if (k0 + k == 0) zgrad[i] = 0.0f;
     const int l = level_of(m, i);
-    if ((mask >> l) & 1u) eps[(size_t)k * m.nz + i] = gauss_at(nt, noise_head(seed, NS_LAT, step, (uint32_t)k), (uint64_t)i);
+    if ((mask >> l) & 1u) eps[(size_t)k * m.nz + i] = gauss_at(nt, noise_head(seed, NS_LAT, step, (uint32_t)(k0 + k)), (uint64_t)i);
 }
 
 // Footprint gather for one level (the gather form of the reference's raster-order scatter,
@@ -128,10 +128,10 @@ __global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevMod
 }
 
 // ---------------------------------------------------------------- launchers
-void launch_lat_eps(Impl& I, int K, unsigned mask) {
+void launch_lat_eps(Impl& I, int k0, int K, unsigned mask) {
     ProfScope ps(I, "lat_eps");
     hipLaunchKernelGGL(k_lat_eps, dim3(blocks_for(I.nz, kTPB), K), dim3(kTPB), 0, I.stream, I.noise, I.dm, I.d.seed,
-                       (uint32_t)I.lat_step_no, mask, I.eps_lat, I.zgrad);
+                       (uint32_t)I.lat_step_no, mask, k0, I.eps_lat, I.zgrad);
     NTC_CHECK(hipGetLastError());
 }
 
@@ -147,13 +147,14 @@ void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask) {
     NTC_CHECK(hipGetLastError());
 }
 
-void launch_lat_gather(Impl& I, int level, int K, float scale, bool rate, float lr, int t) {
+void launch_lat_gather(Impl& I, int level, int k0, int K, float scale, bool rate, float lr, int t) {
     const size_t ntx = (size_t)I.d.lv[level].W * I.d.lv[level].H;
     const float c1 = t > 0 ? 1.0f - powf(0.9f, (float)t) : 1.0f, c2 = t > 0 ? 1.0f - powf(0.999f, (float)t) : 1.0f;
     ProfScope ps(I, "lat_gather");
     hipLaunchKernelGGL(k_lat_gather, dim3(blocks_for(ntx, kGatherTex)), dim3(kGatherTex * kGatherPairs), 0, I.stream, I.dm, level, K,
                        scale, I.dpix, I.eps_lat,
-                       I.ranges, rate ? 1 : 0, I.ddct.rate_scale, I.ddct.BW, I.ddct.n, I.dct_dbits, I.zgrad, t > 0 ? 1 : 0, I.z, I.zm,
+                       I.ranges, rate ? 1 : 0, I.ddct.rate_scale, I.ddct.BW, I.ddct.n, rate ? I.dct_dbits + (size_t)k0 * I.ddct.n : nullptr,
+                       I.zgrad, t > 0 ? 1 : 0, I.z, I.zm,
                        I.zv, lr, c1, c2);
     NTC_CHECK(hipGetLastError());
 }

@@ -296,10 +296,10 @@ void launch_dct_recon(Impl& I) {
                        I.dct_code, I.dct_step, I.zq, I.dct_bits);
     NTC_CHECK(hipGetLastError());
 }
-void launch_dct_rate_pairs(Impl& I, int K, float sigma) {
+void launch_dct_rate_pairs(Impl& I, int k0, int K, float sigma) {
     ProfScope ps(I, "dct_rate");
     hipLaunchKernelGGL(k_dct_rate_pair, dim3(blocks_for(I.ddct.n, kDctWaves), K), dim3(64 * kDctWaves), 0, I.stream, I.ddct, I.dm.lv[0],
-                       (long long)I.nz, sigma, I.z, I.eps_lat, I.dct_code, I.dct_step, I.dct_dbits);
+                       (long long)I.nz, sigma, I.z, I.eps_lat, I.dct_code, I.dct_step, I.dct_dbits + (size_t)k0 * I.ddct.n);
     NTC_CHECK(hipGetLastError());
 }
 void launch_shadow_pull(Impl& I, size_t off, size_t n, float f) {

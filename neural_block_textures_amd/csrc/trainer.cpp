@@ -74,13 +74,27 @@ void ensure_wsets(Impl& I, size_t need) {
     dev_alloc(&I.wsets, need);
 }
 
-void ensure_lat(Impl& I, int K) {
-    if (K <= I.Kcap) return;
-    dev_free(I.eps_lat); dev_free(I.dpix); dev_free(I.dct_dbits);
-    I.Kcap = K;
-    dev_alloc(&I.eps_lat, (size_t)K * I.nz);
-    dev_alloc(&I.dpix, (size_t)K * I.npix);
-    if (I.dct) dev_alloc(&I.dct_dbits, (size_t)K * I.ddct.n);
+// A latent step's pairs run in groups of at most G pairs (its Gaussians and per-pixel differences, G x (nz + W H)
+// floats, within kLatGroupBytes unless a group size is set): the memory of a step no longer grows with K. The
+// DCT rate pass's bit differences (K x n, n = level 0's texels / 64) are kept for every pair.
+constexpr size_t kLatGroupBytes = (size_t)1 << 30;
+int lat_group_of(const Impl& I, int K) {
+    int G = I.lat_group;
+    if (G <= 0) G = (int)std::min<size_t>(65535, std::max<size_t>(1, kLatGroupBytes / (sizeof(float) * ((size_t)I.nz + I.npix))));
+    return std::min(std::min(G, 65535), K);
+}
+void ensure_lat(Impl& I, int G, int K) {
+    if (G > I.Kcap) {
+        dev_free(I.eps_lat); dev_free(I.dpix);
+        I.Kcap = G;
+        dev_alloc(&I.eps_lat, (size_t)G * I.nz);
+        dev_alloc(&I.dpix, (size_t)G * I.npix);
+    }
+    if (I.dct && K > I.Dcap) {
+        dev_free(I.dct_dbits);
+        I.Dcap = K;
+        dev_alloc(&I.dct_dbits, (size_t)K * I.ddct.n);
+    }
 }
 
 void sync(Impl& I) { NTC_CHECK(hipStreamSynchronize(I.stream)); }
@@ -553,26 +567,35 @@ void Trainer::mlp_stats(double& batch_loss, double& diff_std) {
 
 void Trainer::lat_step(int /*it*/, float sigma, float lr, int K) {
     Impl& I = *im;
-    if (K < 1 || K > 65535) die("lat_step takes 1 to 65535 pairs");
+    if (K < 1) die("lat_step takes at least one pair");
     const bool qat = I.d.qat > 0;
     unsigned mask = 0;
     for (int l = 0; l < I.d.nlev; l++) if (!(qat && l == 0)) mask |= 1u << l;
-    ensure_lat(I, K);
+    const int G = lat_group_of(I, K);
+    ensure_lat(I, G, K);
     const bool rate = I.dct_live && I.dct_rate_es;
     I.dct_evals = rate ? I.ddct.n * K : 0;
     if (!mask) launch_fill(I, I.zgrad, I.nz, 0.0f);
     if (mask) {
-        launch_lat_eps(I, K, mask);   // also clears zgrad
-        launch_lat_pair(I, K, sigma, mask);
-        I.lat_last_K = K;
-        if (rate) { launch_dct_rate_pairs(I, K, sigma); I.dct_last_K = K; }
         const float scale = 1.0f / (2.0f * (float)K * sigma);
-        // Adam on the perturbed levels inside their gathers. The other levels' gradients are zero at
-        // every step of this trainer (the mask is fixed by --qat at init), so their Adam moments stay
-        // zero and the reference's step leaves them exactly as they are: it is skipped.
         ++I.lat_t;
-        for (int l = 0; l < I.d.nlev; l++)
-            if ((mask >> l) & 1u) launch_lat_gather(I, l, K, scale, rate && l == 0, lr, I.lat_t);
+        // The pairs in groups, in order: each group's gathers add its pairs to every texel's gradient after the
+        // previous groups' (the reference's pair order, main.cpp:1990-2037: the same sums, bit for bit), and the
+        // shadow and decode buffer stay as they are until the last group. Adam on the perturbed levels inside the
+        // last group's gathers. The other levels' gradients are zero at every step of this trainer (the mask is
+        // fixed by --qat at init), so their Adam moments stay zero and the reference's step leaves them exactly
+        // as they are: it is skipped.
+        for (int k0 = 0; k0 < K; k0 += G) {
+            const int g = std::min(G, K - k0);
+            const bool last = k0 + g == K;
+            launch_lat_eps(I, k0, g, mask);   // the first group also clears zgrad
+            launch_lat_pair(I, g, sigma, mask);
+            I.lat_last_K = g;
+            if (rate) launch_dct_rate_pairs(I, k0, g, sigma);
+            for (int l = 0; l < I.d.nlev; l++)
+                if ((mask >> l) & 1u) launch_lat_gather(I, l, k0, g, scale, rate && l == 0, lr, last ? I.lat_t : 0);
+        }
+        if (rate) I.dct_last_K = K;
     } else {
         launch_adam(I, I.z, I.zgrad, I.zm, I.zv, I.nz, lr, ++I.lat_t);
     }

@@ -77,8 +77,10 @@ struct ntc_cuda::Trainer::Impl {
     double *part = nullptr, *dl = nullptr, *lsum = nullptr, *hh = nullptr;
     size_t part_cap = 0;
     int pairs_cap = 0;
-    float *eps_lat = nullptr, *dpix = nullptr;
+    float *eps_lat = nullptr, *dpix = nullptr;   // one group of pairs of a latent step: Kcap x nz, Kcap x W*H
     int Kcap = 0;
+    int lat_group = 0;         // pairs per latent group (0: as many as kLatGroupBytes of eps_lat + dpix hold)
+    int Dcap = 0;              // pairs dct_dbits holds
     int* ranges = nullptr;     // per level: xb[W] xe[W] yb[H] ye[H] (pixel footprint of each texel row / column)
     float* qat_grid = nullptr; // 9 x 257
     int* qat_bits = nullptr;   // MAX_CH
@@ -95,12 +97,12 @@ struct ntc_cuda::Trainer::Impl {
     int16_t* dct_sym = nullptr;
     uint8_t* dct_code = nullptr;
     int* dct_step = nullptr;
-    int32_t *dct_bits = nullptr, *dct_dbits = nullptr;   // dbits: Kcap x n (pair k's bit differences)
+    int32_t *dct_bits = nullptr, *dct_dbits = nullptr;   // dbits: K x n (pair k's bit differences), every pair of the step
     int* dct_tn = nullptr;     // per (block, channel) of the last snap: truncated ACs [n], then nonzero ACs before truncation [n]
     uint8_t* dct_probe_code = nullptr;   // the device probe's codes (n)
     float* dct_gain = nullptr;           // and block gains (n)
     int dct_evals = 0, dct_last_K = 0;
-    int lat_last_K = 0;            // pairs of the last latent ES step (the K x W*H rows of dpix it wrote)
+    int lat_last_K = 0;            // pairs of the last latent group (the rows of dpix it wrote: the step's last pairs)
 
     // print_stats (kernels_stats.hip): the quantized latent, the histograms and partial sums (grown on first use),
     // and the host's copy of the last histograms (ntc_trainer_debug_print_counts)
@@ -183,11 +185,13 @@ void launch_debug_factors(Impl& I, uint32_t k0, size_t n, float* rad, float* cos
 void launch_copy_calibration(Impl& I, const float* src, float* dst, size_t n);
 
 // kernels_latent.hip
-void launch_lat_eps(Impl& I, int K, unsigned mask);   // also clears the latent gradient
+// the Gaussians of pairs k0 .. k0 + K - 1 (rows 0 .. K - 1 of eps_lat); with k0 = 0 also clears the latent gradient
+void launch_lat_eps(Impl& I, int k0, int K, unsigned mask);
 void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask);
 void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask);
-// the footprint gather of one level; with t > 0 also the Adam step t (learning rate lr) of its texels
-void launch_lat_gather(Impl& I, int level, int K, float scale, bool rate, float lr = 0.0f, int t = 0);
+// the footprint gather of one level for the group of pairs k0 .. k0 + K - 1 (added to the gradient so far); with
+// t > 0 (the step's last group) also the Adam step t (learning rate lr) of its texels
+void launch_lat_gather(Impl& I, int level, int k0, int K, float scale, bool rate, float lr = 0.0f, int t = 0);
 void launch_qat_search(Impl& I);
 
 // kernels_quant.hip
@@ -213,7 +217,8 @@ void decode_error_noalloc_impl(Impl& I, const float* z_host, int ew, int eh, dou
 void print_stats_impl(Impl& I, int qbits, int ew, int eh, ntc_print_stats* out);
 void dct_probe_impl(Impl& I, uint8_t* code, float* gain);
 void dct_refit_impl(Impl& I, uint8_t* code);
-void launch_dct_rate_pairs(Impl& I, int K, float sigma);
+// the rate pass of pairs k0 .. k0 + K - 1 (Gaussians in rows 0 .. K - 1 of eps_lat; bit differences in rows k0 ..)
+void launch_dct_rate_pairs(Impl& I, int k0, int K, float sigma);
 void launch_shadow_pull(Impl& I, size_t off, size_t n, float f);
 
 }   // namespace ntc_hip

@@ -119,6 +119,7 @@ def library() -> C.CDLL:
             "ntc_trainer_kernel_time": (C.c_int, [P, C.c_char_p, P, P]),
             "ntc_trainer_on_matrix_cores": (C.c_int, [P, C.c_char_p]),
             "ntc_trainer_set_matrix_cores": (None, [P, C.c_int]),
+            "ntc_trainer_set_lat_group": (None, [P, C.c_int]),
             "ntc_jit_compile_check": (C.c_int, [C.POINTER(ModelDesc), C.c_char_p, C.POINTER(C.c_double), C.c_char_p, C.c_size_t]),
             "ntc_trainer_dct_probe": (None, [P, P, P]),
             "ntc_trainer_dct_refit": (None, [P, P]),
@@ -474,6 +475,10 @@ class Trainer:
     def set_matrix_cores(self, on: bool):
         """on=False: every stage on the VALU kernels from the next call on (instrumentation)"""
         self._lib.ntc_trainer_set_matrix_cores(self._h, 1 if on else 0)
+
+    def set_lat_group(self, pairs: int):
+        """latent steps in groups of at most `pairs` pairs (0: by the 1 GiB buffer budget); the same results"""
+        self._lib.ntc_trainer_set_lat_group(self._h, int(pairs))
 
     @staticmethod
     def jit_compile_check(d: ModelDesc, arch: str = "gfx950"):
