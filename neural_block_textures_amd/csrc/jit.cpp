@@ -92,7 +92,7 @@ std::vector<std::string> expressions(const std::string& shape, const DevModel& m
         v.push_back(e("k_pop_mfma", std::to_string(a_es) + ", " + c + ", 2"));
         v.push_back(e("k_lat_pair_mfma", std::to_string(a_es) + ", " + c));
     }
-    v.push_back(e("k_qat_mfma", std::to_string(unit ? kActFold : kActAny)));
+    v.push_back(e("k_qat_mfma", std::to_string(unit ? kActFold : kActAny) + ", " + c));
     return v;
 }
 

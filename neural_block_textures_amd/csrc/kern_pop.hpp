@@ -488,7 +488,7 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
 // activation of act<Act>: the reference adds the float terms in double with its own activation, so a
 // choice can differ from the reference's only between candidates whose losses agree to a few float
 // roundings (the reference's own check accepts such rounding ties, main.cpp:3143-3144).
-template <class S, int Act>
+template <class S, int Act, bool Clamp>
 __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __restrict__ w, float* __restrict__ zdec,
                                                  const float* __restrict__ tgt, const int* __restrict__ qat_bits,
                                                  const float* __restrict__ grid) {
@@ -497,7 +497,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
     const int lane = tid_x() & 63, wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6), i16 = lane & 15, g = lane >> 4;
     MfmaWeights<S> W;
     mfma_load<S, false>(W, w, lane);
-    if (!m.clamp_out) scale_output<S>(W, kNegLog2e);
+    if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
     const float ak = act_k(Act, m.leak);
     constexpr bool kVOut = valu_out<S>();   // the output layer on the VALU: output g of pixel j in lane (g, j)
@@ -547,7 +547,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                     mfma_hidden<S, 2, Act, false>(W, b2, ak, x);
 #pragma unroll
                     for (int v = 0; v < 2; v++) {
-                        const float d = out_of<S>(valu_out_g<S>(W, x[v]), m.clamp_out != 0) - t4[t][0];
+                        const float d = out_of<S>(valu_out_g<S>(W, x[v]), Clamp) - t4[t][0];
                         lv[v] = __fmul_rn(cw[0], __fmul_rn(d, d));   // cw (d d), main.cpp:2119
                     }
                 } else {
@@ -558,7 +558,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                         lv[v] = 0.0f;
 #pragma unroll
                         for (int r = 0; r < 4; r++) {
-                            const float d = out_of<S>(o[v][r], m.clamp_out != 0) - t4[t][r];
+                            const float d = out_of<S>(o[v][r], Clamp) - t4[t][r];
                             lv[v] = __builtin_fmaf(cw[r], __fmul_rn(d, d), lv[v]);
                         }
                     }

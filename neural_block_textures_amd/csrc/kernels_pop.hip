@@ -159,7 +159,8 @@ void launch_qat_mfma(Impl& I) {
     if (I.jit) {
         const float leak = I.dm.leak;
         const int act = leak >= 0.0f && leak <= 1.0f ? kActFold : kActAny;
-        jit_launch(k_qat_mfma<ShapeMaterial, kActFold>, I, "k_qat_mfma", std::to_string(act), dim3((unsigned)((I.npix + 255) / 256)),
+        jit_launch(k_qat_mfma<ShapeMaterial, kActFold, false>, I, "k_qat_mfma", std::to_string(act) + (I.dm.clamp_out ? ", true" : ", false"),
+                   dim3((unsigned)((I.npix + 255) / 256)),
                    dim3(256), 0, I.dm, I.w, I.zdec, I.tgt, I.qat_bits, I.qat_grid);
         NTC_CHECK(hipGetLastError());
         return;
@@ -169,7 +170,9 @@ void launch_qat_mfma(Impl& I) {
         if constexpr (MfmaShape<S>::kOk)
         {
             const float leak = I.dm.leak;
-            auto kern = leak >= 0.0f && leak <= 1.0f ? k_qat_mfma<S, kActFold> : k_qat_mfma<S, kActAny>;
+            const bool fold = leak >= 0.0f && leak <= 1.0f;
+            auto kern = I.dm.clamp_out ? (fold ? k_qat_mfma<S, kActFold, true> : k_qat_mfma<S, kActAny, true>)
+                                       : (fold ? k_qat_mfma<S, kActFold, false> : k_qat_mfma<S, kActAny, false>);
             hipLaunchKernelGGL(kern, dim3((unsigned)((I.npix + 255) / 256)), dim3(256), 0, I.stream, I.dm, I.w, I.zdec, I.tgt,
                                I.qat_bits, I.qat_grid);
         }

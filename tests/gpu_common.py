@@ -46,6 +46,9 @@ for _name in ("material", "chief1_36"):
     _lay = Layout(**{k: getattr(LAYOUTS[_name], k) for k in LAYOUTS[_name].__dataclass_fields__})
     _lay.valu_only = True
     LAYOUTS[_name + "_valu"] = _lay
+# the material layout with --clamp outputs (the matrix-core kernels' clamped instances)
+LAYOUTS["material_clamp"] = Layout(**{k: getattr(LAYOUTS["material"], k) for k in LAYOUTS["material"].__dataclass_fields__})
+LAYOUTS["material_clamp"].clamp_out = True
 # "runtime" (hidden widths 20, 12) on the runtime-shaped kernels, and the same model on the kernels
 # specialised at init for its widths (FixedShapeW)
 LAYOUTS["jit_widths"] = Layout(**{k: getattr(LAYOUTS["runtime"], k) for k in LAYOUTS["runtime"].__dataclass_fields__})

@@ -182,7 +182,7 @@ def test_latent_step(orc, name):
     assert np.abs(tr.debug_last_zgrad() - g2_o).max() < 1e-3 * np.sqrt((g2_o.astype(np.float64) ** 2).mean())
 
 
-QAT = {"material": [2, 3], "dct_plane": [1], "runtime": [2, 1, 3], "chief1_36": [2], "mat_qat_36": [2, 2], "image3_27": [4],
+QAT = {"material": [2, 3], "material_clamp": [2, 3], "dct_plane": [1], "runtime": [2, 1, 3], "chief1_36": [2], "mat_qat_36": [2, 2], "image3_27": [4],
        "material_valu": [2, 3], "chief1_36_valu": [2], "mat_qat1x4_36": [2], "jit_mfma_28": [2, 1], "jit_widths": [2, 1, 3]}
 
 
