@@ -84,6 +84,7 @@ def dct_host_state(w, codes=None):
 
 
 MATRIX_CORES = [True]   # False: every stage on the VALU kernels (--valu)
+POP_SAMPLE = 8          # the timed region times one population launch in this many
 
 
 def make_trainer(w, z, p, tgt):
@@ -273,9 +274,11 @@ def run_gpu(w, steps, warmup, fd_steps=0, seconds=0.0):
         tr.synchronize()
         per = (time.perf_counter() - t0) / 2
         steps = int(min(2000, max(3, math.ceil(seconds / per))))
-    # the timed region: every launch of the population kernel bracketed by HIP events on the trainer's
-    # stream (an event pair costs the stream a few microseconds, so the other launches go unbracketed)
-    tr.set_profiling(True, only=["pop_eval"])
+    # the timed region: one launch of the population kernel in POP_SAMPLE timed by HIP events on the trainer's
+    # stream, recorded by the launch itself (a timed launch still costs the stream about 11 us on the
+    # MI355X - 6.7 before it and 4.5 after, in a kernel trace of material512 - so timing every launch would
+    # slow the region it measures; the other launches go untimed)
+    tr.set_profiling(True, only=["pop_eval"], every=POP_SAMPLE)
     tr.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -309,7 +312,7 @@ def run_gpu(w, steps, warmup, fd_steps=0, seconds=0.0):
         tr.reset_mlp_adam()
         it += 1
         fd_iter()   # the first step sizes the weight-set buffer
-        tr.set_profiling(True, only=["pop_eval"])
+        tr.set_profiling(True, only=["pop_eval"], every=POP_SAMPLE)
         tr.synchronize()
         t1 = time.perf_counter()
         for _ in range(fd_steps):

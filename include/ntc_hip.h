@@ -183,6 +183,9 @@ void ntc_trainer_set_profiling(ntc_trainer* t, int on);
 /* restrict the events to the comma-separated kernel families in names (null or "" = every family): each
  * event pair costs the stream a few microseconds */
 void ntc_trainer_set_profiling_only(ntc_trainer* t, const char* names);
+/* time one launch in n of each family (n <= 1: every launch), counted from the last ntc_trainer_set_profiling(t, 1):
+ * a timed launch costs the stream several microseconds around it, so sampling keeps a timed run's own pace */
+void ntc_trainer_set_profiling_every(ntc_trainer* t, int n);
 int ntc_trainer_kernel_time(ntc_trainer* t, const char* name, double* total_ms, long long* launches);
 // 1 if the stage ("pop_eval": the ES and central-difference populations, "lat_pair", "qat_search") runs on
 // the FP32 matrix cores for this model, else 0

@@ -184,8 +184,9 @@ void ntc_trainer_set_profiling(ntc_trainer* t, int on) {
     auto& I = *t->t.im;
     ntc_hip::resolve_times(I);
     I.profiling = on != 0;
-    if (on) I.times.clear();
+    if (on) { I.times.clear(); I.prof_seen.clear(); }
 }
+void ntc_trainer_set_profiling_every(ntc_trainer* t, int n) { t->t.im->prof_every = n > 1 ? n : 1; }
 void ntc_trainer_set_profiling_only(ntc_trainer* t, const char* names) { t->t.im->prof_only = names ? names : ""; }
 int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage) {
     const auto& I = *t->t.im;

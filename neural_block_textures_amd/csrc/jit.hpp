@@ -57,6 +57,12 @@ void jit_launch(void (*proto)(P...), Impl& I, const char* kernel, const std::str
         int i = 0;
         ((ptrs[i++] = (void*)&v), ...);
     }, vals);
+    if (I.ext_a) {   // inside a one-launch ProfScope (launch_timed): the dispatch records its events; sizes in work-items
+        NTC_CHECK(hipExtModuleLaunchKernel(jit_function(I, kernel, targs), grid.x * block.x, grid.y * block.y, grid.z * block.z, block.x,
+                                           block.y, block.z, shm, I.stream, ptrs, nullptr, I.ext_a, I.ext_b, 0));
+        I.ext_a = I.ext_b = nullptr;
+        return;
+    }
     NTC_CHECK(hipModuleLaunchKernel(jit_function(I, kernel, targs), grid.x, grid.y, grid.z, block.x, block.y, block.z, (unsigned)shm,
                                     I.stream, ptrs, nullptr));
 }

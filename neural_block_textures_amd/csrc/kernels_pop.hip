@@ -39,8 +39,7 @@ int pop_chunk(const Impl& I, int pairs, int M) {
 template <class S, int Act, int From>
 static void launch_pop_mfma(Impl& I, const PopSource& src, int pairs, int M, int chunk, int chunks) {
     auto kern = I.dm.clamp_out ? k_pop_mfma<S, Act, true, From> : k_pop_mfma<S, Act, false, From>;
-    hipLaunchKernelGGL(kern, dim3(pairs, chunks), dim3(64 * kPopWaves), 0, I.stream, I.dm, src, M, I.Mcap, chunk, chunks, I.feat,
-                       I.btgt, I.part);
+    launch_timed(kern, I, dim3(pairs, chunks), dim3(64 * kPopWaves), 0, I.dm, src, M, I.Mcap, chunk, chunks, I.feat, I.btgt, I.part);
 }
 
 static void check_pop_launch(const Impl& I, int pairs, int chunk, int chunks) {
@@ -78,7 +77,7 @@ static void launch_pop_matrix(Impl& I, const PopSource& src, int pairs, int M, i
 }
 
 void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks) {
-    ProfScope ps(I, "pop_eval");
+    ProfScope ps(I, "pop_eval", pop_on_matrix_cores(I));   // the matrix path is one launch
     if (!pop_on_matrix_cores(I)) {
         if ((size_t)2 * pairs * chunks > I.part_cap) {
             fprintf(stderr, "ntc_hip backend: population evaluation needs %d partial sums, buffer holds %zu\n", 2 * pairs * chunks,
@@ -102,7 +101,7 @@ void launch_pop_eval_es(Impl& I, int it, float sigma, int N, int M, int chunk, i
     // with three or more chunks per pair, the Gaussians are drawn once (not once per chunk)
     const bool once = chunks >= 3;
     if (once) launch_mlp_eps(I, it, N);
-    ProfScope ps(I, "pop_eval");
+    ProfScope ps(I, "pop_eval", true);
     if (once) launch_pop_matrix<kReadEps>(I, src, N, M, chunk, chunks);
     else launch_pop_matrix<kDraw>(I, src, N, M, chunk, chunks);
 }

@@ -11,6 +11,7 @@
 //   eps_lat, dpix  K x nz latent Gaussians and K x W*H per-pixel loss differences of one latent step
 //   tgt            W*H*nout target, interleaved as the caller's
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <stdio.h>
@@ -125,22 +126,39 @@ struct ntc_cuda::Trainer::Impl {
 
     bool profiling = false;
     std::string prof_only;     // comma-separated kernel families to time; empty = all
+    int prof_every = 1;        // time one launch in this many of each family
+    std::map<std::string, long long> prof_seen;   // launches of each family since profiling was switched on
+    hipEvent_t ext_a = nullptr, ext_b = nullptr;   // a ProfScope's events for the one launch it wraps (launch_timed)
     std::map<std::string, ntc_hip::KernelTimes> times;
 };
 
 namespace ntc_hip {
 using Impl = ntc_cuda::Trainer::Impl;
 
-// profiling: events around one launch on the trainer's stream
+// profiling: events around the launches of a scope on the trainer's stream. A scope that wraps exactly one
+// launch through launch_timed / jit_launch (`one`) hands its events to that launch, which records them with
+// the kernel's own dispatch (the kernel's start and end, no marker packets on the stream: an event record
+// between two kernels costs the stream several microseconds); any other scope records them around its work.
 struct ProfScope {
     Impl& I; const char* name; hipEvent_t a = nullptr, b = nullptr;
-    bool on;
-    ProfScope(Impl& I_, const char* n) : I(I_), name(n), on(I_.profiling && selected(I_.prof_only, n)) {
-        if (on) { NTC_CHECK(hipEventCreate(&a)); NTC_CHECK(hipEventCreate(&b)); NTC_CHECK(hipEventRecord(a, I.stream)); }
+    bool on, one;
+    ProfScope(Impl& I_, const char* n, bool one_launch = false)
+        : I(I_), name(n), on(I_.profiling && selected(I_.prof_only, n) && sampled(I_, n)), one(on && one_launch) {
+        if (!on) return;
+        NTC_CHECK(hipEventCreate(&a)); NTC_CHECK(hipEventCreate(&b));
+        if (one) { I.ext_a = a; I.ext_b = b; }
+        else NTC_CHECK(hipEventRecord(a, I.stream));
     }
     ~ProfScope() {
-        if (on) { NTC_CHECK(hipEventRecord(b, I.stream)); I.times[name].pending.emplace_back(a, b); }
+        if (!on) return;
+        if (one) {
+            if (I.ext_a) { fprintf(stderr, "ntc_hip backend: timed scope %s launched no kernel\n", name); exit(1); }
+        } else {
+            NTC_CHECK(hipEventRecord(b, I.stream));
+        }
+        I.times[name].pending.emplace_back(a, b);
     }
+    static bool sampled(Impl& I, const char* n) { return I.prof_every <= 1 || I.prof_seen[n]++ % I.prof_every == 0; }
     static bool selected(const std::string& only, const char* n) {
         if (only.empty()) return true;
         const std::string key = "," + only + ",", item = "," + std::string(n) + ",";
@@ -150,6 +168,17 @@ struct ProfScope {
 void resolve_times(Impl& I);
 
 inline int blocks_for(size_t n, int tpb) { return (int)((n + tpb - 1) / tpb); }
+
+// a launch on the trainer's stream; inside a one-launch ProfScope the kernel's dispatch records the scope's events
+template <class... P, class... A>
+void launch_timed(void (*kern)(P...), Impl& I, dim3 grid, dim3 block, size_t shm, A&&... args) {
+    if (I.ext_a) {
+        hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)shm, I.stream, I.ext_a, I.ext_b, 0u, std::forward<A>(args)...);
+        I.ext_a = I.ext_b = nullptr;
+    } else {
+        hipLaunchKernelGGL(kern, grid, block, shm, I.stream, std::forward<A>(args)...);
+    }
+}
 
 // noise tables (one pair per device, filled from the host C library on first use)
 // the device's noise correction bits (built once per device); false with a reason if the host's

@@ -120,6 +120,7 @@ def library() -> C.CDLL:
             "ntc_trainer_on_matrix_cores": (C.c_int, [P, C.c_char_p]),
             "ntc_trainer_set_matrix_cores": (None, [P, C.c_int]),
             "ntc_trainer_set_lat_group": (None, [P, C.c_int]),
+            "ntc_trainer_set_profiling_every": (None, [P, C.c_int]),
             "ntc_jit_compile_check": (C.c_int, [C.POINTER(ModelDesc), C.c_char_p, C.POINTER(C.c_double), C.c_char_p, C.c_size_t]),
             "ntc_trainer_dct_probe": (None, [P, P, P]),
             "ntc_trainer_dct_refit": (None, [P, P]),
@@ -463,9 +464,10 @@ class Trainer:
     def synchronize(self):
         self._lib.ntc_trainer_synchronize(self._h)
 
-    def set_profiling(self, on: bool, only=None):
-        """HIP events around every launch (of the kernel families in `only`, if given)"""
+    def set_profiling(self, on: bool, only=None, every: int = 1):
+        """HIP events around every launch (of the kernel families in `only`, if given; one launch in `every` of each)"""
         self._lib.ntc_trainer_set_profiling_only(self._h, ",".join(only).encode() if only else b"")
+        self._lib.ntc_trainer_set_profiling_every(self._h, int(every))
         self._lib.ntc_trainer_set_profiling(self._h, 1 if on else 0)
 
     def on_matrix_cores(self, stage: str) -> bool:
