@@ -203,6 +203,7 @@ void ntc_trainer_set_lat_group(ntc_trainer* t, int pairs) { t->t.im->lat_group =
 int ntc_jit_compile_check(const ntc_model_desc* d, const char* arch, double* seconds, char* why, size_t why_cap) {
     ntc_hip::DevModel m{};
     m.nlev = d->nlev; m.npos = d->npos; m.nl = d->nhidden; m.nout = d->nout; m.nin = d->nin; m.leak = d->leak;
+    m.fold_c = (1.0f - d->leak) / (1.0f + d->leak);
     m.clamp_out = d->clamp_out ? 1 : 0;
     for (int l = 0; l < d->nlev && l < ntc_hip::kMaxLevels; l++) m.lv[l].C = d->lv[l].C;
     for (int l = 0; l < d->nhidden && l < ntc_hip::kMaxHidden; l++) m.hidden[l] = d->hidden[l];

@@ -47,7 +47,7 @@ struct DevModel {
     float wsum;
     float inv_px;        // 1 / (3 wsum W H), float, as LatentTrainer computes it
     int P;               // MLP parameter count
-    int pad;
+    float fold_c;        // (1 - leak) / (1 + leak): the folded activation's constant, divided once on the host
     long long nz;        // latent floats
 };
 

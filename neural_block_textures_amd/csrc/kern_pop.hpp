@@ -132,6 +132,8 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     constexpr bool Es = From != kSets;
     __shared__ double red[kPopWaves];
     __shared__ float wpm_s[Es ? 2 * Q::kP : 1];   // ES: the + member's weights, then the - member's
+    // the pixel-per-lane output layer's transposes: kOwnWave floats per wave
+    __shared__ __attribute__((aligned(16))) float own_s[pop_own<S>() ? kPopWaves * kOwnWave : 4];
     const int lane = tid_x() & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
     const int pair = bid_x(), ch = bid_y(), sgn = wave & 1, half = wave >> 1;
@@ -182,7 +184,7 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     }
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
-    const float ak = act_k(Act, m.leak);
+    const float ak = act_k_of<Act>(m);
     // the channel weight of each of this lane's outputs (pixel-per-lane layer: output r; D layout: rows
     // 4 g + r; VALU output layer: output g), zero past the last output
     float cw[NT];
@@ -207,7 +209,7 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
             // fused multiply-add each, summed in float, then into the double
             float x[U][Q::kKsH];
             mfma_hidden<S, U, Act, false>(W, c.b1, ak, x);
-            const f4v o = mfma_out_own<S>(W, x);
+            const f4v o = mfma_out_own_lds<S>(W, x, own_s + wave * kOwnWave, g, i16);
             float tsum = 0.0f;
 #pragma unroll
             for (int r = 0; r < NT; r++) {
@@ -396,7 +398,7 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     mfma_load<S, false>(W, w, lane);
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
-    const float ak = act_k(Act, m.leak);
+    const float ak = act_k_of<Act>(m);
     float cw[4];
     if constexpr (kVOut) {
 #pragma unroll
@@ -499,7 +501,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
     mfma_load<S, false>(W, w, lane);
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
-    const float ak = act_k(Act, m.leak);
+    const float ak = act_k_of<Act>(m);
     constexpr bool kVOut = valu_out<S>();   // the output layer on the VALU: output g of pixel j in lane (g, j)
     float cw[4];
     if constexpr (kVOut) {

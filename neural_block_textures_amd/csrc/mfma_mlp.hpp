@@ -121,25 +121,28 @@ struct MfmaWeights {
 // the inputs in ascending order (k-step ks = inputs 4 ks .. 4 ks + 3; the activations are transposed
 // to match). Otherwise k-step 4 t + r takes the inputs in the order in which register r of hidden
 // tile t holds them across the lane groups, and the activations feed the next layer untransposed:
-// the same products, summed in another order. Padding units and inputs get zero weights.
+// the same products, summed in another order. Padding units and inputs get zero weights: every lane
+// reads a parameter (the index clamped to a valid one) and selects zero where it has none, so the gather
+// takes no branches.
 template <class S, bool Exact, class Get>
 __device__ __forceinline__ void mfma_load_from(MfmaWeights<S>& W, const Get& w, int lane) {
     using Q = MfmaShape<S>;
     static_assert(!Exact || Q::kLastU == 16, "the ascending-order layout needs whole 16-unit tiles");
     constexpr int NIN = Q::kIn, H = Q::kH, NO = Q::kNout;
     const int i16 = lane & 15, g = lane >> 4;
+    auto at = [&](bool ok, int k) { const float v = w(k); return ok ? v : 0.0f; };
 #pragma unroll
     for (int ot = 0; ot < Q::kHt; ot++) {
-        const int u = unit_of<Q>(ot, i16);
+        const int u = unit_of<Q>(ot, i16), uc = min(u, H - 1);
 #pragma unroll
         for (int ks = 0; ks < Q::kKs1; ks++) {
             const int in = 4 * ks + g;
-            W.a1[ot][ks] = (in < NIN && u < H) ? w(u * NIN + in) : 0.0f;
+            W.a1[ot][ks] = at(in < NIN && u < H, uc * NIN + min(in, NIN - 1));
         }
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int ur = unit_of<Q>(ot, 4 * g + r);
-            W.c1[ot][r] = ur < H ? w(H * NIN + ur) : 0.0f;
+            W.c1[ot][r] = at(ur < H, H * NIN + min(ur, H - 1));
         }
     }
     int p = H * NIN + H;
@@ -147,16 +150,16 @@ __device__ __forceinline__ void mfma_load_from(MfmaWeights<S>& W, const Get& w, 
     for (int l = 0; l < Q::kNL - 1; l++) {
 #pragma unroll
         for (int ot = 0; ot < Q::kHt; ot++) {
-            const int u = unit_of<Q>(ot, i16);
+            const int u = unit_of<Q>(ot, i16), uc = min(u, H - 1);
 #pragma unroll
             for (int ks = 0; ks < Q::kKsH; ks++) {
                 const int in = hidden_input<Q, Exact>(ks, g);
-                W.ah[l][ot][ks] = (u < H && in < H) ? w(p + u * H + in) : 0.0f;
+                W.ah[l][ot][ks] = at(u < H && in < H, p + uc * H + min(in, H - 1));
             }
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int ur = unit_of<Q>(ot, 4 * g + r);
-                W.ch[l][ot][r] = ur < H ? w(p + H * H + ur) : 0.0f;
+                W.ch[l][ot][r] = at(ur < H, p + H * H + min(ur, H - 1));
             }
         }
         p += H * H + H;
@@ -167,27 +170,27 @@ __device__ __forceinline__ void mfma_load_from(MfmaWeights<S>& W, const Get& w, 
 #pragma unroll
             for (int ks = 0; ks < Q::kKsH; ks++) {
                 const int in = hidden_input<Q, Exact>(ks, g);
-                W.wo[c][ks] = (c < NO && in < H) ? w(p + c * H + in) : 0.0f;
+                W.wo[c][ks] = c < NO ? at(in < H, p + c * H + min(in, H - 1)) : 0.0f;
             }
-            W.bo[c] = (c < NO && g == 0) ? w(p + NO * H + c) : 0.0f;
+            W.bo[c] = c < NO ? at(g == 0, p + NO * H + c) : 0.0f;
             W.c4[c] = c < NO ? w(p + NO * H + c) : 0.0f;
         }
-        const int oc = lane & 3;
+        const int oc = lane & 3, occ = min(oc, NO - 1);
 #pragma unroll
         for (int ks = 0; ks < Q::kKsH; ks++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int in = hidden_input<Q, Exact>(ks, r);
-                W.wo4[ks][r] = (oc < NO && in < H) ? w(p + oc * H + in) : 0.0f;
+                W.wo4[ks][r] = in < H ? at(oc < NO, p + occ * H + in) : 0.0f;
             }
     } else {
 #pragma unroll
         for (int ks = 0; ks < Q::kKsH; ks++) {
             const int in = hidden_input<Q, Exact>(ks, g);
-            W.ao[ks] = (i16 < NO && in < H) ? w(p + i16 * H + in) : 0.0f;
+            W.ao[ks] = at(i16 < NO && in < H, p + min(i16, NO - 1) * H + min(in, H - 1));
         }
 #pragma unroll
-        for (int r = 0; r < 4; r++) W.co[r] = 4 * g + r < NO ? w(p + NO * H + 4 * g + r) : 0.0f;
+        for (int r = 0; r < 4; r++) W.co[r] = at(4 * g + r < NO, p + NO * H + min(4 * g + r, NO - 1));
     }
 }
 
@@ -290,6 +293,9 @@ __device__ __forceinline__ float act(float x, float k) {
 // the activation constant k of act<Act> for a model's leak, and the hidden layers' weight scale b of kActFold
 __host__ __device__ inline float act_k(int mode, float leak) { return mode == kActFold ? (1.0f - leak) / (1.0f + leak) : leak; }
 __host__ __device__ inline float fold_scale(float leak) { return 0.5f * (1.0f + leak); }
+// act_k for a model: kActFold's quotient comes divided from the host (DevModel::fold_c, the same IEEE division)
+template <int Act>
+__device__ __forceinline__ float act_k_of(const DevModel& m) { return Act == kActFold ? m.fold_c : m.leak; }
 
 // Every hidden layer's weights and biases times b (kActFold).
 template <class S>
@@ -415,6 +421,49 @@ __device__ __forceinline__ f4v mfma_out_own(const MfmaWeights<S>& W, const float
         o2 = mfma4x4(W.wo4[ks][2], y[2], o2);
         o = mfma4x4(W.wo4[ks][1], y[1], o);
         o2 = mfma4x4(W.wo4[ks][3], y[3], o2);
+    }
+#pragma unroll
+    for (int r = 0; r < MfmaShape<S>::kNout; r++) o[r] += o2[r];
+    return o;
+}
+
+// mfma_out_own with the (lane group, tile) transpose through LDS rows of the wave's own instead of lane
+// swaps (each swap costs the SIMD about three VALU issue slots; the LDS moves issue beside other waves'
+// matrix and VALU work): lane (g, j) writes register ks of tile u to row (u, j), column 4 g + ks, and
+// reads row (g, j) back, column 4 r + ks being what the swaps leave in its register r at k-step ks. Rows
+// are kOwnRow floats apart (20: the 16 lanes of a group write and read 16-byte pieces in 16 distinct
+// groups of four banks). A wave's LDS operations complete in program order, so its reads see its writes
+// and the next pass's writes come after these reads: no barrier (the fences only keep the compiler
+// from reordering them). The same products, summed in the same order as mfma_out_own.
+constexpr int kOwnRow = 20, kOwnWave = 4 * 16 * kOwnRow;
+template <class S>
+__device__ __forceinline__ f4v mfma_out_own_lds(const MfmaWeights<S>& W, const float (&x)[4][MfmaShape<S>::kKsH],
+                                                float* __restrict__ t, int g, int j) {
+    static_assert(valu_out<S>() && MfmaShape<S>::kKsH <= 4, "at most 4 outputs, one 16-unit tile");
+    constexpr int KS = MfmaShape<S>::kKsH;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        f4v v = { 0.0f, 0.0f, 0.0f, 0.0f };
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) v[ks] = x[u][ks];
+        *reinterpret_cast<f4v*>(t + (u * 16 + j) * kOwnRow + 4 * g) = v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    f4v y[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) y[r] = *reinterpret_cast<const f4v*>(t + (g * 16 + j) * kOwnRow + 4 * r);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    f4v o = W.c4, o2 = { 0.0f, 0.0f, 0.0f, 0.0f };
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+        o = mfma4x4(W.wo4[ks][0], y[0][ks], o);
+        o2 = mfma4x4(W.wo4[ks][2], y[2][ks], o2);
+        o = mfma4x4(W.wo4[ks][1], y[1][ks], o);
+        o2 = mfma4x4(W.wo4[ks][3], y[3][ks], o2);
     }
 #pragma unroll
     for (int r = 0; r < MfmaShape<S>::kNout; r++) o[r] += o2[r];

@@ -310,6 +310,7 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
     for (int q = 0; q < d.npos; q++) m.pos[q] = d.pos[q].kind;
     for (int l = 0; l < d.nhidden; l++) m.hidden[l] = d.hidden[l];
     m.leak = d.leak; m.clamp_out = d.clamp_out ? 1 : 0;
+    m.fold_c = (1.0f - d.leak) / (1.0f + d.leak);
     for (int c = 0; c < MAX_OUT; c++) m.cw[c] = c < d.nout ? d.cw[c] : 0.0f;
     m.wsum = d.wsum;
     m.inv_px = 1.0f / (3.0f * d.wsum * (float)d.W * (float)d.H);
