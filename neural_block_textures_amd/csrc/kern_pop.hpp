@@ -134,6 +134,9 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     __shared__ float wpm_s[Es ? 2 * Q::kP : 1];   // ES: the + member's weights, then the - member's
     // the pixel-per-lane output layer's transposes: kOwnWave floats per wave
     __shared__ __attribute__((aligned(16))) float own_s[pop_own<S>() ? kPopWaves * kOwnWave : 4];
+    // the VALU output layer's reduce-scatters: kVoTile floats per tile of a pass, per wave
+    constexpr int kVoWave = kVoTile * pop_u<S>();
+    __shared__ __attribute__((aligned(16))) float vo_s[valu_out<S>() && !pop_own<S>() ? kPopWaves * kVoWave : 4];
     const int lane = tid_x() & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
     const int pair = bid_x(), ch = bid_y(), sgn = wave & 1, half = wave >> 1;
@@ -226,7 +229,7 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
                 mfma_hidden<S, U, Act, false>(W, c.b1, ak, x);
 #pragma unroll
                 for (int u = 0; u < U; u++) {
-                    dd[u][0] = out_of<S>(valu_out_g<S>(W, x[u]), Clamp) - c.t[u][0];
+                    dd[u][0] = out_of<S>(valu_out_g_lds<S>(W, x[u], vo_s + wave * kVoWave + u * kVoTile, g, i16), Clamp) - c.t[u][0];
                     dq[u][0] = __fmul_rn(cw[0], dd[u][0]);
                 }
             } else {

@@ -496,6 +496,37 @@ __device__ __forceinline__ float valu_out_g(const MfmaWeights<S>& W, const float
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// valu_out_g with the reduce-scatter through kVoTile floats of the wave's own LDS (t) instead of lane swaps
+// (cheaper in VALU issue slots, as for mfma_out_own_lds): lane (g, j) writes its partial of output c to row
+// j, column 4 c + g (rows kOwnRow floats apart: conflict-free), then reads row j's columns 4 g .. 4 g + 3 -
+// output g's four partials - and adds them as valu_out_g does, (g0 + g2) + (g1 + g3): the same value bit for bit.
+constexpr int kVoTile = 16 * kOwnRow;
+template <class S>
+__device__ __forceinline__ float valu_out_g_lds(const MfmaWeights<S>& W, const float (&x)[MfmaShape<S>::kKsH], float* __restrict__ t,
+                                                int g, int j) {
+    static_assert(valu_out<S>(), "at most 4 outputs");
+    constexpr int NO = MfmaShape<S>::kNout;
+    float p[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        p[c] = W.bo[c];
+        if (c < NO) {
+#pragma unroll
+            for (int ks = 0; ks < MfmaShape<S>::kKsH; ks++) p[c] = __builtin_fmaf(W.wo[c][ks], x[ks], p[c]);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) t[j * kOwnRow + 4 * c + g] = p[c];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const f4v v = *reinterpret_cast<const f4v*>(t + j * kOwnRow + 4 * g);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    return (v[0] + v[2]) + (v[1] + v[3]);
+}
+
 
 // ---- per-pixel error across the output tile
 // Lane (g, j) holds the output units 4 g + r of pixel j; the reference sums a pixel's channels
