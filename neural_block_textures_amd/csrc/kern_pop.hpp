@@ -394,6 +394,13 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     constexpr bool kVOut = valu_out<S>();
     const int k = bid_y();
     const int lane = tid_x() & 63, wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6), i16 = lane & 15, g = lane >> 4;
+    // each wave's LDS exchanges (in place of lane swaps): both members' tile operands, the VALU output layer's
+    // reduce-scatters of both members, the pixel sums of both members' errors
+    constexpr int kWaveLds = 2 * kTilesLds<S> + (kVOut ? 2 * kVoTile : 0) + kSumsLds;
+    __shared__ __attribute__((aligned(16))) float lds[4 * kWaveLds];
+    float* const tl = lds + wave * kWaveLds;
+    float* const vo = tl + 2 * kTilesLds<S>;
+    float* const sums = vo + (kVOut ? 2 * kVoTile : 0);
     const __amdgpu_buffer_rsrc_t rz = buffer_of(zdec, 4u * (uint32_t)m.nz), re = buffer_of(eps + (size_t)k * m.nz, 4u * (uint32_t)m.nz),
                                  rn = buffer_of(eps, 0u);   // a level outside the mask: no Gaussians (every load 0)
     float* out = dpix + (size_t)k * m.npix;
@@ -438,8 +445,8 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
             round_pixel(m, base, lane, px, py);
             float fp[S::kMaxIn], fm[S::kMaxIn];
             features_pm<S>(m, rz, re, rn, sg, mask, px, py, fp, fm);
-            tiles_of<S>(fp, bp);
-            tiles_of<S>(fm, bm);
+            tiles_of_lds<S>(fp, bp, tl, g, i16);
+            tiles_of_lds<S>(fm, bm, tl + kTilesLds<S>, g, i16);
         }
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -458,7 +465,8 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
             if constexpr (kVOut) {
                 float x[2][Q::kKsH];
                 mfma_hidden<S, 2, Act, false>(W, b1, ak, x);
-                const float dp = out_of<S>(valu_out_g<S>(W, x[0]), Clamp) - tt[0], dm = out_of<S>(valu_out_g<S>(W, x[1]), Clamp) - tt[0];
+                const float dp = out_of<S>(valu_out_g_lds<S>(W, x[0], vo, g, i16), Clamp) - tt[0],
+                            dm = out_of<S>(valu_out_g_lds<S>(W, x[1], vo + kVoTile, g, i16), Clamp) - tt[0];
                 ep = __fmul_rn(cw[0], __fmul_rn(dp, dp));
                 em = __fmul_rn(cw[0], __fmul_rn(dm, dm));
             } else {
@@ -471,12 +479,9 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
                     em = __builtin_fmaf(cw[r], __fmul_rn(dm, dm), em);
                 }
             }
-            const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(ep), __float_as_uint(em), false, false);
-            const float s = __uint_as_float(h[0]) + __uint_as_float(h[1]);   // groups 0 + 2 and 1 + 3
-            const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
-            const float c = __uint_as_float(q[0]) + __uint_as_float(q[1]);   // lanes 0-31: e+, 32-63: e-
-            const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);
-            if (g == 0 && p < m.npix) out[p] = __fmul_rn(__uint_as_float(x[0]) - __uint_as_float(x[1]), m.inv_px);
+            float sp, sm;
+            group_sums_lds(ep, em, sums, g, i16, sp, sm);
+            if (g == 0 && p < m.npix) out[p] = __fmul_rn(sp - sm, m.inv_px);
         }
     }
 }
@@ -500,12 +505,19 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
     using Q = MfmaShape<S>;
     constexpr int NO = Q::kNout, C0 = S::kC0;
     const int lane = tid_x() & 63, wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6), i16 = lane & 15, g = lane >> 4;
+    constexpr bool kVOut = valu_out<S>();   // the output layer on the VALU: output g of pixel j in lane (g, j)
+    // each wave's LDS exchanges (in place of lane swaps): the tile operands, the VALU output layer's
+    // reduce-scatters of both candidates, the candidates' pixel sums
+    constexpr int kWaveLds = kTilesLds<S> + (kVOut ? 2 * kVoTile : 0) + kSumsLds;
+    __shared__ __attribute__((aligned(16))) float lds[4 * kWaveLds];
+    float* const tl = lds + wave * kWaveLds;
+    float* const vo = tl + kTilesLds<S>;
+    float* const sums = vo + (kVOut ? 2 * kVoTile : 0);
     MfmaWeights<S> W;
     mfma_load<S, false>(W, w, lane);
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
     const float ak = act_k_of<Act>(m);
-    constexpr bool kVOut = valu_out<S>();   // the output layer on the VALU: output g of pixel j in lane (g, j)
     float cw[4];
     if constexpr (kVOut) {
 #pragma unroll
@@ -520,7 +532,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
         features<S>(m, PlainLatent{ zdec }, pr % m.W, pr / m.W, f);
     }
     float b[4][Q::kKs1];
-    tiles_of<S>(f, b);
+    tiles_of_lds<S>(f, b, tl, g, i16);
     float t4[4][4];   // targets: lane (g, j) holds channels 4 g .. 4 g + 3 (VALU output layer: g) of pixel j of each tile
 #pragma unroll
     for (int t = 0; t < 4; t++) {
@@ -552,7 +564,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                     mfma_hidden<S, 2, Act, false>(W, b2, ak, x);
 #pragma unroll
                     for (int v = 0; v < 2; v++) {
-                        const float d = out_of<S>(valu_out_g<S>(W, x[v]), Clamp) - t4[t][0];
+                        const float d = out_of<S>(valu_out_g_lds<S>(W, x[v], vo + v * kVoTile, g, i16), Clamp) - t4[t][0];
                         lv[v] = __fmul_rn(cw[0], __fmul_rn(d, d));   // cw (d d), main.cpp:2119
                     }
                 } else {
@@ -568,9 +580,11 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                         }
                     }
                 }
+                float ls[2];
+                group_sums_lds(lv[0], lv[1], sums, g, i16, ls[0], ls[1]);
 #pragma unroll
                 for (int v = 0; v < 2; v++) {
-                    const float l = group_sum_f(lv[v]);
+                    const float l = ls[v];
                     if (kc + v == cur) cur_l = l;
                     else if (best_k < 0 || l < best_l) { best_l = l; best_k = kc + v; }
                 }

@@ -527,6 +527,49 @@ __device__ __forceinline__ float valu_out_g_lds(const MfmaWeights<S>& W, const f
     return (v[0] + v[2]) + (v[1] + v[3]);
 }
 
+// Wave-local LDS exchanges in place of lane swaps (a wave's LDS operations complete in program order, so
+// no barrier; the fences only keep the compiler from moving them across each other).
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// tiles_of through kTilesLds<S> floats of the wave's LDS: lane (t, j) writes feature 4 ks + r of its pixel
+// to [r][ks][j][t], lane (g, j) reads [g][ks][j][0 .. 3] = b[0 .. 3][ks] (every access conflict-free).
+template <class S>
+constexpr int kTilesLds = 4 * MfmaShape<S>::kKs1 * 64;
+template <class S>
+__device__ __forceinline__ void tiles_of_lds(const float (&f)[S::kMaxIn], float (&b)[4][MfmaShape<S>::kKs1], float* __restrict__ t,
+                                             int g, int j) {
+    using Q = MfmaShape<S>;
+#pragma unroll
+    for (int ks = 0; ks < Q::kKs1; ks++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) t[((r * Q::kKs1 + ks) * 16 + j) * 4 + g] = 4 * ks + r < Q::kIn ? f[4 * ks + r] : 0.0f;
+    wave_lds_fence();
+#pragma unroll
+    for (int ks = 0; ks < Q::kKs1; ks++) {
+        const f4v v = *reinterpret_cast<const f4v*>(t + ((g * Q::kKs1 + ks) * 16 + j) * 4);
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) b[tt][ks] = v[tt];
+    }
+    wave_lds_fence();
+}
+
+// The sums of a and of b over the four lane groups of each pixel, in every one of them, added as group_sum_f
+// adds them, (g0 + g2) + (g1 + g3), through kSumsLds floats of the wave's LDS (rows kOwnRow apart).
+constexpr int kSumsLds = 16 * kOwnRow;
+__device__ __forceinline__ void group_sums_lds(float a, float b, float* __restrict__ t, int g, int j, float& sa, float& sb) {
+    t[j * kOwnRow + g] = a;
+    t[j * kOwnRow + 4 + g] = b;
+    wave_lds_fence();
+    const f4v va = *reinterpret_cast<const f4v*>(t + j * kOwnRow), vb = *reinterpret_cast<const f4v*>(t + j * kOwnRow + 4);
+    wave_lds_fence();
+    sa = (va[0] + va[2]) + (va[1] + va[3]);
+    sb = (vb[0] + vb[2]) + (vb[1] + vb[3]);
+}
+
 
 // ---- per-pixel error across the output tile
 // Lane (g, j) holds the output units 4 g + r of pixel j; the reference sums a pixel's channels
