@@ -31,8 +31,8 @@ namespace ntc_hip {
 
 constexpr int kPopWaves = 4;
 // Models with at most 4 outputs and one 16-unit hidden tile take the pixel-per-lane output layer
-// (mfma_out_own): four tiles per pass, transposed so that every lane holds all hidden units of one pixel,
-// then v_mfma_f32_4x4x1_16b_f32 steps leave that pixel's outputs in its own registers.
+// (mfma_out_own): four tiles per pass, exchanged through the wave's LDS so that every lane holds all hidden
+// units of one pixel, then v_mfma_f32_4x4x1_16b_f32 steps leave that pixel's outputs in its own registers.
 template <class S>
 constexpr bool pop_own() { return valu_out<S>() && MfmaShape<S>::kHt == 1; }
 // 16-slot tiles a wave evaluates at once (independent chains of matrix instructions; two for the other
@@ -48,9 +48,9 @@ constexpr int pop_u() { return pop_own<S>() ? 4 : 2; }
 // The targets a lane needs per tile: the pixel-per-lane output layer leaves every output of the lane's
 // own pixel in the lane (its nout targets, once per pass); models with at most 4 outputs otherwise take
 // their output layer on the VALU (valu_out_g), which leaves output g of pixel j in lane (g, j): one
-// target per tile; otherwise the D layout's four per tile (outputs 4 g + r).
+// target per tile; otherwise the D layout's out_regs per tile (outputs out_at(g, r)).
 template <class S>
-constexpr int pop_nt() { return pop_own<S>() ? MfmaShape<S>::kNout : (valu_out<S>() ? 1 : 4); }
+constexpr int pop_nt() { return pop_own<S>() ? MfmaShape<S>::kNout : (valu_out<S>() ? 1 : out_regs<S>()); }
 template <class S>
 constexpr int pop_tt() { return pop_own<S>() ? 1 : pop_u<S>(); }
 
@@ -145,15 +145,15 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     constexpr bool kOwn = pop_own<S>();
     constexpr bool kVOut = valu_out<S>();
     // lane byte offsets of the feature rows 4 ks + g (rows past nin are the array's zero rows) and target
-    // rows 4 g + r, or g (rows past the last one are clamped to it: their channel weights cw are zero); the
-    // pixel-per-lane layer: target row r of pixel i16 of tile g
+    // rows out_at(g, r), or g (padding and rows past the last one read a valid row: their channel weights cw
+    // are zero); the pixel-per-lane layer: target row r of pixel i16 of tile g
     uint32_t fo[Q::kKs1], to[NT];
 #pragma unroll
     for (int ks = 0; ks < Q::kKs1; ks++) fo[ks] = 4u * ((uint32_t)(4 * ks + g) * (uint32_t)Mcap + (uint32_t)i16);
 #pragma unroll
     for (int r = 0; r < NT; r++)
         to[r] = kOwn ? 4u * ((uint32_t)r * (uint32_t)Mcap + 32u * (uint32_t)g + (uint32_t)i16)
-                     : 4u * ((uint32_t)min(kVOut ? g : 4 * g + r, Q::kNout - 1) * (uint32_t)Mcap + (uint32_t)i16);
+                     : 4u * ((uint32_t)(kVOut ? min(g, Q::kNout - 1) : max(out_at<S>(g, r), 0)) * (uint32_t)Mcap + (uint32_t)i16);
     const int s0 = ch * chunk, s1 = min(M, s0 + chunk);
     const int tiles = (s1 - s0 + 15) >> 4;
     const int mine = (tiles - half + 1) >> 1;   // this wave's tiles: 2 j + half, j < mine
@@ -181,9 +181,9 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
             wpm_s[Q::kP + k] = __builtin_fmaf(-src.sigma, e, w0);
         }
         __syncthreads();
-        mfma_load<S, false>(W, wpm_s + sgn * Q::kP, lane);
+        mfma_load<S>(W, wpm_s + sgn * Q::kP, lane);
     } else {
-        mfma_load<S, false>(W, src.wsets + (size_t)(2 * pair + sgn) * Q::kP, lane);
+        mfma_load<S>(W, src.wsets + (size_t)(2 * pair + sgn) * Q::kP, lane);
     }
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
@@ -196,7 +196,7 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
         cw[r] = 0.0f;
 #pragma unroll
         for (int c = 0; c < Q::kNout; c++)
-            if ((kOwn ? r : (kVOut ? g : 4 * g + r)) == c) cw[r] = m.cw[c];
+            if ((kOwn ? r : (kVOut ? g : out_at<S>(g, r))) == c) cw[r] = m.cw[c];
     }
     double e = 0.0;
     // One pass: tiles j .. j + U - 1 from c, while tiles j + U .. load into n. The loop alternates
@@ -211,8 +211,8 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
             // the lane's own pixel (pixel i16 of tile j + g): its channel terms cw (d d), one multiply and one
             // fused multiply-add each, summed in float, then into the double
             float x[U][Q::kKsH];
-            mfma_hidden<S, U, Act, false>(W, c.b1, ak, x);
-            const f4v o = mfma_out_own_lds<S>(W, x, own_s + wave * kOwnWave, g, i16);
+            mfma_hidden<S, U, Act>(W, c.b1, ak, x);
+            const f4v o = mfma_out_own<S>(W, x, own_s + wave * kOwnWave, g, i16);
             float tsum = 0.0f;
 #pragma unroll
             for (int r = 0; r < NT; r++) {
@@ -226,15 +226,15 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
             float dq[pop_tt<S>()][NT], dd[pop_tt<S>()][NT];
             if constexpr (kVOut) {
                 float x[U][Q::kKsH];
-                mfma_hidden<S, U, Act, false>(W, c.b1, ak, x);
+                mfma_hidden<S, U, Act>(W, c.b1, ak, x);
 #pragma unroll
                 for (int u = 0; u < U; u++) {
-                    dd[u][0] = out_of<S>(valu_out_g_lds<S>(W, x[u], vo_s + wave * kVoWave + u * kVoTile, g, i16), Clamp) - c.t[u][0];
+                    dd[u][0] = out_of<S>(valu_out_g<S>(W, x[u], vo_s + wave * kVoWave + u * kVoTile, g, i16), Clamp) - c.t[u][0];
                     dq[u][0] = __fmul_rn(cw[0], dd[u][0]);
                 }
             } else {
                 f4v o[U];
-                mfma_forward<S, U, Act, false>(W, c.b1, ak, o);
+                mfma_forward<S, U, Act>(W, c.b1, ak, o);
 #pragma unroll
                 for (int u = 0; u < U; u++)
 #pragma unroll
@@ -288,11 +288,11 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
 // The latent pair evaluation (LatentTrainer::step_impl, main.cpp:1990-2007) on the matrix cores:
 // block (512 or 256 pixels, pair k), each wave a quarter of them in rounds of 64. In a round every
 // lane builds the features of its own pixel with the pair's texels perturbed by +sg eps and by
-// -sg eps (features_pm: both members from one set of taps and texel loads), and four transposes
-// across the lane groups (tiles_of) turn the 64 pixels into the B operands of four 16-pixel tiles:
-// no shared memory and no barrier, so a wave's feature loads overlap other waves' matrix work. Each
+// -sg eps (features_pm: both members from one set of taps and texel loads), and an exchange through
+// the wave's own LDS rows (tiles_of) turns the 64 pixels into the B operands of four 16-pixel tiles:
+// no barrier, so a wave's feature loads overlap other waves' matrix work. Each
 // tile's + and - members are evaluated together; a pixel's error is decode_err's float sum of
-// cw (d d) over its channels (a lane's four in ascending order, then the lane groups pairwise: within
+// cw (d d) over its channels (a lane's out_regs in ascending order, then the lane groups pairwise: within
 // a few ulp of the reference's ascending chain), and dpix = (e+ - e-) * inv_px.
 // rounds of 64 pixels per wave, at most: 2 (512 pixels per block), or 1 for wide inputs; the launch may
 // take fewer (`rounds`) to spread a small image over more blocks. One rule for the kernel and its
@@ -405,7 +405,7 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
                                  rn = buffer_of(eps, 0u);   // a level outside the mask: no Gaussians (every load 0)
     float* out = dpix + (size_t)k * m.npix;
     MfmaWeights<S> W;
-    mfma_load<S, false>(W, w, lane);
+    mfma_load<S>(W, w, lane);
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
     const float ak = act_k_of<Act>(m);
@@ -414,24 +414,19 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
 #pragma unroll
         for (int r = 0; r < 4; r++) cw[r] = (r == 0 && g < NO) ? m.cw[g] : 0.0f;
     } else {
-        lane_cw<NO>(m.cw, g, cw);
+        lane_cw<S>(m.cw, g, cw);
     }
-    // the targets of the tile at pixel t0: lane (g, j) reads channels 4 g .. 4 g + 3 of pixel t0 + j (one
-    // 16-byte load when a pixel's row is a whole number of float4; rows past the last are clamped);
-    // VALU output layer: channel g
+    // the targets of the tile at pixel t0: lane (g, j) reads channels out_at(g, r) of pixel t0 + j (padding
+    // reads a valid channel; rows past the last pixel are clamped); VALU output layer: channel g
     auto load_t = [&](int t0, float (&t)[4]) {
         const int pr = min(t0 + i16, m.npix - 1);
         if constexpr (kVOut) {
             t[0] = tgt[(size_t)pr * NO + min(g, NO - 1)];
 #pragma unroll
             for (int r = 1; r < 4; r++) t[r] = 0.0f;
-        } else if constexpr (NO % 4 == 0) {
-            const f4v v = *reinterpret_cast<const f4v*>(tgt + (size_t)pr * NO + min(4 * g, NO - 4));
-#pragma unroll
-            for (int r = 0; r < 4; r++) t[r] = v[r];
         } else {
 #pragma unroll
-            for (int r = 0; r < 4; r++) t[r] = tgt[(size_t)pr * NO + min(4 * g + r, NO - 1)];
+            for (int r = 0; r < 4; r++) t[r] = r < out_regs<S>() ? tgt[(size_t)pr * NO + max(out_at<S>(g, r), 0)] : 0.0f;
         }
     };
     for (int rd = 0; rd < kRounds; rd++) {
@@ -445,8 +440,8 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
             round_pixel(m, base, lane, px, py);
             float fp[S::kMaxIn], fm[S::kMaxIn];
             features_pm<S>(m, rz, re, rn, sg, mask, px, py, fp, fm);
-            tiles_of_lds<S>(fp, bp, tl, g, i16);
-            tiles_of_lds<S>(fm, bm, tl + kTilesLds<S>, g, i16);
+            tiles_of<S>(fp, bp, tl, g, i16);
+            tiles_of<S>(fm, bm, tl + kTilesLds<S>, g, i16);
         }
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -458,29 +453,29 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
 #pragma unroll
             for (int ks = 0; ks < Q::kKs1; ks++) { b1[0][ks] = bp[t][ks]; b1[1][ks] = bm[t][ks]; }
             const int p = base + 16 * t + i16;
-            // each lane's channel terms cw (d d) (its four in ascending order, or its one on the VALU output
+            // each lane's channel terms cw (d d) (its out_regs in ascending order, or its one on the VALU output
             // layer), then the four lane groups added pairwise (permlane swaps): e+ in lanes 0-31, e- in
             // lanes 32-63, then e+ - e-
             float ep = 0.0f, em = 0.0f;
             if constexpr (kVOut) {
                 float x[2][Q::kKsH];
-                mfma_hidden<S, 2, Act, false>(W, b1, ak, x);
-                const float dp = out_of<S>(valu_out_g_lds<S>(W, x[0], vo, g, i16), Clamp) - tt[0],
-                            dm = out_of<S>(valu_out_g_lds<S>(W, x[1], vo + kVoTile, g, i16), Clamp) - tt[0];
+                mfma_hidden<S, 2, Act>(W, b1, ak, x);
+                const float dp = out_of<S>(valu_out_g<S>(W, x[0], vo, g, i16), Clamp) - tt[0],
+                            dm = out_of<S>(valu_out_g<S>(W, x[1], vo + kVoTile, g, i16), Clamp) - tt[0];
                 ep = __fmul_rn(cw[0], __fmul_rn(dp, dp));
                 em = __fmul_rn(cw[0], __fmul_rn(dm, dm));
             } else {
                 f4v o[2];
-                mfma_forward<S, 2, Act, false>(W, b1, ak, o);
+                mfma_forward<S, 2, Act>(W, b1, ak, o);
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
+                for (int r = 0; r < out_regs<S>(); r++) {
                     const float dp = out_of<S>(o[0][r], Clamp) - tt[r], dm = out_of<S>(o[1][r], Clamp) - tt[r];
                     ep = __builtin_fmaf(cw[r], __fmul_rn(dp, dp), ep);
                     em = __builtin_fmaf(cw[r], __fmul_rn(dm, dm), em);
                 }
             }
             float sp, sm;
-            group_sums_lds(ep, em, sums, g, i16, sp, sm);
+            group_sums(ep, em, sums, g, i16, sp, sm);
             if (g == 0 && p < m.npix) out[p] = __fmul_rn(sp - sm, m.inv_px);
         }
     }
@@ -494,7 +489,7 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
 // value first, then every other value with strict <, so the first strictly smaller loss wins
 // (main.cpp:2101-2132). The winner enters the features of the next channel and is written to the
 // decode buffer. A candidate's loss is the pixel's float sum of cw (d d) over its channels (a lane's
-// four, then the pixel's four lanes pairwise, the same value in each of them) with the hidden
+// out_regs, then the pixel's four lanes pairwise, the same value in each of them) with the hidden
 // activation of act<Act>: the reference adds the float terms in double with its own activation, so a
 // choice can differ from the reference's only between candidates whose losses agree to a few float
 // roundings (the reference's own check accepts such rounding ties, main.cpp:3143-3144).
@@ -514,7 +509,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
     float* const vo = tl + kTilesLds<S>;
     float* const sums = vo + (kVOut ? 2 * kVoTile : 0);
     MfmaWeights<S> W;
-    mfma_load<S, false>(W, w, lane);
+    mfma_load<S>(W, w, lane);
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
     const float ak = act_k_of<Act>(m);
@@ -523,7 +518,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
 #pragma unroll
         for (int r = 0; r < 4; r++) cw[r] = (r == 0 && g < NO) ? m.cw[g] : 0.0f;
     } else {
-        lane_cw<NO>(m.cw, g, cw);
+        lane_cw<S>(m.cw, g, cw);
     }
     const int base = bid_x() * 256 + wave * 64;   // tile t: pixels base + 16 t + j
     float f[S::kMaxIn];
@@ -532,13 +527,13 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
         features<S>(m, PlainLatent{ zdec }, pr % m.W, pr / m.W, f);
     }
     float b[4][Q::kKs1];
-    tiles_of_lds<S>(f, b, tl, g, i16);
-    float t4[4][4];   // targets: lane (g, j) holds channels 4 g .. 4 g + 3 (VALU output layer: g) of pixel j of each tile
+    tiles_of<S>(f, b, tl, g, i16);
+    float t4[4][4];   // targets: lane (g, j) holds channels out_at(g, r) (VALU output layer: g) of pixel j of each tile
 #pragma unroll
     for (int t = 0; t < 4; t++) {
         const int pr = min(base + 16 * t + i16, m.npix - 1);
 #pragma unroll
-        for (int r = 0; r < 4; r++) t4[t][r] = tgt[(size_t)pr * NO + min(kVOut ? g : 4 * g + r, NO - 1)];
+        for (int r = 0; r < 4; r++) t4[t][r] = tgt[(size_t)pr * NO + (kVOut ? min(g, NO - 1) : max(out_at<S>(g, r), 0))];
     }
 #pragma unroll
     for (int c = 0; c < C0; c++) {
@@ -561,27 +556,27 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                 float lv[2];   // this lane's channels, then the pixel's lanes
                 if constexpr (kVOut) {
                     float x[2][Q::kKsH];
-                    mfma_hidden<S, 2, Act, false>(W, b2, ak, x);
+                    mfma_hidden<S, 2, Act>(W, b2, ak, x);
 #pragma unroll
                     for (int v = 0; v < 2; v++) {
-                        const float d = out_of<S>(valu_out_g_lds<S>(W, x[v], vo + v * kVoTile, g, i16), Clamp) - t4[t][0];
+                        const float d = out_of<S>(valu_out_g<S>(W, x[v], vo + v * kVoTile, g, i16), Clamp) - t4[t][0];
                         lv[v] = __fmul_rn(cw[0], __fmul_rn(d, d));   // cw (d d), main.cpp:2119
                     }
                 } else {
                     f4v o[2];
-                    mfma_forward<S, 2, Act, false>(W, b2, ak, o);
+                    mfma_forward<S, 2, Act>(W, b2, ak, o);
 #pragma unroll
                     for (int v = 0; v < 2; v++) {
                         lv[v] = 0.0f;
 #pragma unroll
-                        for (int r = 0; r < 4; r++) {
+                        for (int r = 0; r < out_regs<S>(); r++) {
                             const float d = out_of<S>(o[v][r], Clamp) - t4[t][r];
                             lv[v] = __builtin_fmaf(cw[r], __fmul_rn(d, d), lv[v]);
                         }
                     }
                 }
                 float ls[2];
-                group_sums_lds(lv[0], lv[1], sums, g, i16, ls[0], ls[1]);
+                group_sums(lv[0], lv[1], sums, g, i16, ls[0], ls[1]);
 #pragma unroll
                 for (int v = 0; v < 2; v++) {
                     const float l = ls[v];
