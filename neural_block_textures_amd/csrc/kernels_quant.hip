@@ -157,7 +157,26 @@ __device__ WaveSyms wave_quantize(const DevDct& D, const DctTables& T, float Cf,
         const float dD = cp * cp - (cp - vq) * (cp - vq);
         uint64_t mm = m, cut = 0;
         int next = 64;
-        while (mm) {   // uniform: the wave walks the block's nonzero ACs from the top
+        // Every nonzero's decision at once, as if every nonzero above it were kept: its next kept nonzero is
+        // then the nearest nonzero above it. Walking down from the top, that holds until the first cut, so
+        // the highest speculative cut is the walk's first cut and every decision above it is the walk's.
+        // Cuts are rare (most blocks have none): the walk below resumes only after a cut.
+        {
+            const uint64_t above = m & ~((2ull << lane) - 1ull);   // lane 63: 2 << 63 wraps to 0, nothing above
+            const int nx = above ? __builtin_ctzll(above) : 64;
+            const int sv = nx == 64 ? token - (lane == 63 ? 32 : 0) : token + c_run(nx - lane - 1) - c_run(nx - lane - 1 + r1 + 1);
+            const uint64_t cm = __ballot(((m >> lane) & 1ull) && dD < lam16 * (float)sv);
+            if (cm) {
+                const int p = 63 - __clzll((long long)cm);
+                cut = 1ull << p;
+                r.ntrunc = 1;
+                next = readlane_i(nx, p);   // p is cut: the next kept nonzero above the positions below it
+                mm = m & ((1ull << p) - 1ull);
+            } else {
+                mm = 0;
+            }
+        }
+        while (mm) {   // uniform: the wave walks the remaining nonzero ACs from the top
             const int p = 63 - __clzll((long long)mm);
             mm &= ~(1ull << p);
             const int tok = readlane_i(token, p), rr = readlane_i(r1, p);
