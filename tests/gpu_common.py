@@ -31,6 +31,9 @@ LAYOUTS = {
     "image3_27": Layout(64, 48, [(64, 48, 1, True), (8, 6, 4, False)], [27, 27], pos=[PK_LV1LOCAL], leak=1 / 1024),
     # README.md:620's 17-wide DCT decoder: 2 hidden tiles, the second with one unit
     "dct_17": Layout(64, 48, [(64, 48, 1, True), (16, 12, 4, False)], [17, 17], pos=[PK_LV1LOCAL], leak=1 / 1024),
+    # an 11-wide decoder (7-11-11-3): one partial hidden tile, so the population kernel's pixel-per-lane output layer
+    # with three k-steps of hidden inputs
+    "dct_11": Layout(64, 48, [(64, 48, 1, True), (16, 12, 4, False)], [11, 11], pos=[PK_LV1LOCAL], leak=1 / 1024),
     # README.md:991's 3-texture material (9 outputs) and README.md:298's 4-texture --qat 2 with a 4-channel block
     "run8x3": Layout(64, 48, [(32, 24, 8, False), (16, 12, 4, False)], [24, 24], T=3, weights=[1.0, 1.0, 0.5]),
     "mat_qat1x4_36": Layout(48, 40, [(48, 40, 1, True), (12, 10, 4, True)], [36, 36], T=4, pos=[PK_LV1LOCAL],
@@ -40,6 +43,8 @@ LAYOUTS = {
     "jit_valu_7": Layout(64, 48, [(16, 12, 4, False)], [7, 7], leak=0.01),
     "jit_mfma_28": Layout(48, 40, [(48, 40, 2, True), (12, 10, 4, False)], [28, 28], T=4, pos=[PK_LV1LOCAL], leak=0.01,
                           weights=[1.0, 0.5, 2.0, 1.0]),
+    # a 13-wide RGB decoder specialised at init: the pixel-per-lane output layer on a partial hidden tile
+    "jit_own_13": Layout(64, 48, [(16, 12, 4, False)], [13, 13], leak=0.01),
 }
 # the same layouts with every stage forced onto the VALU kernels (ntc_trainer_set_matrix_cores(0))
 for _name in ("material", "chief1_36"):

@@ -107,8 +107,8 @@ def test_mlp_es_small_batches(orc, name):
         assert np.array_equal(tr.download_model()[1], pw), (N, M)
 
 
-@pytest.mark.parametrize("name", ["rgb_16x2", "material", "runtime", "chief1_36", "dct_17", "material_valu", "jit_valu_7",
-                                  "jit_mfma_28", "jit_widths"])
+@pytest.mark.parametrize("name", ["rgb_16x2", "material", "runtime", "chief1_36", "dct_17", "dct_11", "material_valu", "jit_valu_7",
+                                  "jit_mfma_28", "jit_own_13", "jit_widths"])
 def test_mlp_es_two_steps_and_fd(orc, name):
     lay = LAYOUTS[name]
     say("mlp es+fd", name)

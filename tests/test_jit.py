@@ -11,6 +11,8 @@ from neural_block_textures_amd.trainer import PK_LV1LOCAL, Layout, Trainer
     Layout(64, 48, [(16, 12, 4, False)], [7, 7], leak=0.01),
     # 6-20-20-3 (58%, the output layer on the VALU)
     Layout(64, 48, [(16, 12, 4, False)], [20, 20], leak=0.01),
+    # 6-13-13-3: one partial hidden tile, the population kernel's pixel-per-lane output layer
+    Layout(64, 48, [(16, 12, 4, False)], [13, 13], leak=0.01),
     # 8-28-28-12 with --qat and lv1local: the matrix-core kernels too (84% useful)
     Layout(48, 40, [(48, 40, 2, True), (12, 10, 4, False)], [28, 28], T=4, pos=[PK_LV1LOCAL], leak=0.0),
     # 3 levels, clamp output, a leak outside [0, 1] (the selector search's general activation)
@@ -18,7 +20,7 @@ from neural_block_textures_amd.trainer import PK_LV1LOCAL, Layout, Trainer
     # hidden layers of different widths (FixedShapeW, VALU kernels only): 20,12 and a deeper 32,16,8
     Layout(32, 32, [(8, 8, 4, False)], [20, 12]),
     Layout(48, 40, [(48, 40, 2, True), (12, 10, 4, False)], [32, 16, 8], T=4, pos=[PK_LV1LOCAL], leak=0.01),
-], ids=["valu_7", "mfma_20", "mfma_28", "three_levels", "widths_20_12", "widths_32_16_8"])
+], ids=["valu_7", "mfma_20", "mfma_own_13", "mfma_28", "three_levels", "widths_20_12", "widths_32_16_8"])
 def test_specialised_kernels_compile(layout):
     sec, why = Trainer.jit_compile_check(Trainer.model_desc(layout))
     assert sec is not None, why
