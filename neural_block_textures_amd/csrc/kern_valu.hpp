@@ -14,12 +14,32 @@ namespace ntc_hip {
 constexpr int kTPB = 256;
 constexpr int kTPB_DCT = 64;   // the probe: one (block, channel) per thread
 
+// The Gaussians of an ES step whose population kernel reads them rather than drawing them per chunk (pair i,
+// weight k -> eps[i P + k]): blocks first_block and up of the minibatch launch draw them, an independent job
+// that would otherwise be a launch of its own. first_block past the grid: none.
+struct EpsJob {
+    NoiseFix nt;
+    uint64_t seed;
+    uint32_t step;
+    int N, P;
+    float* eps;
+    int first_block;
+};
+
 // The minibatch (draw_batch with the counter draw): slot s -> pixel, its feature column
 // feat[.][s] and target column btgt[.][s] (structure of arrays, so the evaluation reads coalesced).
 template <class S>
 __global__ void __launch_bounds__(kTPB) k_batch(DevModel m, uint64_t head, int M, int Mcap, const float* __restrict__ zdec,
                                                const float* __restrict__ tgt, int* __restrict__ bidx,
-                                               float* __restrict__ feat, float* __restrict__ btgt) {
+                                               float* __restrict__ feat, float* __restrict__ btgt, EpsJob ej) {
+    if ((int)blockIdx.x >= ej.first_block) {
+        const long long t = (long long)(blockIdx.x - ej.first_block) * kTPB + threadIdx.x;
+        if (t < (long long)ej.N * ej.P) {
+            const int i = (int)(t / ej.P), k = (int)(t - (long long)i * ej.P);
+            ej.eps[t] = gauss_at(ej.nt, noise_head(ej.seed, NS_MLP, ej.step, (uint32_t)i), (uint64_t)k);
+        }
+        return;
+    }
     const int s = blockIdx.x * kTPB + threadIdx.x;
     if (s >= M) return;
     const uint32_t u = (uint32_t)(noise_bits(head, (uint64_t)s) >> 32);

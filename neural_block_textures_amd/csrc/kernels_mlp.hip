@@ -31,15 +31,6 @@ __global__ void __launch_bounds__(kTPB) k_perturb(NoiseFix nt, uint64_t seed, ui
     wsets[(size_t)(2 * i + 1) * P + k] = __builtin_fmaf(-sigma, e, w);
 }
 
-// The Gaussians of one ES step alone (pair i, weight k), for population evaluations that stage the
-// member weights themselves from them.
-__global__ void __launch_bounds__(kTPB) k_mlp_eps(NoiseFix nt, uint64_t seed, uint32_t step, int N, int P, float* __restrict__ eps) {
-    const long long t = (long long)blockIdx.x * kTPB + threadIdx.x;
-    if (t >= (long long)N * P) return;
-    const int i = (int)(t / P), k = (int)(t - (long long)i * P);
-    eps[t] = gauss_at(nt, noise_head(seed, NS_MLP, step, (uint32_t)i), (uint64_t)k);
-}
-
 // Weight sets of one central-difference step: set pair j < P has w_j + h and w_j - h (float-realized,
 // main.cpp:1905), pair P holds two copies of w for the unperturbed loss; hh[j] = wp - wm in double.
 __global__ void __launch_bounds__(kTPB) k_fd_sets(int P, float h, const float* __restrict__ w0, float* __restrict__ wsets,
@@ -238,16 +229,19 @@ void launch_fill(Impl& I, float* p, size_t n, float v) {
     NTC_CHECK(hipGetLastError());
 }
 
-void launch_batch(Impl& I, int it, int M) {
+void launch_batch(Impl& I, int it, int M, int eps_pairs) {
     const uint64_t head = noise_head(I.d.seed, NS_BATCH_PIX, (uint32_t)it, 0);
+    const unsigned nb = blocks_for(M, kTPB);
+    EpsJob ej{ I.noise, I.d.seed, (uint32_t)it, eps_pairs, I.P, I.eps_mlp, (int)nb };
+    const unsigned grid = nb + (eps_pairs > 0 ? blocks_for((size_t)eps_pairs * I.P, kTPB) : 0u);
     ProfScope ps(I, "batch");
     if (I.jit) {
-        jit_launch(k_batch<ShapeDefault>, I, "k_batch", "", dim3(blocks_for(M, kTPB)), dim3(kTPB), 0, I.dm, head, M, I.Mcap, I.zdec,
-                   I.tgt, I.bidx, I.feat, I.btgt);
+        jit_launch(k_batch<ShapeDefault>, I, "k_batch", "", dim3(grid), dim3(kTPB), 0, I.dm, head, M, I.Mcap, I.zdec,
+                   I.tgt, I.bidx, I.feat, I.btgt, ej);
     } else dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
-        hipLaunchKernelGGL(k_batch<S>, dim3(blocks_for(M, kTPB)), dim3(kTPB), 0, I.stream, I.dm, head, M, I.Mcap, I.zdec, I.tgt,
-                           I.bidx, I.feat, I.btgt);
+        hipLaunchKernelGGL(k_batch<S>, dim3(grid), dim3(kTPB), 0, I.stream, I.dm, head, M, I.Mcap, I.zdec, I.tgt,
+                           I.bidx, I.feat, I.btgt, ej);
     });
     NTC_CHECK(hipGetLastError());
 }
@@ -257,14 +251,6 @@ void launch_perturb(Impl& I, int it, float sigma, int N) {
     ProfScope ps(I, "perturb");
     hipLaunchKernelGGL(k_perturb, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, I.noise, I.d.seed, (uint32_t)it, N, I.P,
                        sigma, I.w, I.wsets, I.eps_mlp);
-    NTC_CHECK(hipGetLastError());
-}
-
-void launch_mlp_eps(Impl& I, int it, int N) {
-    const size_t n = (size_t)N * I.P;
-    ProfScope ps(I, "perturb");
-    hipLaunchKernelGGL(k_mlp_eps, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, I.noise, I.d.seed, (uint32_t)it, N, I.P,
-                       I.eps_mlp);
     NTC_CHECK(hipGetLastError());
 }
 

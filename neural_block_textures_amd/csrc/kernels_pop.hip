@@ -98,11 +98,8 @@ void launch_pop_eval_es(Impl& I, int it, float sigma, int N, int M, int chunk, i
     PopSource src{};
     src.nt = I.noise; src.seed = I.d.seed; src.step = (uint32_t)it; src.sigma = sigma;
     src.w0 = I.w; src.eps = I.eps_mlp;
-    // with three or more chunks per pair, the Gaussians are drawn once (not once per chunk)
-    const bool once = chunks >= 3;
-    if (once) launch_mlp_eps(I, it, N);
     ProfScope ps(I, "pop_eval", true);
-    if (once) launch_pop_matrix<kReadEps>(I, src, N, M, chunk, chunks);
+    if (pop_reads_eps(chunks)) launch_pop_matrix<kReadEps>(I, src, N, M, chunk, chunks);   // drawn by the minibatch launch
     else launch_pop_matrix<kDraw>(I, src, N, M, chunk, chunks);
 }
 

@@ -502,11 +502,12 @@ void Trainer::mlp_step(int it, float sigma, float lr, int N, int M) {
                 I.pairs_cap, I.Mcap);
         exit(1);
     }
-    launch_batch(I, it, M);
     const int chunk = pop_chunk(I, N, M), chunks = (M + chunk - 1) / chunk;
+    const bool mfma = pop_on_matrix_cores(I);
+    launch_batch(I, it, M, mfma && pop_reads_eps(chunks) ? N : 0);   // with the Gaussians the population kernel reads
     ensure_part(I, (size_t)2 * N * chunks);
-    if (pop_on_matrix_cores(I)) {
-        launch_pop_eval_es(I, it, sigma, N, M, chunk, chunks);   // draws the perturbation itself
+    if (mfma) {
+        launch_pop_eval_es(I, it, sigma, N, M, chunk, chunks);   // stages the perturbed weights itself
     } else {
         ensure_wsets(I, (size_t)2 * N * I.P);
         launch_perturb(I, it, sigma, N);

@@ -188,10 +188,10 @@ std::vector<uint32_t> noise_fix_summary(const std::vector<uint32_t>& fix);
 
 // kernels_mlp.hip
 void launch_fill(Impl& I, float* p, size_t n, float v);
-void launch_batch(Impl& I, int it, int M);
+// the minibatch of step it; eps_pairs > 0: the same launch draws the step's Gaussians of that many pairs (EpsJob)
+void launch_batch(Impl& I, int it, int M, int eps_pairs = 0);
 void launch_perturb(Impl& I, int it, float sigma, int N);
 // the Gaussians of one ES step (NS_MLP, it, pair, k) into eps_mlp, N x P
-void launch_mlp_eps(Impl& I, int it, int N);
 void launch_fd_sets(Impl& I, float h);
 // which stages run on the matrix cores for this trainer's model
 bool pop_on_matrix_cores(const Impl& I);
@@ -201,7 +201,10 @@ void launch_qat_mfma(Impl& I);
 // minibatch slots per population-evaluation block for a population of `pairs` pairs
 int pop_chunk(const Impl& I, int pairs, int M);
 void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks);
-// the ES step's population evaluation with the perturbation drawn in the kernel (matrix-core shapes); fills eps_mlp
+// the ES step's population evaluation on the matrix cores, staging the members' weights itself: with three or more
+// chunks per pair it reads the step's Gaussians from eps_mlp, which the step's minibatch launch draws once
+// (launch_batch with eps_pairs = N), else each chunk-0 block draws its pair's and writes them to eps_mlp
+inline bool pop_reads_eps(int chunks) { return chunks >= 3; }
 void launch_pop_eval_es(Impl& I, int it, float sigma, int N, int M, int chunk, int chunks);
 void launch_pop_eval_valu(Impl& I, int pairs, int M, int chunk, int chunks);
 void launch_es_update(Impl& I, int chunks, double norm, float sigma, int N, float lr, int t);
