@@ -454,8 +454,7 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
             for (int ks = 0; ks < Q::kKs1; ks++) { b1[0][ks] = bp[t][ks]; b1[1][ks] = bm[t][ks]; }
             const int p = base + 16 * t + i16;
             // each lane's channel terms cw (d d) (its out_regs in ascending order, or its one on the VALU output
-            // layer), then the four lane groups added pairwise (permlane swaps): e+ in lanes 0-31, e- in
-            // lanes 32-63, then e+ - e-
+            // layer), then the pixel's four lane groups added pairwise for each member (group_sums), then e+ - e-
             float ep = 0.0f, em = 0.0f;
             if constexpr (kVOut) {
                 float x[2][Q::kKsH];
