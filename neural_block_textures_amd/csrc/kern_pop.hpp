@@ -483,7 +483,7 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
 // The selector search (qat_search, main.cpp:2088-2139) on the matrix cores, for a nearest level 0
 // of the image's size (each texel's cell is its own pixel): wave = 64 pixels in four 16-pixel tiles.
 // Every lane builds the features of its own pixel (features<S>) and tiles_of turns them into the four
-// tiles' B operands. Per channel and tile, every candidate value is one MLP evaluation of the tile with
+// tiles' B operands. Per tile and channel, every candidate value is one MLP evaluation of the tile with
 // that feature replaced (two candidates at a time). The choice is the reference's: the current grid
 // value first, then every other value with strict <, so the first strictly smaller loss wins
 // (main.cpp:2101-2132). The winner enters the features of the next channel and is written to the
@@ -527,38 +527,56 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
     }
     float b[4][Q::kKs1];
     tiles_of<S>(f, b, tl, g, i16);
-    float t4[4][4];   // targets: lane (g, j) holds channels out_at(g, r) (VALU output layer: g) of pixel j of each tile
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
+    // the targets of tile t: lane (g, j) holds channels out_at(g, r) (VALU output layer: g) of pixel j; loaded one
+    // tile ahead, so only the first tile's loads are waited for before the search starts
+    auto load_t = [&](int t, float (&tv)[4]) {
         const int pr = min(base + 16 * t + i16, m.npix - 1);
 #pragma unroll
-        for (int r = 0; r < 4; r++) t4[t][r] = tgt[(size_t)pr * NO + (kVOut ? min(g, NO - 1) : max(out_at<S>(g, r), 0))];
-    }
+        for (int r = 0; r < 4; r++) tv[r] = tgt[(size_t)pr * NO + (kVOut ? min(g, NO - 1) : max(out_at<S>(g, r), 0))];
+    };
+    // per channel: its bit depth, its grid, and the current grid index of the lane's own pixel
+    int bits[C0], cur_own[C0];
+    const float* gvs[C0];
 #pragma unroll
     for (int c = 0; c < C0; c++) {
-        const int bits = qat_bits[c], levels = (1 << bits) - 1;
-        const float* gv = grid + bits * 257;
-        // this channel's current value of every pixel, from the lane that built the pixel's features
-        const int cur_own = qat_index(f[c], bits);
+        bits[c] = qat_bits[c];
+        gvs[c] = grid + bits[c] * 257;
+        cur_own[c] = qat_index(f[c], bits[c]);
+    }
+    float tn[4];
+    load_t(0, tn);
+    // Tile by tile (a tile's pixels are independent of the other tiles'), each tile's channels in order: the winner of
+    // channel c enters the features of channel c + 1, as in the reference's per-texel loop.
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int cur = __builtin_amdgcn_ds_bpermute((16 * t + i16) << 2, cur_own);
-            float cur_l = 0.0f, best_l = 0.0f;
+    for (int t = 0; t < 4; t++) {
+        float tt[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) tt[r] = tn[r];
+        if (t + 1 < 4) load_t(t + 1, tn);
+#pragma unroll
+        for (int c = 0; c < C0; c++) {
+            const int levels = (1 << bits[c]) - 1;
+            const float* gv = gvs[c];
+            // the channel's current index of pixel j of tile t, from the lane that built the pixel's features
+            const int cur = __builtin_amdgcn_ds_bpermute((16 * t + i16) << 2, cur_own[c]);
+            // the losses and grid values of the current candidate and of the best other one so far: the winner's
+            // value comes from these registers, not from a load of the grid after the search
+            float cur_l = 0.0f, best_l = 0.0f, cur_v = 0.0f, best_v = 0.0f;
             int best_k = -1;
             for (int kc = 0; kc <= levels; kc += 2) {   // 2^bits candidates: two tiles at a time
+                const float gc[2] = { gv[kc], gv[kc + 1] };
                 float b2[2][Q::kKs1];
 #pragma unroll
                 for (int v = 0; v < 2; v++)
 #pragma unroll
-                    for (int ks = 0; ks < Q::kKs1; ks++) b2[v][ks] = b[t][ks];
-                if (g == c % 4) { b2[0][c / 4] = gv[kc]; b2[1][c / 4] = gv[kc + 1]; }
+                    for (int ks = 0; ks < Q::kKs1; ks++) b2[v][ks] = (ks == c / 4 && g == c % 4) ? gc[v] : b[t][ks];
                 float lv[2];   // this lane's channels, then the pixel's lanes
                 if constexpr (kVOut) {
                     float x[2][Q::kKsH];
                     mfma_hidden<S, 2, Act>(W, b2, ak, x);
 #pragma unroll
                     for (int v = 0; v < 2; v++) {
-                        const float d = out_of<S>(valu_out_g<S>(W, x[v], vo + v * kVoTile, g, i16), Clamp) - t4[t][0];
+                        const float d = out_of<S>(valu_out_g<S>(W, x[v], vo + v * kVoTile, g, i16), Clamp) - tt[0];
                         lv[v] = __fmul_rn(cw[0], __fmul_rn(d, d));   // cw (d d), main.cpp:2119
                     }
                 } else {
@@ -569,7 +587,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                         lv[v] = 0.0f;
 #pragma unroll
                         for (int r = 0; r < out_regs<S>(); r++) {
-                            const float d = out_of<S>(o[v][r], Clamp) - t4[t][r];
+                            const float d = out_of<S>(o[v][r], Clamp) - tt[r];
                             lv[v] = __builtin_fmaf(cw[r], __fmul_rn(d, d), lv[v]);
                         }
                     }
@@ -579,14 +597,15 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
 #pragma unroll
                 for (int v = 0; v < 2; v++) {
                     const float l = ls[v];
-                    if (kc + v == cur) cur_l = l;
-                    else if (best_k < 0 || l < best_l) { best_l = l; best_k = kc + v; }
+                    if (kc + v == cur) { cur_l = l; cur_v = gc[v]; }
+                    else if (best_k < 0 || l < best_l) { best_l = l; best_k = kc + v; best_v = gc[v]; }
                 }
             }
-            const int win = (best_k >= 0 && best_l < cur_l) ? best_k : cur;
-            if (g == c % 4) b[t][c / 4] = gv[win];
+            // cur is in 0 .. levels (qat_index clamps), so cur_v is its grid value
+            const float win_v = (best_k >= 0 && best_l < cur_l) ? best_v : cur_v;
+            if (g == c % 4) b[t][c / 4] = win_v;
             const int p = base + 16 * t + i16;
-            if (g == 0 && p < m.npix) zdec[m.lv[0].off + (size_t)p * m.lv[0].C + c] = gv[win];
+            if (g == 0 && p < m.npix) zdec[m.lv[0].off + (size_t)p * m.lv[0].C + c] = win_v;
         }
     }
 }
