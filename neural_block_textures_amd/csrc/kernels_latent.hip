@@ -41,15 +41,33 @@ __global__ void __launch_bounds__(kTPB) k_lat_eps(NoiseFix nt, DevModel m, uint6
 // of four pairs at once (each sum in raster order), then apply the four pairs in order to the texels'
 // channels (four threads per texel, each on every fourth channel). A texel's gradient is then final
 // (one block owns it), so with `adam` the block also takes the texel's Adam step (the latent ES step's
-// update, main.cpp:2036-2037).
-constexpr int kGatherTex = 16, kGatherPairs = 4, kGatherRun = 32;
+// update, main.cpp:2036-2037). With `first` the gradient starts from zero rather than from grad (the step's
+// first group of pairs).
+//
+// Blocks past the gather's own (blockIdx.x >= gblocks) draw the next latent step's Gaussians for the perturbed
+// levels (the entries lo .. hi - 1 whose level is in `mask`; block d = pair d / eb, entries lo + 128 (d % eb) ..):
+// the values k_lat_eps would draw for step next_step, written to eps_next. They run beside the gather's blocks,
+// which leave most of the chip idle, so the next step needs no draw launch of its own.
+constexpr int kGatherTex = 16, kGatherPairs = 4, kGatherRun = 32, kAheadPerBlock = 128;
+struct LatAhead {
+    NoiseFix nt; uint64_t seed; uint32_t next_step; unsigned mask;
+    float* eps_next; int gblocks, eb; long long lo, hi;
+};
 __global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevModel m, int level, int K, float scale,
                                                                          const float* __restrict__ dpix,
                                                                          const float* __restrict__ eps, const int* __restrict__ ranges,
                                                                          int rate, float rate_scale, int dct_bw, int dct_n,
                                                                          const int32_t* __restrict__ dbits, float* __restrict__ grad,
-                                                                         int adam, float* __restrict__ z, float* __restrict__ zm,
-                                                                         float* __restrict__ zv, float lr, float c1, float c2) {
+                                                                         int first, int adam, float* __restrict__ z, float* __restrict__ zm,
+                                                                         float* __restrict__ zv, float lr, float c1, float c2, LatAhead ah) {
+    if ((int)blockIdx.x >= ah.gblocks) {   // a draw-ahead block (uniform: the whole block returns here)
+        const int d = (int)blockIdx.x - ah.gblocks, k = d / ah.eb;
+        const uint64_t head = noise_head(ah.seed, NS_LAT, ah.next_step, (uint32_t)k);
+        const long long i0 = ah.lo + (long long)(d - k * ah.eb) * kAheadPerBlock, i1 = min(ah.hi, i0 + kAheadPerBlock);
+        for (long long i = i0 + threadIdx.x; i < i1; i += kGatherTex * kGatherPairs)
+            if ((ah.mask >> level_of(m, i)) & 1u) ah.eps_next[(size_t)k * m.nz + i] = gauss_at(ah.nt, head, (uint64_t)i);
+        return;
+    }
     __shared__ float dsum[kGatherPairs][kGatherTex];
     const DevLevel& L = m.lv[level];
     const int j = threadIdx.x % kGatherTex, q = threadIdx.x / kGatherTex;
@@ -110,7 +128,7 @@ __global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevMod
             const bool last = k0 + kGatherPairs >= K;
             for (int c = q; c < L.C; c += kGatherPairs) {
                 const size_t i = (size_t)(base + c);
-                float gc = grad[i];
+                float gc = (first && k0 == 0) ? 0.0f : grad[i];
                 for (int kk = 0; kk < kn; kk++) {
                     const float ei = eps[(size_t)(k0 + kk) * m.nz + i];
                     gc = __builtin_fmaf(dsum[kk][j] * scale, ei, gc);
@@ -147,15 +165,34 @@ void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask) {
     NTC_CHECK(hipGetLastError());
 }
 
-void launch_lat_gather(Impl& I, int level, int k0, int K, float scale, bool rate, float lr, int t) {
+void launch_lat_gather(Impl& I, int level, int k0, int K, float scale, bool rate, float lr, int t, int ahead_K, unsigned mask) {
     const size_t ntx = (size_t)I.d.lv[level].W * I.d.lv[level].H;
     const float c1 = t > 0 ? 1.0f - powf(0.9f, (float)t) : 1.0f, c2 = t > 0 ? 1.0f - powf(0.999f, (float)t) : 1.0f;
+    LatAhead ah{};
+    ah.gblocks = blocks_for(ntx, kGatherTex);
+    ah.eb = 1;
+    size_t grid = (size_t)ah.gblocks;
+    if (ahead_K > 0) {   // the next step's Gaussians: the range of entries the perturbed levels span
+        ah.nt = I.noise; ah.seed = I.d.seed; ah.next_step = (uint32_t)(I.lat_step_no + 1); ah.mask = mask; ah.eps_next = I.eps_ahead;
+        ah.lo = (long long)I.nz; ah.hi = 0;
+        for (int l = 0; l < I.d.nlev; l++)
+            if ((mask >> l) & 1u) {
+                ah.lo = std::min<long long>(ah.lo, I.dm.lv[l].off);
+                ah.hi = std::max<long long>(ah.hi, I.dm.lv[l].off + (long long)I.d.lv[l].W * I.d.lv[l].H * I.d.lv[l].C);
+            }
+        ah.eb = blocks_for((size_t)(ah.hi - ah.lo), kAheadPerBlock);
+        grid += (size_t)ah.eb * (size_t)ahead_K;
+        if (grid > 0x7fffffff) {
+            fprintf(stderr, "ntc_hip backend: latent gather launch of %zu blocks\n", grid);
+            exit(1);
+        }
+    }
     ProfScope ps(I, "lat_gather");
-    hipLaunchKernelGGL(k_lat_gather, dim3(blocks_for(ntx, kGatherTex)), dim3(kGatherTex * kGatherPairs), 0, I.stream, I.dm, level, K,
+    hipLaunchKernelGGL(k_lat_gather, dim3((unsigned)grid), dim3(kGatherTex * kGatherPairs), 0, I.stream, I.dm, level, K,
                        scale, I.dpix, I.eps_lat,
                        I.ranges, rate ? 1 : 0, I.ddct.rate_scale, I.ddct.BW, I.ddct.n, rate ? I.dct_dbits + (size_t)k0 * I.ddct.n : nullptr,
-                       I.zgrad, t > 0 ? 1 : 0, I.z, I.zm,
-                       I.zv, lr, c1, c2);
+                       I.zgrad, k0 == 0 ? 1 : 0, t > 0 ? 1 : 0, I.z, I.zm,
+                       I.zv, lr, c1, c2, ah);
     NTC_CHECK(hipGetLastError());
 }
 

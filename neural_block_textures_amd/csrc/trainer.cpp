@@ -85,11 +85,13 @@ int lat_group_of(const Impl& I, int K) {
 }
 void ensure_lat(Impl& I, int G, int K) {
     if (G > I.Kcap) {
-        dev_free(I.eps_lat); dev_free(I.dpix);
+        dev_free(I.eps_lat); dev_free(I.dpix); dev_free(I.eps_ahead);
+        I.ahead_step = -1;
         I.Kcap = G;
         dev_alloc(&I.eps_lat, (size_t)G * I.nz);
         dev_alloc(&I.dpix, (size_t)G * I.npix);
     }
+    if (G >= K && !I.eps_ahead) dev_alloc(&I.eps_ahead, (size_t)I.Kcap * I.nz);   // a one-group step draws the next one's Gaussians
     if (I.dct && K > I.Dcap) {
         dev_free(I.dct_dbits);
         I.Dcap = K;
@@ -197,7 +199,7 @@ Trainer::~Trainer() {
         dev_free(I.w); dev_free(I.wgrad); dev_free(I.wm); dev_free(I.wv);
         dev_free(I.tgt); dev_free(I.img); dev_free(I.feat); dev_free(I.btgt); dev_free(I.bidx);
         dev_free(I.wsets); dev_free(I.eps_mlp); dev_free(I.gpart); dev_free(I.part); dev_free(I.dl); dev_free(I.lsum); dev_free(I.hh);
-        dev_free(I.eps_lat); dev_free(I.dpix); dev_free(I.ranges); dev_free(I.qat_grid); dev_free(I.qat_bits);
+        dev_free(I.eps_lat); dev_free(I.eps_ahead); dev_free(I.dpix); dev_free(I.ranges); dev_free(I.qat_grid); dev_free(I.qat_bits);
         dev_free(I.qes_dev); dev_free(I.qgrid);
         dev_free(I.zpost); dev_free(I.st_part); dev_free(I.st_keys); dev_free(I.st_hist); dev_free(I.st_dct); dev_free(I.st_sse);
         dev_free(I.dct_sym); dev_free(I.dct_code); dev_free(I.dct_step); dev_free(I.dct_bits); dev_free(I.dct_dbits); dev_free(I.dct_tn); dev_free(I.dct_probe_code); dev_free(I.dct_gain);
@@ -587,16 +589,29 @@ void Trainer::lat_step(int /*it*/, float sigma, float lr, int K) {
         // last group's gathers. The other levels' gradients are zero at every step of this trainer (the mask is
         // fixed by --qat at init), so their Adam moments stay zero and the reference's step leaves them exactly
         // as they are: it is skipped.
+        //
+        // A step that runs as one group has the next step's Gaussians drawn by its last gather launch (for step
+        // lat_step_no + 1 and the same K): the next step then swaps them in and launches no draw of its own. The
+        // first group's gathers start the gradient from zero, so the cleared zgrad of k_lat_eps is not needed then
+        // (the levels outside the mask keep the zeros of the first step's draw: nothing writes them).
+        const bool ahead = I.ahead_step == I.lat_step_no && I.ahead_K == K && G >= K && I.eps_ahead;
+        if (ahead) std::swap(I.eps_lat, I.eps_ahead);
+        int last_level = 0;
+        for (int l = 0; l < I.d.nlev; l++) if ((mask >> l) & 1u) last_level = l;
         for (int k0 = 0; k0 < K; k0 += G) {
             const int g = std::min(G, K - k0);
             const bool last = k0 + g == K;
-            launch_lat_eps(I, k0, g, mask);   // the first group also clears zgrad
+            if (!(ahead && k0 == 0)) launch_lat_eps(I, k0, g, mask);   // the first group also clears zgrad
             launch_lat_pair(I, g, sigma, mask);
             I.lat_last_K = g;
             if (rate) launch_dct_rate_pairs(I, k0, g, sigma);
             for (int l = 0; l < I.d.nlev; l++)
-                if ((mask >> l) & 1u) launch_lat_gather(I, l, k0, g, scale, rate && l == 0, lr, last ? I.lat_t : 0);
+                if ((mask >> l) & 1u)
+                    launch_lat_gather(I, l, k0, g, scale, rate && l == 0, lr, last ? I.lat_t : 0,
+                                      (G >= K && l == last_level) ? K : 0, mask);
         }
+        I.ahead_step = G >= K ? I.lat_step_no + 1 : -1;
+        I.ahead_K = K;
         if (rate) I.dct_last_K = K;
     } else {
         launch_adam(I, I.z, I.zgrad, I.zm, I.zv, I.nz, lr, ++I.lat_t);

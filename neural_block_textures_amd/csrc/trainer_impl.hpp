@@ -80,6 +80,10 @@ struct ntc_cuda::Trainer::Impl {
     int pairs_cap = 0;
     float *eps_lat = nullptr, *dpix = nullptr;   // one group of pairs of a latent step: Kcap x nz, Kcap x W*H
     int Kcap = 0;
+    // The next latent step's Gaussians, drawn ahead by this step's last gather launch (extra blocks beside the
+    // gather's) when the step ran as one group: valid for step ahead_step with ahead_K pairs (-1: none).
+    float* eps_ahead = nullptr;
+    int ahead_step = -1, ahead_K = 0;
     int lat_group = 0;         // pairs per latent group (0: as many as kLatGroupBytes of eps_lat + dpix hold)
     int Dcap = 0;              // pairs dct_dbits holds
     int* ranges = nullptr;     // per level: xb[W] xe[W] yb[H] ye[H] (pixel footprint of each texel row / column)
@@ -223,7 +227,8 @@ void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask);
 void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask);
 // the footprint gather of one level for the group of pairs k0 .. k0 + K - 1 (added to the gradient so far); with
 // t > 0 (the step's last group) also the Adam step t (learning rate lr) of its texels
-void launch_lat_gather(Impl& I, int level, int k0, int K, float scale, bool rate, float lr = 0.0f, int t = 0);
+void launch_lat_gather(Impl& I, int level, int k0, int K, float scale, bool rate, float lr = 0.0f, int t = 0, int ahead_K = 0,
+                       unsigned mask = 0);
 void launch_qat_search(Impl& I);
 
 // kernels_quant.hip
