@@ -45,6 +45,25 @@ def test_grouped_latent_steps_equal(orc, name, K, G):
     b.close()
 
 
+def test_drawn_ahead_gaussians_follow_the_pair_count(orc):
+    """A step that runs as one group draws the next step's latent Gaussians (step + 1, the same pair count) in its last
+    gather launch. Steps whose pair count changes draw their own instead. Against a trainer that never draws ahead
+    (one pair per group), every step's gradient and latent are equal bit for bit, across both kinds of step."""
+    lay = LAYOUTS["two_level"]
+    say("latent draw-ahead", "two_level")
+    z, p, tgt = data(lay, 5)
+    a = trainer(lay, z, p, tgt)
+    b = trainer(lay, z, p, tgt)
+    b.set_lat_group(1)
+    for it, K in enumerate((4, 4, 6, 6, 6, 3, 4), start=1):
+        a.lat_step(it, 0.05, 0.02, K)
+        b.lat_step(it, 0.05, 0.02, K)
+        assert np.array_equal(bits(a.debug_last_zgrad()), bits(b.debug_last_zgrad())), (it, K)
+        assert np.array_equal(bits(a.download_model()[0]), bits(b.download_model()[0])), (it, K)
+    a.close()
+    b.close()
+
+
 def test_grouped_latent_step_dct_rate(orc):
     """a live --dct-q level 0 with the rate term: every group's rate pass writes its pairs' bit differences, so the
     step's hit count, the last pair's differences and the gradient are the ungrouped step's"""
