@@ -10,7 +10,9 @@ MLP ES step, latent ES step, then the --qat selector search when the workload ha
     python bench.py [--steps K] [--warmup W] [--workload material512]
     python bench.py --all-configs profiles/es_iterations_all_configs.md
 
-The default run prints one JSON line for material512. value = every member-pixel MLP evaluation
+Untimed iterations run for --settle seconds (default 1) before the W warm-up steps, so that the K timed steps see
+the steady state of a training run rather than a process's first iterations. The default run prints one JSON line
+for material512. value = every member-pixel MLP evaluation
 of the timed iterations (population, latent pairs, selector search) per second of wall time;
 roofline = the population-evaluation kernel's algorithmic FP32 FLOP per launch over its mean launch
 time (HIP events on the trainer's stream), against the MI355X FP32 peak. --all-configs runs each of
@@ -255,13 +257,26 @@ def cpu_refit_ms(w, r):
     return 1e3 * (time.perf_counter() - t0)
 
 
-def run_gpu(w, steps, warmup, fd_steps=0, seconds=0.0):
-    """GPU ES iterations of workload w; with seconds > 0 the step count is chosen to time about that long."""
+def run_gpu(w, steps, warmup, fd_steps=0, seconds=0.0, settle=0.0):
+    """GPU ES iterations of workload w; with seconds > 0 the step count is chosen to time about that long.
+
+    settle: untimed iterations, in groups of 8, until this many seconds of wall time have passed, before the warm-up
+    steps. On the MI355X the first hundred-odd material512 iterations of a process run slower than the later ones
+    (population launch 1.022-1.034 ms after 5 warm-up iterations, 1.007 ms after 200), so a short timed region right
+    after a short warm-up would time that start rather than the training loop's steady state."""
     import numpy as np
     z, p, tgt = inputs(w)
     tr = make_trainer(w, z, p, tgt)
     log(f"bench: {w.name}:", tr.banner())
     it = 0
+    settle_iters = 0
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < settle:
+        for _ in range(8):
+            it += 1
+            es_iter(tr, w, it)
+        settle_iters += 8
+        tr.synchronize()
     for _ in range(warmup):
         it += 1
         es_iter(tr, w, it)
@@ -345,7 +360,7 @@ def run_gpu(w, steps, warmup, fd_steps=0, seconds=0.0):
     assert np.isfinite(img).all() and np.isfinite(loss)
     name = "k_pop_mfma" if tr.on_matrix_cores("pop_eval") else "k_pop_eval"
     out = {"z": z, "p": p, "tgt": tgt, "steps": steps, "el": el, "kernels": kernels, "fd": fd, "loss": loss, "pop_kernel": name,
-           "refit": refit, "dct_codes": getattr(tr, "dct_codes", None)}
+           "refit": refit, "dct_codes": getattr(tr, "dct_codes", None), "settle": {"seconds": settle, "iterations": settle_iters}}
     if w.dct_q:
         out["host_state"] = (tr.download_model(), tr.download_zq())
     tr.close()
@@ -377,7 +392,7 @@ def all_configs(out_path: str, cpu_seconds: float):
     from neural_block_textures_amd.configs import workloads
     rows = []
     for name, w in workloads().items():
-        r = run_gpu(w, 0, 3, seconds=2.0)
+        r = run_gpu(w, 0, 3, seconds=2.0, settle=1.0)
         gpu_its = r["steps"] / r["el"]
         ev = evals_per_iter(w)
         # a population too large for a bounded CPU sample (over about 4 TFLOP per iteration) is sampled with 64 pairs
@@ -423,6 +438,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="material512")
     ap.add_argument("--fd-steps", type=int, default=5, help="extra timed --mlp-fd iterations, reported apart")
+    ap.add_argument("--settle", type=float, default=1.0, metavar="SECONDS",
+                    help="untimed iterations for this long before the warm-up steps (steady-state clocks; 0 = none)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--all-configs", metavar="OUT_MD", help="run the five workloads and write a table")
     ap.add_argument("--valu", action="store_true",
@@ -470,7 +487,7 @@ def main():
     lay = w.layout
     log(f"bench: {w.name} {lay.W}x{lay.H}x{lay.T} levels {lay.levels} mlp {lay.nin}->{lay.hidden}->{lay.nout} "
         f"pairs {w.mlp_pairs} batch {w.mlp_batch}")
-    r = run_gpu(w, args.steps, args.warmup, fd_steps=args.fd_steps)
+    r = run_gpu(w, args.steps, args.warmup, fd_steps=args.fd_steps, settle=args.settle)
     cpu = None
     if args.cpu_seconds > 0:
         log(f"bench: CPU baseline for {args.cpu_seconds:.0f} s ...")
@@ -494,6 +511,7 @@ def main():
         "fd_phase": r["fd"],
         "kernels": r["kernels"],
         "batch_loss": r["loss"],
+        "settle": r["settle"],
     }
     print(json.dumps(out), flush=True)
 
