@@ -232,6 +232,50 @@ def test_rgb256_fixed_seed_psnr(orc):
     assert abs(ps_g - ps_c) <= 0.05
 
 
+@pytest.mark.skipif(not have_reference(fast=True), reason="the reference's CPU loop is built only where the reference tree is")
+def test_material512_fixed_seed_psnr(orc):
+    """material512 (the headline workload: four 512x512 maps, --qat 2,2 on level 0, population 8192 on 4096-pixel
+    minibatches) trained for 20 iterations at its fixed seed on the device and by the reference's own CPU training
+    loop (main.cpp's MlpTrainer / LatentTrainer / qat_search in main.cpp:4121-4148's order, -O3 -ffast-math,
+    --rng hash), from the same initial model: the final PSNRs must agree within 0.05 dB (README.md:964-970)."""
+    iters = 20
+    w, lay, tr, z, p, tgt = full_trainer("material512")
+    ref = reference(fast=True)
+    cfg = OrTrainCfg()
+    cfg.seed, cfg.mlp_pairs, cfg.mlp_batch, cfg.mlp_sigma, cfg.mlp_lr = w.seed, w.mlp_pairs, w.mlp_batch, w.mlp_sigma, w.mlp_lr
+    cfg.lat_pairs, cfg.lat_sigma, cfg.lat_lr, cfg.fd_from, cfg.fd_h = w.lat_pairs, w.lat_sigma, w.lat_lr, iters + 1, w.fd_h
+    cfg.qat = max(w.qat_bits)
+    for c, b in enumerate(w.qat_bits):
+        cfg.qat_ch[c] = b
+    mc = model_of(lay)
+    h = ref.lib.ref_train_create(C.byref(mc), C.byref(cfg), z.ctypes.data, p.ctypes.data, tgt.ctypes.data)
+    t0 = time.time()
+    try:
+        for it in range(1, iters + 1):
+            ref.lib.ref_train_iter(h, it, iters)
+            if it % 5 == 0:
+                say(f"material512 reference CPU loop: iteration {it} ({time.time() - t0:.1f} s)")
+        zr, pr = np.empty_like(z), np.empty_like(p)
+        ref.lib.ref_train_get(h, zr.ctypes.data, pr.ctypes.data)
+    finally:
+        ref.lib.ref_train_destroy(h)
+    t1 = time.time()
+    for it in range(1, iters + 1):
+        tr.mlp_step(it, w.mlp_sigma, w.mlp_lr, w.mlp_pairs, w.mlp_batch)
+        tr.lat_step(it, w.lat_sigma, w.lat_lr, w.lat_pairs)
+        tr.qat_search()
+    img = tr.decode_full()
+    t2 = time.time()
+    mse_0, ps_0 = mse_psnr(orc, orc.decode_full(lay, p, z), tgt, lay)
+    mse_c, ps_c = mse_psnr(orc, orc.decode_full(lay, pr, zr), tgt, lay)
+    mse_g, ps_g = mse_psnr(orc, img, tgt, lay)
+    say(f"material512 {iters} iterations, seed {w.seed}: start psnr {ps_0:.3f} dB; reference CPU loop mse {mse_c:.3f} psnr "
+        f"{ps_c:.3f} dB ({t1 - t0:.1f} s); device mse {mse_g:.3f} psnr {ps_g:.3f} dB ({t2 - t1:.2f} s); "
+        f"delta {ps_g - ps_c:+.4f} dB")
+    assert ps_c > ps_0 + 0.5                            # training moved
+    assert abs(ps_g - ps_c) <= 0.05
+
+
 def test_material512_selectors_full_size(orc):
     """One selector search (--qat 2,2, qat_search main.cpp:2088-2139) at material512's full size (262144 texels x
     2 channels, 12 outputs), after a few training iterations on the device, against the oracle's search of the
