@@ -276,6 +276,84 @@ def test_material512_fixed_seed_psnr(orc):
     assert abs(ps_g - ps_c) <= 0.05
 
 
+def _reference_loop(w, lay, z, p, tgt, iters, dct=None):
+    """the reference's own CPU training loop (libntc_ref_fast.so, --rng hash) for `iters` iterations from (z, p):
+    the final shadow and weights"""
+    ref = reference(fast=True)
+    cfg = OrTrainCfg()
+    cfg.seed, cfg.mlp_pairs, cfg.mlp_batch, cfg.mlp_sigma, cfg.mlp_lr = w.seed, w.mlp_pairs, w.mlp_batch, w.mlp_sigma, w.mlp_lr
+    cfg.lat_pairs, cfg.lat_sigma, cfg.lat_lr, cfg.fd_from, cfg.fd_h = w.lat_pairs, w.lat_sigma, w.lat_lr, iters + 1, w.fd_h
+    cfg.qat = max(w.qat_bits) if w.qat_bits else 0
+    for c, b in enumerate(w.qat_bits or []):
+        cfg.qat_ch[c] = b
+    mc = model_of(lay)
+    if dct is None:
+        h = ref.lib.ref_train_create(C.byref(mc), C.byref(cfg), z.ctypes.data, p.ctypes.data, tgt.ctypes.data)
+    else:
+        h = ref.lib.ref_train_create_dct(C.byref(mc), C.byref(cfg), z.ctypes.data, p.ctypes.data, tgt.ctypes.data, C.byref(dct.d),
+                                         C.c_float(0.5), 1, 1)
+    t0 = time.time()
+    try:
+        for it in range(1, iters + 1):
+            ref.lib.ref_train_iter(h, it, iters)
+        zr, pr = np.empty_like(z), np.empty_like(p)
+        ref.lib.ref_train_get(h, zr.ctypes.data, pr.ctypes.data)
+    finally:
+        ref.lib.ref_train_destroy(h)
+    return zr, pr, time.time() - t0
+
+
+@pytest.mark.skipif(not have_reference(fast=True), reason="the reference's CPU loop is built only where the reference tree is")
+def test_rgb512_two_level_fixed_seed_psnr(orc):
+    """rgb512_two_level (two bilinear levels, 32-wide MLP, population 1024 on 64K-pixel minibatches) trained for 10
+    iterations at its fixed seed on the device and by the reference's own CPU loop: final PSNRs within 0.05 dB."""
+    iters = 10
+    w, lay, tr, z, p, tgt = full_trainer("rgb512_two_level")
+    zr, pr, el = _reference_loop(w, lay, z, p, tgt, iters)
+    for it in range(1, iters + 1):
+        tr.mlp_step(it, w.mlp_sigma, w.mlp_lr, w.mlp_pairs, w.mlp_batch)
+        tr.lat_step(it, w.lat_sigma, w.lat_lr, w.lat_pairs)
+    img = tr.decode_full()
+    _, ps_0 = mse_psnr(orc, orc.decode_full(lay, p, z), tgt, lay)
+    mse_c, ps_c = mse_psnr(orc, orc.decode_full(lay, pr, zr), tgt, lay)
+    mse_g, ps_g = mse_psnr(orc, img, tgt, lay)
+    say(f"rgb512_two_level {iters} iterations, seed {w.seed}: start psnr {ps_0:.3f} dB; reference CPU loop mse {mse_c:.3f} "
+        f"psnr {ps_c:.3f} dB ({el:.1f} s); device mse {mse_g:.3f} psnr {ps_g:.3f} dB; delta {ps_g - ps_c:+.4f} dB")
+    assert ps_c > ps_0 + 0.5
+    assert abs(ps_g - ps_c) <= 0.05
+
+
+@pytest.mark.skipif(not have_reference(fast=True), reason="the reference's CPU loop is built only where the reference tree is")
+def test_dct512_fixed_seed_psnr(orc):
+    """dct512 (a --dct-q 50 plane as level 0 with the rate proxy in the objective, scale codes from the device's
+    decoder-sensitivity probe) trained for 20 iterations at its fixed seed on the device and by the reference's own
+    CPU loop with the same DCT state (codes, steps, --dct-lambda 0.5 with both parts): the final PSNRs of the decoded
+    (snapped) models within 0.05 dB."""
+    iters = 20
+    w, lay, tr, z, p, tgt = full_trainer("dct512")
+    H = HostDct(orc, lay, w.dct_q, deadzone=0, lam=0.5, lo16=4, rate="both")
+    code_d, _ = tr.dct_probe()
+    H.code[:] = code_d
+    zd, _ = tr.download_model()                       # the shadow as the trainer holds it (level 0 clamped)
+    H.snap(zd)
+    tr.set_dct(H.desc(), H.code, H.sym, H.steps)
+    zr, pr, el = _reference_loop(w, lay, zd, p, tgt, iters, dct=H)
+    for it in range(1, iters + 1):
+        tr.mlp_step(it, w.mlp_sigma, w.mlp_lr, w.mlp_pairs, w.mlp_batch)
+        tr.lat_step(it, w.lat_sigma, w.lat_lr, w.lat_pairs)
+    img = tr.decode_full()
+    n0 = lay.levels[0][0] * lay.levels[0][1] * lay.levels[0][2]
+    _, zq_r, _, _ = H.snap(zr)                        # the reference's final plane, snapped with the same codes
+    _, zq_0, _, _ = H.snap(zd)
+    _, ps_0 = mse_psnr(orc, orc.decode_full(lay, p, np.concatenate([zq_0, zd[n0:]])), tgt, lay)
+    mse_c, ps_c = mse_psnr(orc, orc.decode_full(lay, pr, np.concatenate([zq_r, zr[n0:]])), tgt, lay)
+    mse_g, ps_g = mse_psnr(orc, img, tgt, lay)
+    say(f"dct512 {iters} iterations, seed {w.seed}: start psnr {ps_0:.3f} dB; reference CPU loop mse {mse_c:.3f} psnr "
+        f"{ps_c:.3f} dB ({el:.1f} s); device mse {mse_g:.3f} psnr {ps_g:.3f} dB; delta {ps_g - ps_c:+.4f} dB")
+    assert ps_c > ps_0 + 0.5
+    assert abs(ps_g - ps_c) <= 0.05
+
+
 def test_material512_selectors_full_size(orc):
     """One selector search (--qat 2,2, qat_search main.cpp:2088-2139) at material512's full size (262144 texels x
     2 channels, 12 outputs), after a few training iterations on the device, against the oracle's search of the
