@@ -484,7 +484,9 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
 // of the image's size (each texel's cell is its own pixel): wave = 64 pixels in four 16-pixel tiles.
 // Every lane builds the features of its own pixel (features<S>) and tiles_of turns them into the four
 // tiles' B operands. Per tile and channel, every candidate value is one MLP evaluation of the tile with
-// that feature replaced (two candidates at a time). The choice is the reference's: the current grid
+// that feature replaced (two candidates at a time); the first layer's sums over the other inputs are formed
+// once per tile and channel and the candidate's term is added to them last (the reference adds it in input
+// order, main.cpp:603-627: the same products, one rounding order apart). The choice is the reference's: the current grid
 // value first, then every other value with strict <, so the first strictly smaller loss wins
 // (main.cpp:2101-2132). The winner enters the features of the next channel and is written to the
 // decode buffer. A candidate's loss is the pixel's float sum of cw (d d) over its channels (a lane's
@@ -563,17 +565,36 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
             // value comes from these registers, not from a load of the grid after the search
             float cur_l = 0.0f, best_l = 0.0f, cur_v = 0.0f, best_v = 0.0f;
             int best_k = -1;
+            // The first layer's sums of the tile without input c (a zero in its place: fma(w, 0, s) = s) and, in D
+            // layout, the weight of input c into each of this lane's units (read from the lane of W.a1 that holds
+            // it): a candidate's first-layer pre-activations are then one fused multiply-add, w_c gc + base, and
+            // the matrix cores take only the layers after the first for each candidate.
+            f4v s1[1][Q::kHt];
+            {
+                float b0[1][Q::kKs1];
+#pragma unroll
+                for (int ks = 0; ks < Q::kKs1; ks++) b0[0][ks] = (ks == c / 4 && g == c % 4) ? 0.0f : b[t][ks];
+                mfma_layer1<S, 1>(W, b0, s1);
+            }
+            float w1c[Q::kHt][4];
+#pragma unroll
+            for (int ot = 0; ot < Q::kHt; ot++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    w1c[ot][r] = __int_as_float(__builtin_amdgcn_ds_bpermute(((c % 4) * 16 + 4 * g + r) << 2, __float_as_int(W.a1[ot][c / 4])));
             for (int kc = 0; kc <= levels; kc += 2) {   // 2^bits candidates: two tiles at a time
                 const float gc[2] = { gv[kc], gv[kc + 1] };
-                float b2[2][Q::kKs1];
+                f4v a1[2][Q::kHt];
 #pragma unroll
                 for (int v = 0; v < 2; v++)
 #pragma unroll
-                    for (int ks = 0; ks < Q::kKs1; ks++) b2[v][ks] = (ks == c / 4 && g == c % 4) ? gc[v] : b[t][ks];
+                    for (int ot = 0; ot < Q::kHt; ot++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) a1[v][ot][r] = __builtin_fmaf(w1c[ot][r], gc[v], s1[0][ot][r]);
                 float lv[2];   // this lane's channels, then the pixel's lanes
+                float x[2][Q::kKsH];
+                mfma_hidden_from1<S, 2, Act>(W, a1, ak, x);
                 if constexpr (kVOut) {
-                    float x[2][Q::kKsH];
-                    mfma_hidden<S, 2, Act>(W, b2, ak, x);
 #pragma unroll
                     for (int v = 0; v < 2; v++) {
                         const float d = out_of<S>(valu_out_g<S>(W, x[v], vo + v * kVoTile, g, i16), Clamp) - tt[0];
@@ -581,7 +602,7 @@ __global__ void __launch_bounds__(256) k_qat_mfma(DevModel m, const float* __res
                     }
                 } else {
                     f4v o[2];
-                    mfma_forward<S, 2, Act>(W, b2, ak, o);
+                    mfma_output<S, 2>(W, x, o);
 #pragma unroll
                     for (int v = 0; v < 2; v++) {
                         lv[v] = 0.0f;

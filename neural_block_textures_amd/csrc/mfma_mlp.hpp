@@ -308,29 +308,34 @@ __device__ __forceinline__ void scale_hidden(MfmaWeights<S>& W, float b) {
 // l / 16 of pixel l % 16, zero past nin); x[u] = the last hidden layer's activations of tile u as the
 // next layer's B operands (k-step ks: hidden_input(ks, l / 16) of pixel l % 16). Every lane of the wave
 // must be active. k is act_k(Act, leak).
-template <class S, int U, int Act>
-__device__ __forceinline__ void mfma_hidden(const MfmaWeights<S>& W, const float (&b1)[U][MfmaShape<S>::kKs1], float k,
-                                            float (&x)[U][MfmaShape<S>::kKsH]) {
+// mfma_hidden in two parts. The first layer's pre-activations of U tiles in D layout (acc[u][ot]: hidden tile ot).
+template <class S, int U>
+__device__ __forceinline__ void mfma_layer1(const MfmaWeights<S>& W, const float (&b1)[U][MfmaShape<S>::kKs1],
+                                            f4v (&acc)[U][MfmaShape<S>::kHt]) {
     using Q = MfmaShape<S>;
-    {
-        f4v acc[U][Q::kHt];
+#pragma unroll
+    for (int u = 0; u < U; u++)
+#pragma unroll
+        for (int ot = 0; ot < Q::kHt; ot++) acc[u][ot] = W.c1[ot];
+#pragma unroll
+    for (int ks = 0; ks < Q::kKs1; ks++)
 #pragma unroll
         for (int u = 0; u < U; u++)
 #pragma unroll
-            for (int ot = 0; ot < Q::kHt; ot++) acc[u][ot] = W.c1[ot];
+            for (int ot = 0; ot < Q::kHt; ot++) acc[u][ot] = mfma4(W.a1[ot][ks], b1[u][ks], acc[u][ot]);
+}
+// ... and from those pre-activations through the activation and the other hidden layers (x as mfma_hidden
+// leaves it).
+template <class S, int U, int Act>
+__device__ __forceinline__ void mfma_hidden_from1(const MfmaWeights<S>& W, const f4v (&acc1)[U][MfmaShape<S>::kHt], float k,
+                                                  float (&x)[U][MfmaShape<S>::kKsH]) {
+    using Q = MfmaShape<S>;
 #pragma unroll
-        for (int ks = 0; ks < Q::kKs1; ks++)
+    for (int u = 0; u < U; u++)
 #pragma unroll
-            for (int u = 0; u < U; u++)
+        for (int ot = 0; ot < Q::kHt; ot++)
 #pragma unroll
-                for (int ot = 0; ot < Q::kHt; ot++) acc[u][ot] = mfma4(W.a1[ot][ks], b1[u][ks], acc[u][ot]);
-#pragma unroll
-        for (int u = 0; u < U; u++)
-#pragma unroll
-            for (int ot = 0; ot < Q::kHt; ot++)
-#pragma unroll
-                for (int r = 0; r < Q::regs(ot); r++) x[u][4 * ot + r] = act<Act>(acc[u][ot][r], k);
-    }
+            for (int r = 0; r < Q::regs(ot); r++) x[u][4 * ot + r] = act<Act>(acc1[u][ot][r], k);
 #pragma unroll
     for (int l = 0; l < Q::kNL - 1; l++) {
         f4v acc[U][Q::kHt];
@@ -352,20 +357,31 @@ __device__ __forceinline__ void mfma_hidden(const MfmaWeights<S>& W, const float
                 for (int r = 0; r < Q::regs(ot); r++) x[u][4 * ot + r] = act<Act>(acc[u][ot][r], k);
     }
 }
-// ... and through the output layer on the matrix cores: the pre-activations of each tile in D layout
-// (lane l, register r = output out_at(l / 16, r) of pixel l % 16).
 template <class S, int U, int Act>
-__device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const float (&b1)[U][MfmaShape<S>::kKs1], float k,
-                                             f4v (&o)[U]) {
-    using Q = MfmaShape<S>;
-    float x[U][Q::kKsH];
-    mfma_hidden<S, U, Act>(W, b1, k, x);
+__device__ __forceinline__ void mfma_hidden(const MfmaWeights<S>& W, const float (&b1)[U][MfmaShape<S>::kKs1], float k,
+                                            float (&x)[U][MfmaShape<S>::kKsH]) {
+    f4v acc[U][MfmaShape<S>::kHt];
+    mfma_layer1<S, U>(W, b1, acc);
+    mfma_hidden_from1<S, U, Act>(W, acc, k, x);
+}
+// The output layer on the matrix cores: the pre-activations of each tile in D layout (lane l, register r =
+// output out_at(l / 16, r) of pixel l % 16).
+template <class S, int U>
+__device__ __forceinline__ void mfma_output(const MfmaWeights<S>& W, const float (&x)[U][MfmaShape<S>::kKsH], f4v (&o)[U]) {
 #pragma unroll
     for (int u = 0; u < U; u++) o[u] = W.co;
 #pragma unroll
-    for (int ks = 0; ks < Q::kKsH; ks++)
+    for (int ks = 0; ks < MfmaShape<S>::kKsH; ks++)
 #pragma unroll
         for (int u = 0; u < U; u++) o[u] = mfma4(W.ao[ks], x[u][ks], o[u]);
+}
+// The whole MLP of U tiles from the first layer's B operands to the output pre-activations.
+template <class S, int U, int Act>
+__device__ __forceinline__ void mfma_forward(const MfmaWeights<S>& W, const float (&b1)[U][MfmaShape<S>::kKs1], float k,
+                                             f4v (&o)[U]) {
+    float x[U][MfmaShape<S>::kKsH];
+    mfma_hidden<S, U, Act>(W, b1, k, x);
+    mfma_output<S, U>(W, x, o);
 }
 
 // ---- exchanges between lane groups through the wave's own LDS rows
