@@ -480,6 +480,14 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
     }
 }
 
+// The selector search's occupancy target: four waves per SIMD for the 8-input, 32-wide models with more than 4
+// outputs and the folded activation, which fit in 128 VGPRs without scratch (the compiler alone gives them 130 and
+// three waves); the compiler's choice for the other shapes, several of which spill at four.
+template <class S, int Act>
+constexpr int qat_occupancy() {
+    return (MfmaShape<S>::kIn <= 8 && MfmaShape<S>::kH == 32 && !valu_out<S>() && Act == kActFold) ? 4 : 1;
+}
+
 // The selector search (qat_search, main.cpp:2088-2139) on the matrix cores, for a nearest level 0
 // of the image's size (each texel's cell is its own pixel): wave = 64 pixels in four 16-pixel tiles.
 // Every lane builds the features of its own pixel (features<S>) and tiles_of turns them into the four
@@ -494,13 +502,6 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
 // activation of act<Act>: the reference adds the float terms in double with its own activation, so a
 // choice can differ from the reference's only between candidates whose losses agree to a few float
 // roundings (the reference's own check accepts such rounding ties, main.cpp:3143-3144).
-// The selector search's occupancy target: four waves per SIMD for the 8-input, 32-wide models with more than 4
-// outputs and the folded activation, which fit in 128 VGPRs without scratch (the compiler alone gives them 130 and
-// three waves); the compiler's choice for the other shapes, several of which spill at four.
-template <class S, int Act>
-constexpr int qat_occupancy() {
-    return (MfmaShape<S>::kIn <= 8 && MfmaShape<S>::kH == 32 && !valu_out<S>() && Act == kActFold) ? 4 : 1;
-}
 template <class S, int Act, bool Clamp>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(qat_occupancy<S, Act>()))) k_qat_mfma(DevModel m, const float* __restrict__ w, float* __restrict__ zdec,
                                                  const float* __restrict__ tgt, const int* __restrict__ qat_bits,
