@@ -120,6 +120,9 @@ def make_trainer(w, z, p, tgt):
 def es_iter(tr, w, it):
     tr.mlp_step(it, w.mlp_sigma, w.mlp_lr, w.mlp_pairs, w.mlp_batch)
     tr.lat_step(it, w.lat_sigma, w.lat_lr, w.lat_pairs)
+    if w.dct_q and w.shadow_pull > 0:   # the live plane's shadow pulled toward it and re-snapped (main.cpp:4136)
+        W0, H0, C0, _ = w.layout.levels[0]
+        tr.shadow_pull(0, W0 * H0 * C0, w.shadow_pull)
     if w.qat_bits:
         tr.qat_search()
 
@@ -143,8 +146,11 @@ def cpu_baseline(w, z, p, tgt, seconds: float, pairs=None, dct_codes=None):
     cfg.fd_from, cfg.fd_h = w.iters + 1, w.fd_h
     ev = evals_per_iter(w, pairs)["total"]
     keep = []
+    isa = None
     if O.have_reference(fast=True):
-        L = O.reference(fast=True).lib
+        isa = O.host_isa()
+        ref_path = O.reference_path(fast=True, isa="auto")   # the widest build the host supports (-march=native's choice)
+        L = O.reference(fast=True, isa="auto").lib
         if w.dct_q:
             h = dct_host_state(w, dct_codes)
             d = O.OrDct()
@@ -188,9 +194,14 @@ def cpu_baseline(w, z, p, tgt, seconds: float, pairs=None, dct_codes=None):
     if pairs != w.mlp_pairs:
         sample = (f"{its} ES iteration(s) of {w.name} with {pairs} of its {w.mlp_pairs} pairs (population evaluation scaled "
                   f"down, everything else at full size), {el:.1f} s")
-    return {"value": ev * its / el, "unit": "member·pixel evals/s", "cores": threads, "kind": kind, "sample": sample,
-            "es_iters_per_s": its / el, "cpu": cpu_model(), "nproc": os.cpu_count(),
-            "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None}
+    out = {"value": ev * its / el, "unit": "member·pixel evals/s", "cores": threads, "kind": kind, "sample": sample,
+           "es_iters_per_s": its / el, "cpu": cpu_model(), "cpuid": cpu_ids(), "nproc": os.cpu_count(),
+           "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None}
+    if kind == "reference":
+        out["isa"] = isa
+        out["build"] = f"{os.path.relpath(ref_path, ROOT)} (-O3 -ffast-math -fopenmp -march=" + \
+            ("x86-64-v4" if ref_path.endswith("_v4.so") else "x86-64-v3") + ")"
+    return out
 
 
 def gauss_draw(w, reps: int):
@@ -228,6 +239,25 @@ def cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
+def cpu_ids() -> dict:
+    """/proc/cpuinfo's vendor, family, model and stepping numbers of the first CPU, and its AVX-512 flags"""
+    out = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if not line.strip():
+                    break
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k in ("vendor_id", "cpu family", "model", "stepping", "microcode"):
+                    out[k.replace(" ", "_")] = v
+                elif k == "flags":
+                    out["avx512"] = sorted(x for x in v.split() if x.startswith("avx512"))
+    except OSError:
+        pass
+    return out
+
+
 def cpu_refit_ms(w, r):
     """The reference's host refit of the same state (main.cpp:4110-4120 with --cuda: the model downloaded,
     dct_probe_codes and the level-0 snap on the host's cores; the set_dct upload not included)."""
@@ -236,7 +266,7 @@ def cpu_refit_ms(w, r):
     from oracle import oracle as O
     if not O.have_reference(fast=True):
         return None
-    L = O.reference(fast=True).lib
+    L = O.reference(fast=True, isa="auto").lib
     (z, p), zq = r["host_state"]
     h = dct_host_state(w, r["dct_codes"])
     d = O.OrDct()

@@ -82,7 +82,9 @@ size_t ntc_trainer_banner(const ntc_trainer* t, char* buf, size_t cap);
 /* Trainer::upload_model / download_model (cuda/ntc_cuda.h:88-89): z = nz floats, p = P floats */
 void ntc_trainer_upload_model(ntc_trainer* t, const float* z, const float* p);
 void ntc_trainer_download_model(ntc_trainer* t, float* z, float* p);
-/* Trainer::set_qes / snap_latent / shadow_pull / download_zq (cuda/ntc_cuda.h:93-96) */
+/* Trainer::set_qes / snap_latent / shadow_pull / download_zq (cuda/ntc_cuda.h:93-96). snap_latent and shadow_pull
+ * touch device memory only and return once their kernels are enqueued on the trainer's stream, as the
+ * reference's do (cuda/ntc_cuda.cu:978-988); every call that copies to or from the host waits for them. */
 void ntc_trainer_set_qes(ntc_trainer* t, const ntc_qes_desc* q, const float* grid, size_t grid_n);
 void ntc_trainer_snap_latent(ntc_trainer* t);
 void ntc_trainer_shadow_pull(ntc_trainer* t, size_t off, size_t n, float f);
@@ -112,10 +114,12 @@ void ntc_trainer_decode_error(ntc_trainer* t, const float* z_host, int ew, int e
 /* ntc_trainer_decode_error with no allocation at call time (no hipMalloc / hipFree, no allocating library
  * call): the same figures from the same kernels, with the per-block partial sums kept in a static per-GPU
  * scratch array of 512 KiB and added on the device. No counterpart in the reference: it is for callers that
- * cannot allocate (code under HIP graph capture, a serving or progress-print loop that must not synchronize
- * the device through hipMalloc / hipFree). The extent ew x eh may hold at most 2^24 pixels (4096 x 4096);
- * a larger one prints an error and exits, as every other misuse. Every call on one GPU shares that GPU's
- * array: calls that overlap on one GPU (from several host threads or trainers) race. */
+ * cannot allocate, such as a serving or progress-print loop that must not synchronize the device through
+ * hipMalloc / hipFree. It is not for HIP graph capture: like decode_error it copies z_host (when given) from
+ * pageable host memory and waits on the trainer's stream to copy the totals back. The extent ew x eh may hold
+ * at most 2^24 pixels (4096 x 4096); a larger one prints an error and exits, as every other misuse. Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (from several host threads or trainers)
+ * race. */
 void ntc_trainer_decode_error_noalloc(ntc_trainer* t, const float* z_host, int ew, int eh, double* tex_mse, double* weighted);
 /* The figures of the reference's progress line (main.cpp:4155-4212) computed on the device, without downloading
  * the model (the reference's --cuda print path downloads the latent and the weights at every print):
@@ -219,6 +223,9 @@ void ntc_trainer_debug_copy_calibration(ntc_trainer* t, size_t n, int reps);
 /* the device's copy of the two Gaussian factors for 24-bit draws k0 .. k0 + n - 1:
  * rad[k] = sqrtf(-2 logf((k + 1) / 2^24)), cosv[k] = cosf(2 pi k / 2^24) */
 void ntc_trainer_debug_noise_factors(ntc_trainer* t, uint32_t k0, size_t n, float* rad, float* cosv);
+/* device allocations (hipMalloc) and releases (hipFree) this library has made in the process so far, in *allocs and
+ * *frees: read around a call, they show whether it allocated */
+void ntc_debug_device_allocations(long long* allocs, long long* frees);
 
 #ifdef __cplusplus
 }

@@ -29,6 +29,7 @@ class Workload:
     fd_iters: int = 0          # trailing --mlp-fd iterations
     fd_h: float = 1e-3
     dct_q: list = None         # --dct-q per level-0 channel
+    shadow_pull: float = 0.0   # --dct-shadow-pull: after every latent step on a live DCT plane (main.cpp:4136, 4142-4146)
     fp16_end: bool = False     # --write-ntcb: weights rounded to fp16 at the end
     seed: int = 1
     textures: int = 1
@@ -63,7 +64,8 @@ def workloads() -> dict:
         # 512x512 RGB, --dct-q 50 plane 512x512x1 + 128x128x4, 32,32, population 4096
         "dct512": Workload("dct512", Layout(512, 512, [(512, 512, 1, True), (128, 128, 4, False)], [32, 32], T=1,
                                             pos=[PK_UV], leak=0.01),
-                           mlp_pairs=2048, mlp_batch=4096, iters=4000, dct_q=[50], seed=14),
+                           mlp_pairs=2048, mlp_batch=4096, iters=4000, dct_q=[50], shadow_pull=0.01, seed=14,
+                           notes="--dct-shadow-pull at its default 0.01 (main.cpp:175)"),
         # 4 x 2048x2048 maps, 1024x1024x4 + 256x256x8 bilinear, 64,64, population 16384, 256K batches
         "material2048": Workload("material2048",
                                  Layout(2048, 2048, [(1024, 1024, 4, False), (256, 256, 8, False)], [64, 64], T=4,

@@ -225,23 +225,23 @@ int ntc_trainer_kernel_time(ntc_trainer* t, const char* name, double* total_ms, 
 void ntc_trainer_debug_gauss(ntc_trainer* t, uint32_t stream, uint32_t step, uint32_t pair, uint64_t index0, size_t n, float* out) {
     auto& I = *t->t.im;
     float* d = nullptr;
-    NTC_CHECK(hipMalloc(&d, std::max<size_t>(n, 1) * sizeof(float)));
+    NTC_CHECK(ntc_hip::ntc_malloc(&d, std::max<size_t>(n, 1) * sizeof(float)));
     ntc_hip::launch_debug_gauss(I, stream, step, pair, index0, n, d);
     NTC_CHECK(hipMemcpyAsync(out, d, n * sizeof(float), hipMemcpyDeviceToHost, I.stream));
     NTC_CHECK(hipStreamSynchronize(I.stream));
-    NTC_CHECK(hipFree(d));
+    NTC_CHECK(ntc_hip::ntc_free(d));
 }
 void ntc_trainer_debug_copy_calibration(ntc_trainer* t, size_t n, int reps) {
     auto& I = *t->t.im;
     n &= ~(size_t)3;
     float *a = nullptr, *b = nullptr;
-    NTC_CHECK(hipMalloc(&a, std::max<size_t>(n, 4) * sizeof(float)));
-    NTC_CHECK(hipMalloc(&b, std::max<size_t>(n, 4) * sizeof(float)));
+    NTC_CHECK(ntc_hip::ntc_malloc(&a, std::max<size_t>(n, 4) * sizeof(float)));
+    NTC_CHECK(ntc_hip::ntc_malloc(&b, std::max<size_t>(n, 4) * sizeof(float)));
     NTC_CHECK(hipMemsetAsync(a, 0, n * sizeof(float), I.stream));
     for (int r = 0; r < reps; r++) ntc_hip::launch_copy_calibration(I, a, b, n);
     NTC_CHECK(hipStreamSynchronize(I.stream));
-    NTC_CHECK(hipFree(a));
-    NTC_CHECK(hipFree(b));
+    NTC_CHECK(ntc_hip::ntc_free(a));
+    NTC_CHECK(ntc_hip::ntc_free(b));
 }
 void ntc_trainer_debug_noise_factors(ntc_trainer* t, uint32_t k0, size_t n, float* rad, float* cosv) {
     auto& I = *t->t.im;
@@ -250,14 +250,19 @@ void ntc_trainer_debug_noise_factors(ntc_trainer* t, uint32_t k0, size_t n, floa
     if (n > total - k0) n = total - k0;
     if (!n) return;
     float *dr = nullptr, *dc = nullptr;
-    NTC_CHECK(hipMalloc(&dr, n * sizeof(float)));
-    NTC_CHECK(hipMalloc(&dc, n * sizeof(float)));
+    NTC_CHECK(ntc_hip::ntc_malloc(&dr, n * sizeof(float)));
+    NTC_CHECK(ntc_hip::ntc_malloc(&dc, n * sizeof(float)));
     ntc_hip::launch_debug_factors(I, k0, n, dr, dc);
     if (rad) NTC_CHECK(hipMemcpyAsync(rad, dr, n * sizeof(float), hipMemcpyDeviceToHost, I.stream));
     if (cosv) NTC_CHECK(hipMemcpyAsync(cosv, dc, n * sizeof(float), hipMemcpyDeviceToHost, I.stream));
     NTC_CHECK(hipStreamSynchronize(I.stream));
-    NTC_CHECK(hipFree(dr));
-    NTC_CHECK(hipFree(dc));
+    NTC_CHECK(ntc_hip::ntc_free(dr));
+    NTC_CHECK(ntc_hip::ntc_free(dc));
+}
+
+void ntc_debug_device_allocations(long long* allocs, long long* frees) {
+    if (allocs) *allocs = ntc_hip::g_device_allocs.load();
+    if (frees) *frees = ntc_hip::g_device_frees.load();
 }
 
 }   // extern "C"

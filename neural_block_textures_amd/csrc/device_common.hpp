@@ -68,6 +68,8 @@ __host__ __device__ __forceinline__ uint64_t noise_head(uint64_t seed, uint32_t 
     return mix64(seed ^ ((uint64_t)stream << 56) ^ ((uint64_t)step << 32) ^ (uint64_t)pair);
 }
 __host__ __device__ __forceinline__ uint64_t noise_bits(uint64_t head, uint64_t index) { return mix64(head + index * kPhi64); }
+// x is not a NaN, decided on its bits (valid in code compiled to assume no NaNs, where a float test folds away)
+__device__ __forceinline__ bool not_nan_bits(float x) { return (__float_as_uint(x) & 0x7fffffffu) <= 0x7f800000u; }
 __host__ __device__ __forceinline__ uint32_t noise_uniform(uint32_t u, uint32_t n) { return (uint32_t)(((uint64_t)u * (uint64_t)n) >> 32); }
 // One standard normal draw: the 24-bit halves of the key select the two factors, whose product
 // is the reference's sqrtf(-2 logf(u1)) * cosf(2 pi u2) bit for bit (one IEEE multiply).

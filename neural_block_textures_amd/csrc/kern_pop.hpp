@@ -571,7 +571,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(qat_oc
             const int cur = __builtin_amdgcn_ds_bpermute((16 * t + i16) << 2, cur_own[c]);
             // the losses and grid values of the current candidate and of the best other one so far: the winner's
             // value comes from these registers, not from a load of the grid after the search
-            float cur_l = 0.0f, best_l = 0.0f, cur_v = 0.0f, best_v = 0.0f;
+            // best over the other candidates in ascending k, from +inf with a strict <; a NaN loss never wins and a NaN
+            // current loss keeps the current value, as the reference's running minimum from the current loss gives
+            // (main.cpp:2122-2127). The NaN tests are on the bits: this file is compiled assuming no NaNs.
+            float cur_l = 0.0f, best_l = __builtin_inff(), cur_v = 0.0f, best_v = 0.0f;
             int best_k = -1;
             // The first layer's sums of the tile without input c (a zero in its place: fma(w, 0, s) = s) and, in D
             // layout, the weight of input c into each of this lane's units (read from the lane of W.a1 that holds
@@ -627,11 +630,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(qat_oc
                 for (int v = 0; v < 2; v++) {
                     const float l = ls[v];
                     if (kc + v == cur) { cur_l = l; cur_v = gc[v]; }
-                    else if (best_k < 0 || l < best_l) { best_l = l; best_k = kc + v; best_v = gc[v]; }
+                    else if (not_nan_bits(l) && l < best_l) { best_l = l; best_k = kc + v; best_v = gc[v]; }
                 }
             }
             // cur is in 0 .. levels (qat_index clamps), so cur_v is its grid value
-            const float win_v = (best_k >= 0 && best_l < cur_l) ? best_v : cur_v;
+            const float win_v = (best_k >= 0 && not_nan_bits(cur_l) && best_l < cur_l) ? best_v : cur_v;
             if (g == c % 4) b[t][c / 4] = win_v;
             const int p = base + 16 * t + i16;
             if (g == 0 && p < m.npix) zdec[m.lv[0].off + (size_t)p * m.lv[0].C + c] = win_v;

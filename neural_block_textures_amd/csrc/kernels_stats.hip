@@ -177,8 +177,8 @@ namespace {
 template <class T>
 void ensure(T** p, size_t& cap, size_t need) {
     if (need <= cap) return;
-    if (*p) (void)hipFree(*p);
-    NTC_CHECK(hipMalloc((void**)p, need * sizeof(T)));
+    if (*p) (void)ntc_hip::ntc_free(*p);
+    NTC_CHECK(ntc_hip::ntc_malloc((void**)p, need * sizeof(T)));
     cap = need;
 }
 
@@ -403,7 +403,7 @@ void print_stats_impl(Impl& I, int qbits, int ew, int eh, ntc_print_stats* out) 
             o.dct_ntok_nz += I.st_dct_counts[(size_t)c * kDctPerCh + kDScal + 0];
             o.dct_ntok_eob += I.st_dct_counts[(size_t)c * kDctPerCh + kDScal + 1];
         }
-        o.dct_nmag_over = tail[4];
+        o.dct_nmag_over = 2 * tail[4];   // dct_analyze counts each |symbol| > 256 in both of its passes (main.cpp:1113, 1147)
         o.dct_nz_mean = (double)tail[0] / (double)nbc;
         o.dct_lnz_mean = tail[2] ? (double)tail[1] / (double)tail[2] : 0.0;
         o.dct_eob_only_frac = (double)tail[3] / (double)nbc;

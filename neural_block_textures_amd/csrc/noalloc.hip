@@ -1,8 +1,9 @@
 // The printed error of the current model (decode_error: mse_of, main.cpp:1764-1788) without any
-// allocation at call time, for callers that cannot allocate device memory (code under HIP graph
-// capture, a serving or progress-print loop that must not synchronize the device through
-// hipMalloc / hipFree). decode_error allocates its per-block partial sums on every call; this variant
-// keeps them in `scratch`, one statically sized array per GPU, and adds them on the device.
+// allocation at call time, for callers that cannot allocate device memory (a serving or progress-print
+// loop that must not synchronize the device through hipMalloc / hipFree). decode_error allocates its
+// per-block partial sums on every call; this variant keeps them in `scratch`, one statically sized array
+// per GPU, and adds them on the device. Like decode_error it copies a host latent from pageable memory and
+// waits on the trainer's stream to read the totals back, so it cannot be captured into a HIP graph.
 //
 // `scratch` is a device symbol: in host code its name is no device address. Its address on each GPU
 // is looked up once (noalloc_scratch_setup, from Trainer::init with that GPU current) and only that

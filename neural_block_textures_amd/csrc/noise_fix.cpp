@@ -81,7 +81,7 @@ bool noise_fix_for_device(int device, NoiseFix& out, std::string& why) {
     const uint32_t swords = (uint32_t)lany.size();
     uint32_t* buf = nullptr;
     const size_t total = 2 * (size_t)words + 2 * (size_t)swords;
-    NTC_CHECK(hipMalloc(&buf, total * sizeof(uint32_t)));
+    NTC_CHECK(ntc_hip::ntc_malloc(&buf, total * sizeof(uint32_t)));
     uint32_t *l = buf, *c = buf + words, *la = buf + 2 * (size_t)words, *ca = la + swords;
     NTC_CHECK(hipMemcpy(l, lfix.data(), (size_t)words * sizeof(uint32_t), hipMemcpyHostToDevice));
     NTC_CHECK(hipMemcpy(c, cfix.data(), (size_t)words * sizeof(uint32_t), hipMemcpyHostToDevice));

@@ -25,11 +25,11 @@ namespace {
 template <class T>
 void dev_alloc(T** p, size_t n) {
     *p = nullptr;
-    if (n) NTC_CHECK(hipMalloc((void**)p, n * sizeof(T)));
+    if (n) NTC_CHECK(ntc_hip::ntc_malloc((void**)p, n * sizeof(T)));
 }
 template <class T>
 void dev_free(T*& p) {
-    if (p) { (void)hipFree(p); p = nullptr; }
+    if (p) { (void)ntc_hip::ntc_free(p); p = nullptr; }
 }
 
 // Pixel footprint of every texel row / column of one level: the pixels whose tap reads the
@@ -104,21 +104,24 @@ void sync(Impl& I) { NTC_CHECK(hipStreamSynchronize(I.stream)); }
 }   // namespace
 
 namespace ntc_hip {
+std::atomic<long long> g_device_allocs{ 0 }, g_device_frees{ 0 };
 // The decoder sensitivity probe on the device (the host's dct_probe_codes, main.cpp:1001-1032).
 void dct_probe_impl(Impl& I, uint8_t* code, float* gain) {
     if (!I.dct) die("dct_probe without --dct-q in the model description");
     launch_dct_probe(I, I.dct_probe_code, I.dct_gain);
     if (code) NTC_CHECK(hipMemcpyAsync(code, I.dct_probe_code, (size_t)I.ddct.n, hipMemcpyDeviceToHost, I.stream));
     if (gain) NTC_CHECK(hipMemcpyAsync(gain, I.dct_gain, (size_t)I.ddct.n * sizeof(float), hipMemcpyDeviceToHost, I.stream));
-    sync(I);
+    if (code || gain) sync(I);   // the host reads what was copied; without an output the launch stays enqueued
 }
 // Decoder::dct_refit (main.cpp:1672-1680) on the device: probe, replace the codes, re-snap (qes_refresh).
 void dct_refit_impl(Impl& I, uint8_t* code) {
     if (!I.dct || !I.dct_live) die("dct_refit before set_dct");
     launch_dct_probe(I, I.dct_code, nullptr);
     snap_latent_impl(I);
-    if (code) NTC_CHECK(hipMemcpyAsync(code, I.dct_code, (size_t)I.ddct.n, hipMemcpyDeviceToHost, I.stream));
-    sync(I);
+    if (code) {
+        NTC_CHECK(hipMemcpyAsync(code, I.dct_code, (size_t)I.ddct.n, hipMemcpyDeviceToHost, I.stream));
+        sync(I);
+    }
 }
 
 // The print path's error figures without a download (mse_of, main.cpp:1764-1788): decode the decode
@@ -130,7 +133,7 @@ void decode_error_impl(Impl& I, const float* z_host, int ew, int eh, double* tex
     if (eh <= 0 || eh > I.d.H) eh = I.d.H;
     const size_t blocks = ((size_t)ew * eh + 255) / 256;
     unsigned long long* part = nullptr;
-    NTC_CHECK(hipMalloc(&part, blocks * 4 * sizeof(unsigned long long)));
+    NTC_CHECK(ntc_hip::ntc_malloc(&part, blocks * 4 * sizeof(unsigned long long)));
     const float* zsrc = I.zdec;
     if (z_host) {
         NTC_CHECK(hipMemcpyAsync(I.ztmp, z_host, I.nz * sizeof(float), hipMemcpyHostToDevice, I.stream));
@@ -141,7 +144,7 @@ void decode_error_impl(Impl& I, const float* z_host, int ew, int eh, double* tex
     std::vector<unsigned long long> h(blocks * 4);
     NTC_CHECK(hipMemcpyAsync(h.data(), part, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost, I.stream));
     sync(I);
-    NTC_CHECK(hipFree(part));
+    NTC_CHECK(ntc_hip::ntc_free(part));
     const int T = I.d.nout / 3;
     const double npix = (double)ew * eh;
     double ws = 0.0;
@@ -159,12 +162,12 @@ void decode_error_impl(Impl& I, const float* z_host, int ew, int eh, double* tex
 void decode_rgb8_impl(Impl& I, uint8_t* out) {
     const size_t n = (size_t)I.npix * I.d.nout;
     uint8_t* d = nullptr;
-    NTC_CHECK(hipMalloc(&d, n));
+    NTC_CHECK(ntc_hip::ntc_malloc(&d, n));
     launch_decode(I, I.zdec);
     launch_pack_u8(I, d);
     NTC_CHECK(hipMemcpyAsync(out, d, n, hipMemcpyDeviceToHost, I.stream));
     sync(I);
-    NTC_CHECK(hipFree(d));
+    NTC_CHECK(ntc_hip::ntc_free(d));
 }
 
 void resolve_times(Impl& I) {
@@ -429,7 +432,9 @@ void Trainer::set_qes(const QesDesc& q, const float* grid, size_t grid_n) {
     sync(I);
 }
 
-void Trainer::snap_latent() { snap_latent_impl(*im); sync(*im); }
+// Reads and writes device memory only: enqueued on the trainer's stream, as the reference's kernels are
+// (cuda/ntc_cuda.cu:978-988); the next call that copies to or from the host waits for it.
+void Trainer::snap_latent() { snap_latent_impl(*im); }
 
 void Trainer::shadow_pull(size_t off, size_t n, float f) {
     Impl& I = *im;
@@ -437,7 +442,6 @@ void Trainer::shadow_pull(size_t off, size_t n, float f) {
     if (off + n > I.nz) die("shadow_pull range outside the latent");
     launch_shadow_pull(I, off, n, f);
     snap_latent_impl(I);
-    sync(I);
 }
 
 void Trainer::download_zq(float* zq) {

@@ -34,7 +34,22 @@
         }                                                                                                     \
     } while (0)
 
+#include <atomic>
+
 namespace ntc_hip {
+
+// Every device allocation and release the library makes goes through these two, which count them
+// (ntc_debug_device_allocations: a test that an entry point allocates nothing reads the count around it).
+extern std::atomic<long long> g_device_allocs, g_device_frees;
+template <class T>
+hipError_t ntc_malloc(T** p, size_t bytes) {
+    g_device_allocs.fetch_add(1, std::memory_order_relaxed);
+    return hipMalloc((void**)p, bytes);
+}
+inline hipError_t ntc_free(void* p) {
+    g_device_frees.fetch_add(1, std::memory_order_relaxed);
+    return hipFree(p);
+}
 
 // --dct-q level 0 as the kernels see it (by value)
 struct DevDct {

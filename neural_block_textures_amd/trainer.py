@@ -132,6 +132,7 @@ def library() -> C.CDLL:
             "ntc_trainer_debug_gauss": (None, [P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, C.c_size_t, P]),
             "ntc_trainer_debug_noise_factors": (None, [P, C.c_uint32, C.c_size_t, P, P]),
             "ntc_trainer_debug_copy_calibration": (None, [P, C.c_size_t, C.c_int]),
+            "ntc_debug_device_allocations": (None, [P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -458,6 +459,13 @@ class Trainer:
         return rad, cosv
 
     # ---- instrumentation
+    @staticmethod
+    def device_allocations():
+        """(hipMalloc calls, hipFree calls) the library has made in this process"""
+        a, f = C.c_longlong(), C.c_longlong()
+        library().ntc_debug_device_allocations(C.byref(a), C.byref(f))
+        return a.value, f.value
+
     def debug_copy_calibration(self, n, reps=1):
         self._lib.ntc_trainer_debug_copy_calibration(self._h, n, reps)
 

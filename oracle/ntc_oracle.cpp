@@ -997,7 +997,7 @@ void or_dct_analyze(const OrDct* d, int dc_raw_bits, int ctx, OrDctStats* out) {
             for (int p = 1; p < 64; p++) {
                 const int q = sym[zz[p]];
                 if (q == 0) { run++; continue; }
-                const int mag = std::min(256, std::abs(q));
+                const int mag = std::min(256, std::abs(q)); if (std::abs(q) > 256) S.nmag_over++;   // counted again, as main.cpp:1147 does
                 const double r0 = cl0((double)run_cnt[run], (double)nruntok), m0 = cl0((double)mag_cnt[mag], (double)nrun);
                 const double rc = cl0((double)ctx_run[(size_t)prev * 65 + run], (double)ctxr_cnt[prev]);
                 const double mc = cl0((double)ctx_mag[(size_t)prev * 257 + mag], (double)ctxm_cnt[prev]);
@@ -1182,6 +1182,15 @@ void or_print_counts(const OrModel* mp, const OrPrintIn* in, const float* z, con
             tri[u * 256 + lf * 16 + k]++; pair[u * 16 + lf]++;
         }
     }
+}
+
+int or_host_isa_level(void) {
+    __builtin_cpu_init();
+    if (__builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") && __builtin_cpu_supports("avx512cd") &&
+        __builtin_cpu_supports("avx512dq") && __builtin_cpu_supports("avx512vl"))
+        return 4;
+    if (__builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma") && __builtin_cpu_supports("bmi2")) return 3;
+    return 1;
 }
 
 }   // extern "C"

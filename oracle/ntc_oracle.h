@@ -225,6 +225,9 @@ void or_latent_stats(const OrModel* m, int l, const float* z, float* mean, float
 void or_print_counts_size(const OrModel* m, const OrPrintIn* in, long long* n_bitrate, long long* n_dct);
 void or_print_counts(const OrModel* m, const OrPrintIn* in, const float* z, const float* zdec, long long* bitrate, float* lohi,
                      long long* dct);
+/* The widest x86-64 level the host CPU and OS support, by cpuid: 4 (AVX-512 F/BW/CD/DQ/VL), 3 (AVX2, FMA,
+ * BMI2), else 1. Picks the reference build the CPU baseline loads. */
+int or_host_isa_level(void);
 #ifdef __cplusplus
 }
 #endif

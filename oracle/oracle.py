@@ -16,6 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "libntc_oracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libntc_ref.so")
 REF_FAST_SO = os.path.join(HERE, "_ref", "libntc_ref_fast.so")
+REF_FAST_V4_SO = os.path.join(HERE, "_ref", "libntc_ref_fast_v4.so")
 
 MAX_LEVELS, MAX_POS, MAX_OUT, MAX_HIDDEN = 3, 16, 12, 8
 NS_LAT, NS_MLP, NS_BATCH_PIX, NS_BATCH_TEX = 1, 2, 3, 4
@@ -241,6 +242,7 @@ class Lib:
                               "latent_stats": [_P, C.c_int, _P, _P, _P, _P], "print_counts_size": [_P, _P, _P, _P],
                               "print_counts": [_P, _P, _P, _P, _P, _P, _P]}[fn]
         if prefix == "or_":
+            self.lib.or_host_isa_level.restype = C.c_int
             self.lib.or_train_iter.restype = C.c_double
             self.lib.or_train_iter.argtypes = [_P, _P, _P, _P, C.c_int, C.c_int]
             self.lib.or_round_fp16.restype = C.c_int
@@ -266,6 +268,18 @@ class Lib:
             L.ref_train_create.argtypes = [_P, _P, _P, _P, _P]
             L.ref_train_create_dct.restype = C.c_void_p
             L.ref_train_create_dct.argtypes = [_P, _P, _P, _P, _P, _P, C.c_float, C.c_int, C.c_int]
+            L.ref_train_create_dct_sched.restype = C.c_void_p
+            L.ref_train_create_dct_sched.argtypes = [_P, _P, _P, _P, _P, _P, C.c_float, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
+            L.ref_train_set_shadow_pull.argtypes = [C.c_void_p, C.c_float]
+            L.ref_shadow_pull.argtypes = [_P, _P, C.c_longlong, C.c_float]
+            L.ref_train_get_zdec.argtypes = [C.c_void_p, _P]
+            L.ref_train_round_fp16.restype = C.c_int
+            L.ref_train_round_fp16.argtypes = [C.c_void_p]
+            L.ref_train_get_dct_codes.argtypes = [C.c_void_p, _P]
+            L.ref_train_save.restype = C.c_int
+            L.ref_train_save.argtypes = [C.c_void_p, C.c_char_p]
+            L.ref_train_load.restype = C.c_int
+            L.ref_train_load.argtypes = [C.c_void_p, C.c_char_p]
             L.ref_train_iter.restype = C.c_double
             L.ref_train_iter.argtypes = [C.c_void_p, C.c_int, C.c_int]
             L.ref_train_get.argtypes = [C.c_void_p, _P, _P]
@@ -441,8 +455,25 @@ def oracle() -> Lib:
     return Lib(ORACLE_SO, "or_")
 
 
-def reference(fast: bool = False) -> Lib:
-    return Lib(REF_FAST_SO if fast else REF_SO, "ref_")
+def host_isa() -> str:
+    """the widest x86-64 level the host CPU and OS support, by cpuid (or_host_isa_level): "x86-64-v4" with
+    AVX-512 F/BW/CD/DQ/VL, "x86-64-v3" with AVX2/FMA/BMI2, else "x86-64" """
+    return {4: "x86-64-v4", 3: "x86-64-v3"}.get(oracle().lib.or_host_isa_level(), "x86-64")
+
+
+def reference_path(fast: bool = False, isa: str = "x86-64-v3") -> str:
+    """the reference build for an ISA level; "auto" = the widest one built that the host supports"""
+    if not fast:
+        return REF_SO
+    if isa == "auto":
+        isa = host_isa()
+        if isa == "x86-64-v4" and not os.path.exists(REF_FAST_V4_SO):
+            isa = "x86-64-v3"
+    return REF_FAST_V4_SO if isa == "x86-64-v4" else REF_FAST_SO
+
+
+def reference(fast: bool = False, isa: str = "x86-64-v3") -> Lib:
+    return Lib(reference_path(fast, isa), "ref_")
 
 
 def have_reference(fast: bool = False) -> bool:

@@ -330,6 +330,8 @@ struct RefTrain {
     LatentTrainer lt;
     std::mt19937 rng{ 1 };
     int fd_from = 0;
+    float shadow_pull = 0.0f;   // --dct-shadow-pull (the reference's default 0.01 with a DCT level)
+    int dct_start_it = 0;       // the DCT switch (main.cpp:3804): 0 = the plane is live from the start
 };
 void* ref_train_create(const OrModel* m, const OrTrainCfg* c, const float* z, const float* p, const float* tgt) {
     RefTrain* T = new RefTrain;
@@ -355,7 +357,31 @@ void* ref_train_create_dct(const OrModel* m, const OrTrainCfg* c, const float* z
     D.dct.lambda = lambda; D.dct.rate_es = rate_es != 0; D.dct.rate_trunc = rate_trunc != 0;
     D.zq.assign(D.lat.z.size(), 0.0f);
     D.qes_refresh();
+    T->shadow_pull = 0.01f;   // the default --dct-shadow-pull (main.cpp:175)
     return T;
+}
+// The reference's DCT schedule (main.cpp:3800-3833, 4100-4120 on the CPU branch): level 0 is a continuous
+// plane clamped to [-1,1] until iteration start_it, where the host probe fits the scale codes and the plane
+// goes live (Decoder::dct_fit_all); every refit_every iterations after that, up to refit_until_it and short
+// of the last iteration, the probe is re-run and the plane re-snapped from the shadow (Decoder::dct_refit).
+void* ref_train_create_dct_sched(const OrModel* m, const OrTrainCfg* c, const float* z, const float* p, const float* tgt,
+                                 const OrDct* d, float lambda, int rate_es, int rate_trunc, int start_it, int refit_every,
+                                 int refit_until_it) {
+    RefTrain* T = (RefTrain*)ref_train_create(m, c, z, p, tgt);
+    Decoder& D = T->R.D;
+    D.dct = dct_level_of(d);
+    D.dct.live = false;
+    D.dct.lambda = lambda; D.dct.rate_es = rate_es != 0; D.dct.rate_trunc = rate_trunc != 0;
+    D.dct.refit_every = refit_every; D.dct.refit_until_it = refit_until_it;
+    T->dct_start_it = start_it;
+    T->shadow_pull = 0.01f;
+    D.qes_refresh();   // the pre-start clamp of level 0 (main.cpp:3786)
+    return T;
+}
+void ref_train_set_shadow_pull(void* h, float f) { ((RefTrain*)h)->shadow_pull = f; }
+// --dct-shadow-pull on the CPU branch, as main.cpp:4142-4146 writes it, compiled under this build's flags.
+void ref_shadow_pull(float* z, const float* zq, long long n, float f) {
+    for (long long i = 0; i < n; i++) z[i] += f * (zq[i] - z[i]);
 }
 double ref_train_iter(void* h, int it, int iters) {
     RefTrain& T = *(RefTrain*)h;
@@ -363,11 +389,84 @@ double ref_train_iter(void* h, int it, int iters) {
     double batch_loss = 0, diff_std = 0;
     const bool fd = it >= T.fd_from;
     if (it == T.fd_from) T.mt.adam.init(D.mlp.size());
+    if (D.dct.on && !D.dct.live && it == T.dct_start_it) D.dct_fit_all(it);
+    if (D.dct.live && D.dct.refit_every > 0 && it < iters && it != T.dct_start_it && it <= D.dct.refit_until_it &&
+        it % D.dct.refit_every == 0) {
+        size_t m1 = 0, m2 = 0;
+        D.dct_refit(it, m1, m2);
+    }
     T.mt.cur_it = it;
     batch_loss = fd ? T.mt.step_fd(D, T.R.target, T.rng, o, diff_std) : T.mt.step(D, T.R.target, T.rng, o, diff_std);
     if (!(o.qat > 0 && D.lat.lv.size() == 1)) T.lt.step(D, T.R.target, T.rng, o);
+    if (D.dct.live && T.shadow_pull > 0.0f) {
+        const size_t o0 = D.lat.lv[0].off, n0 = D.lat.lv[0].size();
+        ref_shadow_pull(D.lat.z.data() + o0, D.zq.data() + o0, (long long)n0, T.shadow_pull);
+        D.qes_refresh();
+    }
     if (o.qat > 0 && (it % o.qat_every == 0 || it == iters)) qat_search(D, T.R.target, o.qat_ch);
     return batch_loss;
+}
+// The decode buffer (the snapped copy once a DCT or --qes level is live, otherwise the shadow).
+void ref_train_get_zdec(void* h, float* zdec) {
+    const Decoder& D = ((RefTrain*)h)->R.D;
+    memcpy(zdec, D.zdec(), D.lat.z.size() * sizeof(float));
+}
+// --write-ntcb's rounding of the final weights to fp16 values (main.cpp:2472-2481, 4160); 0 if a weight has no fp16 value.
+int ref_train_round_fp16(void* h) {
+    size_t changed = 0; float maxdw = 0.0f;
+    return ntcb_mlp_round_fp16(((RefTrain*)h)->R.D.mlp.p, changed, maxdw) ? 1 : 0;
+}
+// The loop's whole state in a file (latent, decode buffer, weights, both Adam states, the latent step counter,
+// the DCT level's codes, symbols and flags), so that a long fixture run can be resumed. Returns 1 on success.
+}   // extern "C"
+namespace {
+template <class T> void put_vec(FILE* f, const std::vector<T>& v) {
+    const uint64_t n = v.size();
+    fwrite(&n, sizeof(n), 1, f);
+    if (n) fwrite(v.data(), sizeof(T), n, f);
+}
+template <class T> bool get_vec(FILE* f, std::vector<T>& v) {
+    uint64_t n = 0;
+    if (fread(&n, sizeof(n), 1, f) != 1) return false;
+    v.resize(n);
+    return n == 0 || fread(v.data(), sizeof(T), n, f) == n;
+}
+}   // namespace
+extern "C" {
+int ref_train_save(void* h, const char* path) {
+    RefTrain& T = *(RefTrain*)h;
+    Decoder& D = T.R.D;
+    FILE* f = fopen(path, "wb");
+    if (!f) return 0;
+    const int32_t ints[8] = { T.mt.adam.t, T.lt.adam.t, T.lt.step_no, D.dct.live ? 1 : 0, D.dct.refits, D.dct.refitted_at,
+                              D.dct.fitted_at, 0 };
+    fwrite(ints, sizeof(ints), 1, f);
+    put_vec(f, D.lat.z); put_vec(f, D.zq); put_vec(f, D.mlp.p);
+    put_vec(f, T.mt.adam.m); put_vec(f, T.mt.adam.v); put_vec(f, T.lt.adam.m); put_vec(f, T.lt.adam.v);
+    put_vec(f, D.dct.code); put_vec(f, D.dct.sym); put_vec(f, D.dct.bits);
+    const bool ok = fflush(f) == 0;
+    return (fclose(f) == 0 && ok) ? 1 : 0;
+}
+int ref_train_load(void* h, const char* path) {
+    RefTrain& T = *(RefTrain*)h;
+    Decoder& D = T.R.D;
+    FILE* f = fopen(path, "rb");
+    if (!f) return 0;
+    int32_t ints[8];
+    bool ok = fread(ints, sizeof(ints), 1, f) == 1;
+    ok = ok && get_vec(f, D.lat.z) && get_vec(f, D.zq) && get_vec(f, D.mlp.p);
+    ok = ok && get_vec(f, T.mt.adam.m) && get_vec(f, T.mt.adam.v) && get_vec(f, T.lt.adam.m) && get_vec(f, T.lt.adam.v);
+    ok = ok && get_vec(f, D.dct.code) && get_vec(f, D.dct.sym) && get_vec(f, D.dct.bits);
+    fclose(f);
+    if (!ok) return 0;
+    T.mt.adam.t = ints[0]; T.lt.adam.t = ints[1]; T.lt.step_no = ints[2];
+    D.dct.live = ints[3] != 0; D.dct.refits = ints[4]; D.dct.refitted_at = ints[5]; D.dct.fitted_at = ints[6];
+    return 1;
+}
+// The scale codes of the live DCT level.
+void ref_train_get_dct_codes(void* h, uint8_t* code) {
+    const DctLevel& Q = ((RefTrain*)h)->R.D.dct;
+    memcpy(code, Q.code.data(), Q.code.size());
 }
 void ref_train_get(void* h, float* z, float* p) {
     RefTrain& T = *(RefTrain*)h;

@@ -33,6 +33,8 @@ CASES = {
     "qes_pending": (Model(32, 24, [(16, 12, 4, 0), (8, 6, 3, 0)], [8], T=1), 8, None, [6, 0], False, None),
     "dct1": (Model(32, 24, [(32, 24, 1, 1), (8, 6, 4, 0)], [8], T=1), 8, None, None, False, [50]),
     "dct2": (Model(64, 48, [(64, 48, 2, 1), (16, 12, 4, 0)], [8], T=1), 8, None, [0, 8], True, [75, 30]),
+    # AC symbols beyond the token magnitude cap of 256 (dct_analyze's nmag_over, main.cpp:1113, 1147)
+    "dct_big": (Model(32, 24, [(32, 24, 1, 1), (8, 6, 4, 0)], [8], T=1), 8, None, None, False, [90]),
 }
 
 
@@ -90,6 +92,10 @@ def case_inputs(ref, name, seed):
         zs, zq = np.clip(z[:n0], -1, 1).astype(np.float32), np.zeros(n0, np.float32)
         ref._dct_snap_level0(C.byref(d), C.byref(L0), zs.ctypes.data, zq.ctypes.data, None, None)
         z[:n0], zdec[:n0] = zs, zq
+        if name == "dct_big":                   # large AC symbols (a snap of a [-1, 1] plane stays far below the cap)
+            s3 = sym.reshape(nb * C0, 64)
+            for i, (pos, val) in enumerate([(1, 300), (9, -257), (17, 256), (63, -1000), (8, 4000), (2, 257)]):
+                s3[i % s3.shape[0], pos] = val
         arrs.update(dct_steps=steps, dct_code=code, dct_sym=sym)
         d._keep = (steps, code, sym)
     arrs["zdec"] = zdec

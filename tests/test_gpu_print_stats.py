@@ -74,6 +74,7 @@ def check(orc, tr, lay, pin, qbits, dct=None, label=""):
             assert np.isclose(st.dct_raw[k], s.raw[k], rtol=1e-15) and np.isclose(st.dct_h0[k], s.h0[k], rtol=1e-12)
             assert np.isclose(st.dct_ctx[k], s.ctx[k], rtol=1e-12)
         assert st.dct_nz_mean == s.nz_mean and st.dct_lnz_mean == s.lnz_mean and st.dct_eob_only_frac == s.eob_only_frac
+        assert st.dct_nmag_over == s.nmag_over
     say(f"{label}: bpp q{qbits} {st.bpp_q8:.4f} ent {st.bpp_q8_ent:.4f} est {st.bpp_est:.4f}, quantized mse {st.q_weighted_mse:.4f}"
         + (f", dct nz {st.dct_nz_mean:.2f} bits/blk {st.dct_raw_total / st.dct_nblk:.1f}/{st.dct_h0_total / st.dct_nblk:.1f}/"
            f"{st.dct_ctx_total / st.dct_nblk:.1f}" if dct is not None else ""))
@@ -131,6 +132,26 @@ def test_print_stats_dct(orc, C0, q):
     tr.lat_step(1, 0.05, 0.02, 2)
     d = device_dct(tr, H)
     check(orc, tr, lay, oracle_in(tr, lay, 8, dct=d), 8, dct=d, label=f"dct C{C0}")
+
+
+def test_print_stats_dct_large_symbols(orc):
+    """AC symbols beyond the token magnitude cap (|q| > 256: a plane handed over by set_dct, as a loaded container can
+    carry): the capped magnitude histogram and nmag_over, which the reference counts in both of dct_analyze's passes"""
+    lay = Layout(64, 48, [(64, 48, 1, True), (16, 12, 4, False)], [32, 32], leak=0.01)
+    z, p, tgt = data(lay, 36, zscale=0.7)
+    basis, zz = dct_tables(orc)
+    tr = trainer(lay, z, p, tgt, dct={"C": 1, "dc_step": 4, "q": [90]}, dct_basis=basis, dct_zigzag=zz)
+    H = HostDct(orc, lay, [90], lam=0.3)
+    zd, _ = tr.download_model()
+    H.probe(lay, p, tr.download_zq())
+    H.snap(zd)
+    s3 = H.sym.reshape(-1, 64)
+    for i, (pos, val) in enumerate([(1, 300), (9, -257), (17, 256), (63, -1000), (8, 4000), (2, 257), (3, -300)]):
+        s3[7 * i, pos] = val
+    tr.set_dct(H.desc(), H.code, H.sym, H.steps)   # the device rebuilds its plane from these symbols
+    d = device_dct(tr, H)
+    st = check(orc, tr, lay, oracle_in(tr, lay, 8, dct=d), 8, dct=d, label="dct large symbols")
+    assert st.dct_nmag_over == 2 * 6
 
 
 @pytest.mark.parametrize("name", ["material512", "dct512", "rgb512_two_level"])

@@ -327,8 +327,9 @@ def test_rgb512_two_level_fixed_seed_psnr(orc):
 def test_dct512_fixed_seed_psnr(orc):
     """dct512 (a --dct-q 50 plane as level 0 with the rate proxy in the objective, scale codes from the device's
     decoder-sensitivity probe) trained for 20 iterations at its fixed seed on the device and by the reference's own
-    CPU loop with the same DCT state (codes, steps, --dct-lambda 0.5 with both parts): the final PSNRs of the decoded
-    (snapped) models within 0.05 dB."""
+    CPU loop with the same DCT state (codes, steps, --dct-lambda 0.5 with both parts, the shadow pulled toward the
+    plane by --dct-shadow-pull 0.01 after every latent step): the final PSNRs of the decoded (snapped) models within
+    0.05 dB."""
     iters = 20
     w, lay, tr, z, p, tgt = full_trainer("dct512")
     H = HostDct(orc, lay, w.dct_q, deadzone=0, lam=0.5, lo16=4, rate="both")
@@ -337,12 +338,13 @@ def test_dct512_fixed_seed_psnr(orc):
     zd, _ = tr.download_model()                       # the shadow as the trainer holds it (level 0 clamped)
     H.snap(zd)
     tr.set_dct(H.desc(), H.code, H.sym, H.steps)
-    zr, pr, el = _reference_loop(w, lay, zd, p, tgt, iters, dct=H)
+    zr, pr, el = _reference_loop(w, lay, zd, p, tgt, iters, dct=H)   # with the default --dct-shadow-pull 0.01
+    n0 = lay.levels[0][0] * lay.levels[0][1] * lay.levels[0][2]
     for it in range(1, iters + 1):
         tr.mlp_step(it, w.mlp_sigma, w.mlp_lr, w.mlp_pairs, w.mlp_batch)
         tr.lat_step(it, w.lat_sigma, w.lat_lr, w.lat_pairs)
+        tr.shadow_pull(0, n0, w.shadow_pull)       # main.cpp:4136
     img = tr.decode_full()
-    n0 = lay.levels[0][0] * lay.levels[0][1] * lay.levels[0][2]
     _, zq_r, _, _ = H.snap(zr)                        # the reference's final plane, snapped with the same codes
     _, zq_0, _, _ = H.snap(zd)
     _, ps_0 = mse_psnr(orc, orc.decode_full(lay, p, np.concatenate([zq_0, zd[n0:]])), tgt, lay)

@@ -2,7 +2,8 @@
 per-GPU scratch) against ntc_trainer_decode_error (per-call allocation) through the C ABI: identical
 figures (integer sums of squared 8-bit differences, exact), on two calls in a row - the second over a
 smaller extent, so the scratch still holds the first call's larger set of partials - and with a host
-latent, on RGB and 4-texture models, and on two trainers of different sizes on the same GPU."""
+latent, on RGB and 4-texture models, and on two trainers of different sizes on the same GPU; the library's own
+count of its hipMalloc / hipFree calls is unchanged across every no-allocation call."""
 import numpy as np
 import pytest
 
@@ -26,14 +27,23 @@ def test_noalloc_matches_decode_error(orc, name):
     tr = trainer(lay, z, p, tgt)
     full = tr.decode_error()
     assert full[1] > 0
+    before = tr.device_allocations()
     assert same(tr.decode_error_noalloc(), full)                                  # whole image
+    assert tr.device_allocations() == before                                      # no hipMalloc / hipFree in the call
     ew, eh = lay.W - 7, lay.H // 2
     small = tr.decode_error(ew, eh)
     assert same(tr.decode_error_noalloc(ew, eh), small)                           # then a smaller extent
     assert not same(small, full)
     zq = np.round(z * 4) / 4
-    assert same(tr.decode_error_noalloc(z=zq), tr.decode_error(z=zq))             # a host latent
+    want = tr.decode_error(z=zq)
+    a0 = tr.device_allocations()
+    got = tr.decode_error_noalloc(z=zq)                                          # a host latent
+    assert tr.device_allocations() == a0 and same(got, want)
     assert same(tr.decode_error_noalloc(), full)                                  # and the decode buffer again
+    assert tr.device_allocations() == a0
+    tr.decode_error()
+    a1 = tr.device_allocations()                                                  # the allocating entry point counts
+    assert a1[0] == a0[0] + 1 and a1[1] == a0[1] + 1
     # the oracle's mse_of (pinned to the reference's by a golden vector) of the device's decode
     cw, wsum = lay.loss_weights()
     T = lay.nout // 3
