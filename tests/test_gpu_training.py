@@ -159,10 +159,39 @@ def test_full_size_properties(orc, name):
     say(f"{name}: sampled member losses within {worst:.2e} relative of the oracle")
     assert worst < 1e-5
     # the unperturbed pair of a central-difference step is the loss of w on the step's minibatch
-    tr.mlp_step_fd(2, np.float32(w.fd_h), 0.0, M)
+    h = np.float32(w.fd_h)
+    tr.mlp_step_fd(2, h, 0.0, M)
     l0, _ = tr.mlp_stats()
-    assert rel(l0, orc.loss_subset(lay, p, zdec, tgt, tr.debug_last_batch())) < 1e-6
-    assert np.isfinite(tr.debug_last_dl()).all()
+    idx_fd = tr.debug_last_batch()
+    assert rel(l0, orc.loss_subset(lay, p, zdec, tgt, idx_fd)) < 1e-6
+    dl_fd = tr.debug_last_dl()
+    assert dl_fd.size == p.size and np.isfinite(dl_fd).all()
+    # every weight's loss difference L(w_j + h) - L(w_j - h) (main.cpp:1890-1920) against the oracle on the device's own
+    # minibatch, to 1e-3 of their RMS (the reference's own bar is 1e-2, main.cpp:3034); where the oracle would take
+    # minutes (more than ~100 GFLOP), at weights sampled over every layer
+    hh = (p + h).astype(np.float64) - (p - h).astype(np.float64)    # the steps as realized in float
+    rms = np.sqrt((dl_fd ** 2).mean())
+    if 2 * p.size * M * macs(lay) <= 60e9:
+        dl_o, hh_o, l0_o = orc.mlp_fd_eval(lay, p, zdec, tgt, h, idx_fd)
+        assert np.array_equal(hh_o, hh) and rel(l0, l0_o) < 1e-6
+        js = np.arange(p.size)
+    else:
+        js = np.unique(np.linspace(0, p.size - 1, 12 if M > 65536 else 24).astype(int))
+        dl_o = np.zeros(p.size)
+        for j in js:
+            wpj, wmj = p.copy(), p.copy()
+            wpj[j], wmj[j] = p[j] + h, p[j] - h
+            dl_o[j] = orc.loss_subset(lay, wpj, zdec, tgt, idx_fd) - orc.loss_subset(lay, wmj, zdec, tgt, idx_fd)
+    err = np.abs(dl_fd[js] - dl_o[js]).max() / rms
+    say(f"{name}: central differences of {js.size} of {p.size} weights within {err:.2e} of their RMS ({rms:.3e})")
+    assert err < 1e-3
+    # Adam on the central-difference gradient, after the reset of the switch (main.cpp:4075-4084), bit for bit
+    tr.reset_mlp_adam()
+    tr.mlp_step_fd(2, h, w.mlp_lr, M)
+    assert np.array_equal(tr.debug_last_dl(), dl_fd)
+    pf, m0, v0 = p.copy(), np.zeros_like(p), np.zeros_like(p)
+    orc.adam(pf, orc.fd_grad(dl_fd, hh), m0, v0, w.mlp_lr, 1)
+    assert np.array_equal(tr.download_model()[1], pf)
     tr.mlp_step(3, w.mlp_sigma, w.mlp_lr, N, M)
     assert np.isfinite(tr.download_model()[1]).all()
     tr.lat_step(1, w.lat_sigma, w.lat_lr, w.lat_pairs)
@@ -180,6 +209,11 @@ def test_full_size_properties(orc, name):
         assert g[:n0].any()
     img = tr.decode_full()
     assert np.isfinite(img).all() and img.min() >= 0 and img.max() <= 1
+
+
+def macs(lay) -> int:
+    w = [lay.nin] + list(lay.hidden) + [lay.nout]
+    return sum(w[i] * w[i + 1] for i in range(len(w) - 1))
 
 
 def mse_psnr(orc, img, tgt, lay):
