@@ -368,6 +368,66 @@ __device__ __forceinline__ void features_pm(const DevModel& m, __amdgpu_buffer_r
     }
 }
 
+// Models whose latent step perturbs level 1 only (level 0 searched under --qat, so the step's mask is 2) and whose
+// level-0 channels and positional features fill whole k-steps of the first layer: the latent pair takes those
+// inputs first (level 0, then the positional features, then level 1), so the k-steps over them are one chain of
+// matrix instructions for both members of a pair, which each member's level-1 k-steps continue. Each unit's
+// first-layer sum then adds the same products in that order instead of the reference's (main.cpp:603-627).
+// The shared k-steps, or 0 where the layout has none.
+template <class S>
+constexpr int lat_shared_ksteps() {
+    return (S::kFixed && S::kC2 == 0 && S::kC1 > 0 && (S::kC0 + 2 * S::kNpos) % 4 == 0) ? (S::kC0 + 2 * S::kNpos) / 4 : 0;
+}
+// position p of that order holds input map(p) of the reference's order
+template <class S>
+struct InLatShared {
+    __host__ __device__ static constexpr int map(int p) {
+        return p < S::kC0 ? p : (p < S::kC0 + 2 * S::kNpos ? S::kC0 + S::kC1 + (p - S::kC0) : S::kC0 + (p - S::kC0 - 2 * S::kNpos));
+    }
+};
+template <bool B, class A, class C> struct PickType { using type = A; };
+template <class A, class C> struct PickType<false, A, C> { using type = C; };
+
+// sample_latent of an unperturbed level through its raw buffer (sample_level_pm's loads and blend, one member)
+template <int C>
+__device__ __forceinline__ void sample_level_plain(const DevLevel& L, __amdgpu_buffer_rsrc_t rz, const Tap& t, float* f) {
+    const uint32_t off = (uint32_t)L.off, LW = (uint32_t)L.W, LC = (uint32_t)L.C;
+    const uint32_t a = 4u * (off + ((uint32_t)t.y0 * LW + (uint32_t)t.x0) * LC);
+    if (L.nearest) {
+#pragma unroll
+        for (int c = 0; c < C; c++) f[c] = buffer_f32(rz, a + 4u * c, 0u);
+        return;
+    }
+    const uint32_t tap[4] = { a, 4u * (off + ((uint32_t)t.y0 * LW + (uint32_t)t.x1) * LC),
+                              4u * (off + ((uint32_t)t.y1 * LW + (uint32_t)t.x0) * LC),
+                              4u * (off + ((uint32_t)t.y1 * LW + (uint32_t)t.x1) * LC) };
+    const Blend w = blend_of(t);
+#pragma unroll
+    for (int c = 0; c < C; c++)
+        f[c] = blend(w, buffer_f32(rz, tap[0] + 4u * c, 0u), buffer_f32(rz, tap[1] + 4u * c, 0u), buffer_f32(rz, tap[2] + 4u * c, 0u),
+                     buffer_f32(rz, tap[3] + 4u * c, 0u));
+}
+
+// The features of one pixel for a latent pair in the shared order (lat_shared_ksteps): fs = level 0 and the
+// positional features, common to both members; fp / fm = level 1 perturbed by +sg eps / -sg eps (features_pm's
+// values, in another arrangement).
+template <class S>
+__device__ __forceinline__ void features_lat_shared(const DevModel& m, __amdgpu_buffer_rsrc_t rz, __amdgpu_buffer_rsrc_t re, float sg,
+                                                    int px, int py, float (&fs)[S::kC0 + 2 * S::kNpos], float (&fp)[S::kC1],
+                                                    float (&fm)[S::kC1]) {
+    const float u = pixel_u(px, m.W), v = pixel_u(py, m.H);
+    const Tap t0 = tap_of(m.lv[0].W, m.lv[0].H, m.lv[0].nearest != 0, u, v);
+    const Tap t1 = tap_of(m.lv[1].W, m.lv[1].H, m.lv[1].nearest != 0, u, v);
+    sample_level_plain<S::kC0>(m.lv[0], rz, t0, fs);
+    sample_level_pm<S::kC1>(m.lv[1], rz, re, sg, t1, fp, fm);
+#pragma unroll
+    for (int q = 0; q < S::kNpos; q++) {
+        const bool uv = m.pos[q] == 0;
+        fs[S::kC0 + 2 * q] = __builtin_fmaf(uv ? u : t1.fx, 2.0f, -1.0f);
+        fs[S::kC0 + 2 * q + 1] = __builtin_fmaf(uv ? v : t1.fy, 2.0f, -1.0f);
+    }
+}
+
 // The column and row of pixel base + lane for a wave's 64 pixels from base (a multiple of 64): when the
 // image's width is a multiple of 64 they share one row (a scalar division), else each lane divides (pixels
 // past the last clamped to it).
@@ -384,28 +444,33 @@ __device__ __forceinline__ void round_pixel(const DevModel& m, int base, int lan
 }
 
 
-template <class S, int Act, bool Clamp>
+// Sh > 0: the shared first-layer k-steps of lat_shared_ksteps (the launch's mask must be 2: level 1 perturbed only)
+template <class S, int Act, bool Clamp, int Sh = 0>
 __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* __restrict__ w, const float* __restrict__ zdec,
                                                       const float* __restrict__ eps, const float* __restrict__ tgt, float sg,
                                                       unsigned mask, float* __restrict__ dpix, int rounds) {
     using Q = MfmaShape<S>;
     constexpr int NO = Q::kNout, kRounds = lat_rounds<S>();
+    static_assert(Sh == 0 || Sh == lat_shared_ksteps<S>(), "the shared k-steps of the layout");
+    constexpr int kM = Q::kKs1 - Sh;   // each member's own k-steps of the first layer
     // at most 4 outputs: the output layer on the VALU leaves output g of pixel j in lane (g, j)
     constexpr bool kVOut = valu_out<S>();
     const int k = bid_y();
     const int lane = tid_x() & 63, wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6), i16 = lane & 15, g = lane >> 4;
-    // each wave's LDS exchanges (in place of lane swaps): both members' tile operands, the VALU output layer's
-    // reduce-scatters of both members, the pixel sums of both members' errors
-    constexpr int kWaveLds = 2 * kTilesLds<S> + (kVOut ? 2 * kVoTile : 0) + kSumsLds;
+    // each wave's LDS exchanges (in place of lane swaps): the tile operands (both members', or the shared k-steps
+    // and both members' own), the VALU output layer's reduce-scatters of both members, the pixel sums of both
+    // members' errors
+    constexpr int kTileLds = Sh > 0 ? 4 * 64 * (Sh + 2 * kM) : 2 * kTilesLds<S>;
+    constexpr int kWaveLds = kTileLds + (kVOut ? 2 * kVoTile : 0) + kSumsLds;
     __shared__ __attribute__((aligned(16))) float lds[4 * kWaveLds];
     float* const tl = lds + wave * kWaveLds;
-    float* const vo = tl + 2 * kTilesLds<S>;
+    float* const vo = tl + kTileLds;
     float* const sums = vo + (kVOut ? 2 * kVoTile : 0);
     const __amdgpu_buffer_rsrc_t rz = buffer_of(zdec, 4u * (uint32_t)m.nz), re = buffer_of(eps + (size_t)k * m.nz, 4u * (uint32_t)m.nz),
                                  rn = buffer_of(eps, 0u);   // a level outside the mask: no Gaussians (every load 0)
     float* out = dpix + (size_t)k * m.npix;
     MfmaWeights<S> W;
-    mfma_load<S>(W, w, lane);
+    mfma_load<S, typename PickType<(Sh > 0), InLatShared<S>, InIdentity>::type>(W, w, lane);
     if constexpr (!Clamp) scale_output<S>(W, kNegLog2e);
     if constexpr (Act == kActFold) scale_hidden<S>(W, fold_scale(m.leak));
     const float ak = act_k_of<Act>(m);
@@ -434,14 +499,23 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
         const int base = bid_x() * 256 * rounds + 64 * rounds * wave + 64 * rd;   // tile t: pixels base + 16 t + j
         float tn[4];
         load_t(base, tn);
-        float bp[4][Q::kKs1], bm[4][Q::kKs1];
+        // both members' first-layer operands (Sh = 0), or the shared k-steps' and each member's own (Sh > 0)
+        float bp[4][Sh > 0 ? kM : Q::kKs1], bm[4][Sh > 0 ? kM : Q::kKs1], bs[4][Sh > 0 ? Sh : 1];
         {
             int px, py;
             round_pixel(m, base, lane, px, py);
-            float fp[S::kMaxIn], fm[S::kMaxIn];
-            features_pm<S>(m, rz, re, rn, sg, mask, px, py, fp, fm);
-            tiles_of<S>(fp, bp, tl, g, i16);
-            tiles_of<S>(fm, bm, tl + kTilesLds<S>, g, i16);
+            if constexpr (Sh > 0) {
+                float fs[S::kC0 + 2 * S::kNpos], fp[S::kC1], fm[S::kC1];
+                features_lat_shared<S>(m, rz, re, sg, px, py, fs, fp, fm);
+                tiles_of_n<Sh>(fs, bs, tl, g, i16);
+                tiles_of_n<kM>(fp, bp, tl + 4 * 64 * Sh, g, i16);
+                tiles_of_n<kM>(fm, bm, tl + 4 * 64 * (Sh + kM), g, i16);
+            } else {
+                float fp[S::kMaxIn], fm[S::kMaxIn];
+                features_pm<S>(m, rz, re, rn, sg, mask, px, py, fp, fm);
+                tiles_of<S>(fp, bp, tl, g, i16);
+                tiles_of<S>(fm, bm, tl + kTilesLds<S>, g, i16);
+            }
         }
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -449,23 +523,46 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
 #pragma unroll
             for (int r = 0; r < 4; r++) tt[r] = tn[r];
             if (t + 1 < 4) load_t(base + 16 * (t + 1), tn);
-            float b1[2][Q::kKs1];
-#pragma unroll
-            for (int ks = 0; ks < Q::kKs1; ks++) { b1[0][ks] = bp[t][ks]; b1[1][ks] = bm[t][ks]; }
             const int p = base + 16 * t + i16;
+            // the first layer's pre-activations of both members (D layout)
+            f4v a1[2][Q::kHt];
+            if constexpr (Sh > 0) {
+                f4v as[Q::kHt];
+#pragma unroll
+                for (int ot = 0; ot < Q::kHt; ot++) as[ot] = W.c1[ot];
+#pragma unroll
+                for (int ks = 0; ks < Sh; ks++)
+#pragma unroll
+                    for (int ot = 0; ot < Q::kHt; ot++) as[ot] = mfma4(W.a1[ot][ks], bs[t][ks], as[ot]);
+#pragma unroll
+                for (int ot = 0; ot < Q::kHt; ot++) { a1[0][ot] = as[ot]; a1[1][ot] = as[ot]; }
+#pragma unroll
+                for (int ks = 0; ks < kM; ks++)
+#pragma unroll
+                    for (int v = 0; v < 2; v++)
+#pragma unroll
+                        for (int ot = 0; ot < Q::kHt; ot++) a1[v][ot] = mfma4(W.a1[ot][Sh + ks], v ? bm[t][ks] : bp[t][ks], a1[v][ot]);
+            } else {
+                float b1[2][Q::kKs1];
+#pragma unroll
+                for (int ks = 0; ks < Q::kKs1; ks++) { b1[0][ks] = bp[t][ks]; b1[1][ks] = bm[t][ks]; }
+                mfma_layer1<S, 2>(W, b1, a1);
+            }
             // each lane's channel terms cw (d d) (its out_regs in ascending order, or its one on the VALU output
             // layer), then the pixel's four lane groups added pairwise for each member (group_sums), then e+ - e-
             float ep = 0.0f, em = 0.0f;
             if constexpr (kVOut) {
                 float x[2][Q::kKsH];
-                mfma_hidden<S, 2, Act>(W, b1, ak, x);
+                mfma_hidden_from1<S, 2, Act>(W, a1, ak, x);
                 const float dp = out_of<S>(valu_out_g<S>(W, x[0], vo, g, i16), Clamp) - tt[0],
                             dm = out_of<S>(valu_out_g<S>(W, x[1], vo + kVoTile, g, i16), Clamp) - tt[0];
                 ep = __fmul_rn(cw[0], __fmul_rn(dp, dp));
                 em = __fmul_rn(cw[0], __fmul_rn(dm, dm));
             } else {
+                float x[2][Q::kKsH];
+                mfma_hidden_from1<S, 2, Act>(W, a1, ak, x);
                 f4v o[2];
-                mfma_forward<S, 2, Act>(W, b1, ak, o);
+                mfma_output<S, 2>(W, x, o);
 #pragma unroll
                 for (int r = 0; r < out_regs<S>(); r++) {
                     const float dp = out_of<S>(o[0][r], Clamp) - tt[r], dm = out_of<S>(o[1][r], Clamp) - tt[r];

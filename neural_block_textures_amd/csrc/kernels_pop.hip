@@ -120,7 +120,12 @@ bool lat_pair_on_matrix_cores(const Impl& I) { return pop_on_matrix_cores(I); }
 
 template <class S, int Act>
 static void launch_lat_mfma(Impl& I, int K, float sigma, unsigned mask) {
+    // a step that perturbs level 1 only shares the first layer's level-0 and positional k-steps between the members
+    constexpr int Sh = lat_shared_ksteps<S>();
     auto kern = I.dm.clamp_out ? k_lat_pair_mfma<S, Act, true> : k_lat_pair_mfma<S, Act, false>;
+    if constexpr (Sh > 0) {
+        if (mask == 2u) kern = I.dm.clamp_out ? k_lat_pair_mfma<S, Act, true, Sh> : k_lat_pair_mfma<S, Act, false, Sh>;
+    }
     static_assert(lat_rounds<S>() >= 1, "a latent pair kernel takes at least one round");
     const int rounds = lat_rounds_for(I, lat_rounds<S>(), K), pix = 256 * rounds;
     hipLaunchKernelGGL(kern, dim3((unsigned)((I.npix + pix - 1) / pix), K), dim3(256), 0, I.stream, I.dm, I.w, I.zdec,

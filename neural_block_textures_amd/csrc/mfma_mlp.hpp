@@ -134,11 +134,17 @@ struct MfmaWeights {
     f4v c4;
 };
 
+// The order in which the first layer's k-steps take the model's inputs: position p of the operand rows holds
+// input InMap::map(p) (the identity: the reference's input order).
+struct InIdentity {
+    __host__ __device__ static constexpr int map(int p) { return p; }
+};
+
 // Gathers a member's flat parameter vector (per layer W[out][in] row-major, then b[out]) into
 // operand layout; lane = threadIdx.x % 64. Padding units, inputs and outputs get zero weights: every lane
 // reads a parameter (the index clamped to a valid one) and selects zero where it has none, so the gather
 // takes no branches.
-template <class S, class Get>
+template <class S, class Get, class InMap = InIdentity>
 __device__ __forceinline__ void mfma_load_from(MfmaWeights<S>& W, const Get& w, int lane) {
     using Q = MfmaShape<S>;
     constexpr int NIN = Q::kIn, H = Q::kH, NO = Q::kNout;
@@ -149,7 +155,7 @@ __device__ __forceinline__ void mfma_load_from(MfmaWeights<S>& W, const Get& w, 
         const int u = unit_of<Q>(ot, i16), uc = min(u, H - 1);
 #pragma unroll
         for (int ks = 0; ks < Q::kKs1; ks++) {
-            const int in = 4 * ks + g;
+            const int pos = 4 * ks + g, in = pos < NIN ? InMap::map(pos) : pos;
             W.a1[ot][ks] = at(in < NIN && u < H, uc * NIN + min(in, NIN - 1));
         }
 #pragma unroll
@@ -217,9 +223,9 @@ struct ParamsAt {
     __device__ __forceinline__ float operator()(int k) const { return w[k]; }
 };
 
-template <class S>
+template <class S, class InMap = InIdentity>
 __device__ __forceinline__ void mfma_load(MfmaWeights<S>& W, const float* __restrict__ w, int lane) {
-    mfma_load_from<S>(W, ParamsAt{ w }, lane);
+    mfma_load_from<S, ParamsAt, InMap>(W, ParamsAt{ w }, lane);
 }
 
 // Output weights and biases times sc (the evaluations with the hardware sigmoid fold its -log2(e)
@@ -484,6 +490,24 @@ __device__ __forceinline__ void tiles_of(const float (&f)[S::kMaxIn], float (&b)
 #pragma unroll
     for (int ks = 0; ks < Q::kKs1; ks++) {
         const f4v v = *reinterpret_cast<const f4v*>(t + ((g * Q::kKs1 + ks) * 16 + j) * 4);
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) b[tt][ks] = v[tt];
+    }
+    wave_lds_fence();
+}
+
+// tiles_of for NK k-steps of values f[0 .. N) (zero from N on): b[t][ks] in lane (g, j) = value 4 ks + g of the
+// pixel that lane (t, j) built, through 4 NK 64 floats of the wave's LDS.
+template <int NK, int N>
+__device__ __forceinline__ void tiles_of_n(const float (&f)[N], float (&b)[4][NK], float* __restrict__ t, int g, int j) {
+#pragma unroll
+    for (int ks = 0; ks < NK; ks++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) t[((r * NK + ks) * 16 + j) * 4 + g] = 4 * ks + r < N ? f[4 * ks + r] : 0.0f;
+    wave_lds_fence();
+#pragma unroll
+    for (int ks = 0; ks < NK; ks++) {
+        const f4v v = *reinterpret_cast<const f4v*>(t + ((g * NK + ks) * 16 + j) * 4);
 #pragma unroll
         for (int tt = 0; tt < 4; tt++) b[tt][ks] = v[tt];
     }
