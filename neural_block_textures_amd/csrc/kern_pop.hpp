@@ -285,6 +285,189 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     }
 }
 
+// ---- The ES population with the pair's first layer shared (models with more than 4 outputs and at most two
+// 16-unit hidden tiles, whose minibatch's first-layer pre-activations stay in the L2). The two members of a pair differ
+// in every weight by +-sigma eps, so their first layers are h+- = u +- d with u the unperturbed layer's pre-activations
+// (bias + w x, the same for every pair; the minibatch launch computes it once per step, lay1[unit][slot]) and d the
+// perturbation's: h- = 2 u - h+, one fused multiply-add per value instead of the - member's first-layer matrix
+// instructions. A wave evaluates both members of its pair on one 16-slot tile at a time (two independent chains
+// after the first layer), on tiles wave, wave + 4, ... of the chunk; the member's A operands stay in VGPRs, the
+// biases come from LDS rows in operand layout (every lane of a group reads the same 16 bytes), so the two members'
+// weights fit the four waves per SIMD the chains need. Every parameter is the reference's w0 +- sigma eps
+// (main.cpp:1852-1856) scaled as k_pop_mfma scales it; the - member's first layer is within a few roundings of its
+// own chain's, inside the 1e-5 member-loss bar.
+template <class S, bool = MfmaShape<S>::kOk>
+struct PopPairOk { static constexpr bool value = false; };
+template <class S>
+struct PopPairOk<S, true> { static constexpr bool value = !valu_out<S>() && MfmaShape<S>::kHt <= 2 && MfmaShape<S>::kH % 16 == 0; };
+template <class S>
+constexpr bool pop_pair_ok() { return PopPairOk<S>::value; }
+// bias rows per member: the first layer's kHt tiles, each deeper hidden layer's kHt, the output tile
+template <class S>
+constexpr int pair_bias_rows() { return MfmaShape<S>::kHt * MfmaShape<S>::kNL + 1; }
+// a member's parameters in LDS, padded to whole 16-byte pieces
+template <class S>
+constexpr int pair_p_pad() { return (MfmaShape<S>::kP + 3) & ~3; }
+
+template <class S, bool Clamp, int From>
+__global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_per_eu(4))) k_pop_pair(DevModel m, PopSource src, int M, int Mcap,
+                                                            int chunk, int chunks, const float* __restrict__ feat,
+                                                            const float* __restrict__ btgt, const float* __restrict__ lay1,
+                                                            double* __restrict__ part) {
+    using Q = MfmaShape<S>;
+    static_assert(From != kSets && pop_pair_ok<S>(), "an ES step of a shape the pair kernel takes");
+    constexpr int H = Q::kH, NIN = Q::kIn, NO = Q::kNout, RO = out_regs<S>(), NB = pair_bias_rows<S>(), PP = pair_p_pad<S>();
+    constexpr int kPout = H * NIN + H + (Q::kNL - 1) * (H * H + H);   // the first output-layer parameter
+    __shared__ double red[2][kPopWaves];
+    __shared__ __attribute__((aligned(16))) float wpm_s[2 * PP];          // the + member's parameters, then the - member's
+    __shared__ __attribute__((aligned(16))) float bias_s[2 * NB * 16];    // [member][row][4 g + r]
+    __shared__ __attribute__((aligned(16))) float cw_s[16];               // the channel weight of register r of group g
+    const int lane = tid_x() & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
+    const int pair = bid_x(), ch = bid_y();
+    const int i16 = lane & 15, g = lane >> 4;
+    const int s0 = ch * chunk, s1 = min(M, s0 + chunk);
+    const int tiles = (s1 - s0 + 15) >> 4;
+    const int mine = (tiles - wave + kPopWaves - 1) / kPopWaves;   // this wave's tiles: wave + 4 j, j < mine
+    // lane byte offsets: feature rows 4 ks + g, first-layer rows 16 ot + 4 g + r, target rows out_at(g, r) (a valid row
+    // for padding: its channel weight is zero)
+    // (register r of lane group g holds output RO g + r, so row r of a group is its first row + r)
+    static_assert(out_at<S>(3, RO - 1) == 3 * RO + RO - 1 || out_at<S>(3, RO - 1) < 0, "packed output rows");
+    const uint32_t fo = 4u * ((uint32_t)g * (uint32_t)Mcap + (uint32_t)i16);
+    const uint32_t uo = 4u * (4u * (uint32_t)g * (uint32_t)Mcap + (uint32_t)i16);
+    const uint32_t to = 4u * ((uint32_t)min(RO * g, NO - RO) * (uint32_t)Mcap + (uint32_t)i16);
+    const __amdgpu_buffer_rsrc_t rf = buffer_of(feat, 4u * ((uint32_t)minibatch_rows(NIN) * (uint32_t)Mcap + (uint32_t)kMinibatchSlack));
+    const __amdgpu_buffer_rsrc_t rt = buffer_of(btgt, 4u * ((uint32_t)NO * (uint32_t)Mcap + (uint32_t)kMinibatchSlack));
+    const __amdgpu_buffer_rsrc_t ru = buffer_of(lay1, 4u * ((uint32_t)H * (uint32_t)Mcap + (uint32_t)kMinibatchSlack));
+    struct TileIn { float b1[Q::kKs1]; float u[Q::kHt][4]; float t[RO]; };
+    auto load = [&](TileIn& in, int j) {   // tile wave + 4 j (uniform)
+        const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane((int)(4u * (uint32_t)(s0 + 16 * (wave + kPopWaves * j))));
+#pragma unroll
+        for (int ks = 0; ks < Q::kKs1; ks++) in.b1[ks] = buffer_f32(rf, fo, so + 16u * (uint32_t)ks * (uint32_t)Mcap);
+#pragma unroll
+        for (int ot = 0; ot < Q::kHt; ot++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) in.u[ot][r] = buffer_f32(ru, uo, so + 4u * (uint32_t)(16 * ot + r) * (uint32_t)Mcap);
+#pragma unroll
+        for (int r = 0; r < RO; r++) in.t[r] = buffer_f32(rt, to, so + 4u * (uint32_t)r * (uint32_t)Mcap);
+    };
+    TileIn in0, in1;
+    load(in0, 0);
+    // stage both members: w0 +- sigma eps, scaled as k_pop_mfma scales its registers (the hidden layers by the folded
+    // activation's (1 + leak) / 2, the output layer by -log2 e for the hardware sigmoid); the biases also to their
+    // operand rows
+    {
+        const uint64_t head = noise_head(src.seed, NS_MLP, src.step, (uint32_t)pair);
+        float* eg = src.eps + (size_t)pair * Q::kP;
+        const float fb = fold_scale(m.leak);
+        if (tid_x() < 16) {   // the output tile's padding rows; the channel weights (zero on padding)
+            const int gg = tid_x() >> 2, r = tid_x() & 3, c = out_at<S>(gg, r);
+            if (c < 0) { bias_s[(NB - 1) * 16 + tid_x()] = 0.0f; bias_s[(2 * NB - 1) * 16 + tid_x()] = 0.0f; }
+            cw_s[tid_x()] = c < 0 ? 0.0f : m.cw[c];
+        }
+        for (int k = tid_x(); k < Q::kP; k += 64 * kPopWaves) {
+            float e;
+            if constexpr (From == kDraw) {
+                e = gauss_at(src.nt, head, (uint64_t)k);
+                if (ch == 0) eg[k] = e;
+            } else {
+                e = eg[k];
+            }
+            const float w0 = src.w0[k];
+            const float sc = k < kPout ? fb : (Clamp ? 1.0f : kNegLog2e);
+            const float vp = __builtin_fmaf(src.sigma, e, w0) * sc, vm = __builtin_fmaf(-src.sigma, e, w0) * sc;
+            wpm_s[k] = vp;
+            wpm_s[PP + k] = vm;
+            int row = -1, col = 0;   // a bias: its operand row and column
+            if (k >= H * NIN && k < H * NIN + H) {
+                row = (k - H * NIN) >> 4; col = (k - H * NIN) & 15;
+            } else if (k >= H * NIN + H && k < kPout) {
+                const int q = k - (H * NIN + H), l = q / (H * H + H), o = q - l * (H * H + H) - H * H;
+                if (o >= 0) { row = Q::kHt * (1 + l) + (o >> 4); col = o & 15; }
+            } else if (k >= kPout + NO * H) {
+                const int c = k - (kPout + NO * H);
+                row = NB - 1; col = 4 * (c / RO) + c % RO;   // output c sits in register c % RO of lane group c / RO
+            }
+            if (row >= 0) { bias_s[row * 16 + col] = vp; bias_s[(NB + row) * 16 + col] = vm; }
+        }
+    }
+    __syncthreads();
+    MfmaWeights<S> Wp, Wm;   // the A operands of both members (their bias fields unused)
+    mfma_load<S>(Wp, wpm_s, lane);
+    mfma_load<S>(Wm, wpm_s + PP, lane);
+    const float ak = act_k_of<kActFold>(m);
+    auto bias = [&](int mem, int row) { return *reinterpret_cast<const f4v*>(bias_s + (mem * NB + row) * 16 + 4 * g); };
+    double ep = 0.0, em = 0.0;
+    auto pass = [&](TileIn& c, TileIn& n, int j) {
+        j = __builtin_amdgcn_readfirstlane(j);
+        load(n, j + 1 < mine ? j + 1 : j);
+        // first layer: the + member's chain, the - member as 2 u - h+
+        f4v hp[Q::kHt], hm[Q::kHt];
+#pragma unroll
+        for (int ot = 0; ot < Q::kHt; ot++) hp[ot] = bias(0, ot);
+#pragma unroll
+        for (int ks = 0; ks < Q::kKs1; ks++)
+#pragma unroll
+            for (int ot = 0; ot < Q::kHt; ot++) hp[ot] = mfma4(Wp.a1[ot][ks], c.b1[ks], hp[ot]);
+#pragma unroll
+        for (int ot = 0; ot < Q::kHt; ot++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) hm[ot][r] = __builtin_fmaf(2.0f, c.u[ot][r], -hp[ot][r]);
+        float xp[Q::kKsH], xm[Q::kKsH];
+#pragma unroll
+        for (int ot = 0; ot < Q::kHt; ot++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) { xp[4 * ot + r] = act<kActFold>(hp[ot][r], ak); xm[4 * ot + r] = act<kActFold>(hm[ot][r], ak); }
+#pragma unroll
+        for (int l = 0; l < Q::kNL - 1; l++) {
+            f4v ap[Q::kHt], am[Q::kHt];
+#pragma unroll
+            for (int ot = 0; ot < Q::kHt; ot++) { ap[ot] = bias(0, Q::kHt * (1 + l) + ot); am[ot] = bias(1, Q::kHt * (1 + l) + ot); }
+#pragma unroll
+            for (int ks = 0; ks < Q::kKsH; ks++)
+#pragma unroll
+                for (int ot = 0; ot < Q::kHt; ot++) {
+                    ap[ot] = mfma4(Wp.ah[l][ot][ks], xp[ks], ap[ot]);
+                    am[ot] = mfma4(Wm.ah[l][ot][ks], xm[ks], am[ot]);
+                }
+#pragma unroll
+            for (int ot = 0; ot < Q::kHt; ot++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) { xp[4 * ot + r] = act<kActFold>(ap[ot][r], ak); xm[4 * ot + r] = act<kActFold>(am[ot][r], ak); }
+        }
+        f4v op = bias(0, NB - 1), om = bias(1, NB - 1);
+#pragma unroll
+        for (int ks = 0; ks < Q::kKsH; ks++) {
+            op = mfma4(Wp.ao[ks], xp[ks], op);
+            om = mfma4(Wm.ao[ks], xm[ks], om);
+        }
+        // each member's channel terms cw (d d): one multiply and one fused multiply-add each, summed in float over the
+        // tile's outputs in this lane, then into the member's double
+        float tp = 0.0f, tm = 0.0f;
+        const f4v cw = *reinterpret_cast<const f4v*>(cw_s + 4 * g);
+#pragma unroll
+        for (int r = 0; r < RO; r++) {
+            const float dp = out_of<S>(op[r], Clamp) - c.t[r], dm = out_of<S>(om[r], Clamp) - c.t[r];
+            tp = __builtin_fmaf(__fmul_rn(cw[r], dp), dp, tp);
+            tm = __builtin_fmaf(__fmul_rn(cw[r], dm), dm, tm);
+        }
+        if (s0 + 16 * (wave + kPopWaves * j) + i16 < s1) { ep += (double)tp; em += (double)tm; }
+    };
+    for (int j = 0; j < mine; j += 2) {
+        pass(in0, in1, j);
+        if (j + 1 >= mine) break;
+        pass(in1, in0, j + 1);
+    }
+    ep = wave_sum(ep);
+    em = wave_sum(em);
+    if (lane == 0) { red[0][wave] = ep; red[1][wave] = em; }
+    __syncthreads();
+    if (tid_x() == 0) {
+        part[(size_t)(2 * pair) * chunks + ch] = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+        part[(size_t)(2 * pair + 1) * chunks + ch] = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    }
+}
+
 // The latent pair evaluation (LatentTrainer::step_impl, main.cpp:1990-2007) on the matrix cores:
 // block (512 or 256 pixels, pair k), each wave a quarter of them in rounds of 64. In a round every
 // lane builds the features of its own pixel with the pair's texels perturbed by +sg eps and by

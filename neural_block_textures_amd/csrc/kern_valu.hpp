@@ -26,12 +26,20 @@ struct EpsJob {
     int first_block;
 };
 
+// The unperturbed first layer of every minibatch slot, for the population kernel that shares it between the members of
+// a pair (k_pop_pair): out[u][s] = fl(b_u fb) + sum_i fl(w_ui fb) f_i as one chain of fused multiply-adds in input order
+// (the matrix instructions' order), fb the folded activation's scale. w null: none.
+struct Lay1Job {
+    const float* w;
+    float* out;
+};
+
 // The minibatch (draw_batch with the counter draw): slot s -> pixel, its feature column
 // feat[.][s] and target column btgt[.][s] (structure of arrays, so the evaluation reads coalesced).
 template <class S>
 __global__ void __launch_bounds__(kTPB) k_batch(DevModel m, uint64_t head, int M, int Mcap, const float* __restrict__ zdec,
                                                const float* __restrict__ tgt, int* __restrict__ bidx,
-                                               float* __restrict__ feat, float* __restrict__ btgt, EpsJob ej) {
+                                               float* __restrict__ feat, float* __restrict__ btgt, EpsJob ej, Lay1Job l1) {
     if ((int)blockIdx.x >= ej.first_block) {
         const long long t = (long long)(blockIdx.x - ej.first_block) * kTPB + threadIdx.x;
         if (t < (long long)ej.N * ej.P) {
@@ -55,6 +63,19 @@ __global__ void __launch_bounds__(kTPB) k_batch(DevModel m, uint64_t head, int M
     }
     const float* t = tgt + (size_t)idx * m.nout;
     for (int c = 0; c < m.nout; c++) btgt[(size_t)c * Mcap + s] = t[c];
+    if constexpr (S::kFixed && S::kUniform) {
+        if (l1.w) {
+            constexpr int H = S::kH, NIN = S::kNin;
+            const float fb = 0.5f * (1.0f + m.leak);
+#pragma unroll 4
+            for (int u = 0; u < H; u++) {
+                float a = l1.w[H * NIN + u] * fb;
+#pragma unroll
+                for (int i = 0; i < NIN; i++) a = __builtin_fmaf(l1.w[u * NIN + i] * fb, f[i], a);
+                l1.out[(size_t)u * Mcap + s] = a;
+            }
+        }
+    }
 }
 
 // The population evaluation: block (pair, chunk) evaluates both members of the pair on the

@@ -229,19 +229,24 @@ void launch_fill(Impl& I, float* p, size_t n, float v) {
     NTC_CHECK(hipGetLastError());
 }
 
-void launch_batch(Impl& I, int it, int M, int eps_pairs) {
+void launch_batch(Impl& I, int it, int M, int eps_pairs, bool lay1) {
     const uint64_t head = noise_head(I.d.seed, NS_BATCH_PIX, (uint32_t)it, 0);
     const unsigned nb = blocks_for(M, kTPB);
     EpsJob ej{ I.noise, I.d.seed, (uint32_t)it, eps_pairs, I.P, I.eps_mlp, (int)nb };
+    if (lay1 && !I.lay1) {
+        fprintf(stderr, "ntc_hip backend: minibatch launch asked for the first layer without its buffer\n");
+        exit(1);
+    }
+    Lay1Job l1{ lay1 ? I.w : nullptr, lay1 ? I.lay1 : nullptr };
     const unsigned grid = nb + (eps_pairs > 0 ? blocks_for((size_t)eps_pairs * I.P, kTPB) : 0u);
     ProfScope ps(I, "batch");
     if (I.jit) {
         jit_launch(k_batch<ShapeDefault>, I, "k_batch", "", dim3(grid), dim3(kTPB), 0, I.dm, head, M, I.Mcap, I.zdec,
-                   I.tgt, I.bidx, I.feat, I.btgt, ej);
+                   I.tgt, I.bidx, I.feat, I.btgt, ej, l1);
     } else dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         hipLaunchKernelGGL(k_batch<S>, dim3(grid), dim3(kTPB), 0, I.stream, I.dm, head, M, I.Mcap, I.zdec, I.tgt,
-                           I.bidx, I.feat, I.btgt, ej);
+                           I.bidx, I.feat, I.btgt, ej, l1);
     });
     NTC_CHECK(hipGetLastError());
 }

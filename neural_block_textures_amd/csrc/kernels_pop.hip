@@ -93,12 +93,44 @@ void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks) {
     launch_pop_matrix<kSets>(I, src, pairs, M, chunk, chunks);
 }
 
+// The pair-sharing population kernel (k_pop_pair) takes an ES step of a fixed shape it supports whose minibatch's
+// first layer stays in the L2 (H x Mcap floats within 2 MiB); NTC_HIP_POP_PAIR=0 keeps k_pop_mfma for every step.
+bool pop_pair_possible(const Impl& I) {
+    if (I.jit || I.valu_only || !(I.dm.leak >= 0.0f && I.dm.leak <= 1.0f)) return false;
+    const char* env = getenv("NTC_HIP_POP_PAIR");
+    if (env && env[0] == '0') return false;
+    bool ok = false;
+    dispatch_shape(I.dm, [&](auto s) {
+        using S = decltype(s);
+        if constexpr (pop_pair_ok<S>()) ok = (size_t)MfmaShape<S>::kH * (size_t)I.Mcap * sizeof(float) <= ((size_t)2 << 20);
+    });
+    return ok;
+}
+
+template <int From>
+static void launch_pop_pair(Impl& I, const PopSource& src, int N, int M, int chunk, int chunks) {
+    dispatch_shape(I.dm, [&](auto s) {
+        using S = decltype(s);
+        if constexpr (pop_pair_ok<S>()) {
+            auto kern = I.dm.clamp_out ? k_pop_pair<S, true, From> : k_pop_pair<S, false, From>;
+            launch_timed(kern, I, dim3(N, chunks), dim3(64 * kPopWaves), 0, I.dm, src, M, I.Mcap, chunk, chunks, I.feat, I.btgt,
+                         (const float*)I.lay1, I.part);
+        }
+    });
+    NTC_CHECK(hipGetLastError());
+}
+
 void launch_pop_eval_es(Impl& I, int it, float sigma, int N, int M, int chunk, int chunks) {
     check_pop_launch(I, N, chunk, chunks);
     PopSource src{};
     src.nt = I.noise; src.seed = I.d.seed; src.step = (uint32_t)it; src.sigma = sigma;
     src.w0 = I.w; src.eps = I.eps_mlp;
     ProfScope ps(I, "pop_eval", true);
+    if (I.pop_pair && pop_on_matrix_cores(I)) {   // the step's minibatch launch wrote the first layer
+        if (pop_reads_eps(chunks)) launch_pop_pair<kReadEps>(I, src, N, M, chunk, chunks);
+        else launch_pop_pair<kDraw>(I, src, N, M, chunk, chunks);
+        return;
+    }
     if (pop_reads_eps(chunks)) launch_pop_matrix<kReadEps>(I, src, N, M, chunk, chunks);   // drawn by the minibatch launch
     else launch_pop_matrix<kDraw>(I, src, N, M, chunk, chunks);
 }

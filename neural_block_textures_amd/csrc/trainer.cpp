@@ -200,7 +200,7 @@ Trainer::~Trainer() {
             for (auto& ev : kv.second.pending) { (void)hipEventDestroy(ev.first); (void)hipEventDestroy(ev.second); }
         dev_free(I.z); dev_free(I.zq); dev_free(I.zgrad); dev_free(I.zm); dev_free(I.zv); dev_free(I.ztmp);
         dev_free(I.w); dev_free(I.wgrad); dev_free(I.wm); dev_free(I.wv);
-        dev_free(I.tgt); dev_free(I.img); dev_free(I.feat); dev_free(I.btgt); dev_free(I.bidx);
+        dev_free(I.tgt); dev_free(I.img); dev_free(I.feat); dev_free(I.btgt); dev_free(I.bidx); dev_free(I.lay1);
         dev_free(I.wsets); dev_free(I.eps_mlp); dev_free(I.gpart); dev_free(I.part); dev_free(I.dl); dev_free(I.lsum); dev_free(I.hh);
         dev_free(I.eps_lat); dev_free(I.eps_ahead); dev_free(I.dpix); dev_free(I.ranges); dev_free(I.qat_grid); dev_free(I.qat_bits);
         dev_free(I.qes_dev); dev_free(I.qgrid);
@@ -394,6 +394,12 @@ bool Trainer::init(const ModelDesc& d, const float* z, const float* p, const flo
             fprintf(stderr, "ntc_hip backend: the runtime-shaped kernels run this model (%s)\n", jwhy.c_str());
         }
     }
+    I.pop_pair = pop_pair_possible(I);
+    if (I.pop_pair) {
+        const size_t n = (size_t)I.d.hidden[0] * I.Mcap + kMinibatchSlack;
+        dev_alloc(&I.lay1, n);
+        NTC_CHECK(hipMemset(I.lay1, 0, n * sizeof(float)));
+    }
     upload_model(z, p);
     return true;
 }
@@ -510,7 +516,8 @@ void Trainer::mlp_step(int it, float sigma, float lr, int N, int M) {
     }
     const int chunk = pop_chunk(I, N, M), chunks = (M + chunk - 1) / chunk;
     const bool mfma = pop_on_matrix_cores(I);
-    launch_batch(I, it, M, mfma && pop_reads_eps(chunks) ? N : 0);   // with the Gaussians the population kernel reads
+    // with the Gaussians the population kernel reads, and the first layer the pair-sharing kernel reads
+    launch_batch(I, it, M, mfma && pop_reads_eps(chunks) ? N : 0, mfma && I.pop_pair);
     ensure_part(I, (size_t)2 * N * chunks);
     if (mfma) {
         launch_pop_eval_es(I, it, sigma, N, M, chunk, chunks);   // stages the perturbed weights itself
