@@ -339,17 +339,19 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     const __amdgpu_buffer_rsrc_t rf = buffer_of(feat, 4u * ((uint32_t)minibatch_rows(NIN) * (uint32_t)Mcap + (uint32_t)kMinibatchSlack));
     const __amdgpu_buffer_rsrc_t rt = buffer_of(btgt, 4u * ((uint32_t)NO * (uint32_t)Mcap + (uint32_t)kMinibatchSlack));
     const __amdgpu_buffer_rsrc_t ru = buffer_of(lay1, 4u * ((uint32_t)H * (uint32_t)Mcap + (uint32_t)kMinibatchSlack));
-    struct TileIn { float b1[Q::kKs1]; float u[Q::kHt][4]; float t[RO]; };
-    auto load = [&](TileIn& in, int j) {   // tile wave + 4 j (uniform)
-        const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane((int)(4u * (uint32_t)(s0 + 16 * (wave + kPopWaves * j))));
+    // a tile's inputs, loaded one pass ahead; its targets at the start of its own pass (used at the end)
+    struct TileIn { float b1[Q::kKs1]; float u[Q::kHt][4]; };
+    auto tile_off = [&](int j) {   // tile wave + 4 j (uniform)
+        return (uint32_t)__builtin_amdgcn_readfirstlane((int)(4u * (uint32_t)(s0 + 16 * (wave + kPopWaves * j))));
+    };
+    auto load = [&](TileIn& in, int j) {
+        const uint32_t so = tile_off(j);
 #pragma unroll
         for (int ks = 0; ks < Q::kKs1; ks++) in.b1[ks] = buffer_f32(rf, fo, so + 16u * (uint32_t)ks * (uint32_t)Mcap);
 #pragma unroll
         for (int ot = 0; ot < Q::kHt; ot++)
 #pragma unroll
             for (int r = 0; r < 4; r++) in.u[ot][r] = buffer_f32(ru, uo, so + 4u * (uint32_t)(16 * ot + r) * (uint32_t)Mcap);
-#pragma unroll
-        for (int r = 0; r < RO; r++) in.t[r] = buffer_f32(rt, to, so + 4u * (uint32_t)r * (uint32_t)Mcap);
     };
     TileIn in0, in1;
     load(in0, 0);
@@ -400,6 +402,12 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     double ep = 0.0, em = 0.0;
     auto pass = [&](TileIn& c, TileIn& n, int j) {
         j = __builtin_amdgcn_readfirstlane(j);
+        float tt[RO];
+        {
+            const uint32_t so = tile_off(j);
+#pragma unroll
+            for (int r = 0; r < RO; r++) tt[r] = buffer_f32(rt, to, so + 4u * (uint32_t)r * (uint32_t)Mcap);
+        }
         load(n, j + 1 < mine ? j + 1 : j);
         // first layer: the + member's chain, the - member as 2 u - h+
         f4v hp[Q::kHt], hm[Q::kHt];
@@ -447,7 +455,7 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
         const f4v cw = *reinterpret_cast<const f4v*>(cw_s + 4 * g);
 #pragma unroll
         for (int r = 0; r < RO; r++) {
-            const float dp = out_of<S>(op[r], Clamp) - c.t[r], dm = out_of<S>(om[r], Clamp) - c.t[r];
+            const float dp = out_of<S>(op[r], Clamp) - tt[r], dm = out_of<S>(om[r], Clamp) - tt[r];
             tp = __builtin_fmaf(__fmul_rn(cw[r], dp), dp, tp);
             tm = __builtin_fmaf(__fmul_rn(cw[r], dm), dm, tm);
         }
@@ -854,8 +862,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(qat_oc
             // best over the other candidates in ascending k, from +inf with a strict <; a NaN loss never wins and a NaN
             // current loss keeps the current value, as the reference's running minimum from the current loss gives
             // (main.cpp:2122-2127). The NaN tests are on the bits: this file is compiled assuming no NaNs.
+            // (selects, not branches: the choice is per lane. A best_l still at +inf means no other candidate won.)
             float cur_l = 0.0f, best_l = __builtin_inff(), cur_v = 0.0f, best_v = 0.0f;
-            int best_k = -1;
             // The first layer's sums of the tile without input c (a zero in its place: fma(w, 0, s) = s) and, in D
             // layout, the weight of input c into each of this lane's units (read from the lane of W.a1 that holds
             // it): a candidate's first-layer pre-activations are then one fused multiply-add, w_c gc + base, and
@@ -909,12 +917,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(qat_oc
 #pragma unroll
                 for (int v = 0; v < 2; v++) {
                     const float l = ls[v];
-                    if (kc + v == cur) { cur_l = l; cur_v = gc[v]; }
-                    else if (not_nan_bits(l) && l < best_l) { best_l = l; best_k = kc + v; best_v = gc[v]; }
+                    const bool is_cur = kc + v == cur;
+                    const bool better = !is_cur && not_nan_bits(l) && l < best_l;
+                    cur_l = is_cur ? l : cur_l;
+                    cur_v = is_cur ? gc[v] : cur_v;
+                    best_l = better ? l : best_l;
+                    best_v = better ? gc[v] : best_v;
                 }
             }
             // cur is in 0 .. levels (qat_index clamps), so cur_v is its grid value
-            const float win_v = (best_k >= 0 && not_nan_bits(cur_l) && best_l < cur_l) ? best_v : cur_v;
+            const float win_v = (not_nan_bits(cur_l) && best_l < cur_l) ? best_v : cur_v;
             if (g == c % 4) b[t][c / 4] = win_v;
             const int p = base + 16 * t + i16;
             if (g == 0 && p < m.npix) zdec[m.lv[0].off + (size_t)p * m.lv[0].C + c] = win_v;

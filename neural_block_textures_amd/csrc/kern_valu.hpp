@@ -34,6 +34,12 @@ struct Lay1Job {
     float* out;
 };
 
+// floats of the first layer's weights and biases (fixed shapes of one hidden width; 1 otherwise)
+template <class S, bool = S::kFixed && S::kUniform>
+struct FirstLayerSize { static constexpr int value = 1; };
+template <class S>
+struct FirstLayerSize<S, true> { static constexpr int value = S::kH * (S::kNin + 1); };
+
 // The minibatch (draw_batch with the counter draw): slot s -> pixel, its feature column
 // feat[.][s] and target column btgt[.][s] (structure of arrays, so the evaluation reads coalesced).
 template <class S>
@@ -47,6 +53,16 @@ __global__ void __launch_bounds__(kTPB) k_batch(DevModel m, uint64_t head, int M
             ej.eps[t] = gauss_at(ej.nt, noise_head(ej.seed, NS_MLP, ej.step, (uint32_t)i), (uint64_t)k);
         }
         return;
+    }
+    // the first layer's weights and biases times fb, once per block (the Lay1Job below reads them from LDS)
+    constexpr int kW1 = FirstLayerSize<S>::value;
+    __shared__ float w1_s[kW1];
+    if constexpr (S::kFixed && S::kUniform) {
+        if (l1.w) {   // uniform: the whole block stages, before any thread leaves
+            const float fb = 0.5f * (1.0f + m.leak);
+            for (int k = (int)threadIdx.x; k < kW1; k += kTPB) w1_s[k] = l1.w[k] * fb;
+            __syncthreads();
+        }
     }
     const int s = blockIdx.x * kTPB + threadIdx.x;
     if (s >= M) return;
@@ -66,12 +82,11 @@ __global__ void __launch_bounds__(kTPB) k_batch(DevModel m, uint64_t head, int M
     if constexpr (S::kFixed && S::kUniform) {
         if (l1.w) {
             constexpr int H = S::kH, NIN = S::kNin;
-            const float fb = 0.5f * (1.0f + m.leak);
-#pragma unroll 4
-            for (int u = 0; u < H; u++) {
-                float a = l1.w[H * NIN + u] * fb;
 #pragma unroll
-                for (int i = 0; i < NIN; i++) a = __builtin_fmaf(l1.w[u * NIN + i] * fb, f[i], a);
+            for (int u = 0; u < H; u++) {
+                float a = w1_s[H * NIN + u];
+#pragma unroll
+                for (int i = 0; i < NIN; i++) a = __builtin_fmaf(w1_s[u * NIN + i], f[i], a);
                 l1.out[(size_t)u * Mcap + s] = a;
             }
         }
