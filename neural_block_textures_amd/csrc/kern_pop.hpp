@@ -309,7 +309,8 @@ constexpr int pair_bias_rows() { return MfmaShape<S>::kHt * MfmaShape<S>::kNL + 
 template <class S>
 constexpr int pair_p_pad() { return (MfmaShape<S>::kP + 3) & ~3; }
 
-template <class S, bool Clamp, int From>
+// UnitCw: every channel weight is 1 (a single texture, or equally weighted ones), so cw (d d) is d d without a multiply
+template <class S, bool Clamp, int From, bool UnitCw>
 __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_per_eu(4))) k_pop_pair(DevModel m, PopSource src, int M, int Mcap,
                                                             int chunk, int chunks, const float* __restrict__ feat,
                                                             const float* __restrict__ btgt, const float* __restrict__ lay1,
@@ -400,6 +401,7 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     const float ak = act_k_of<kActFold>(m);
     auto bias = [&](int mem, int row) { return *reinterpret_cast<const f4v*>(bias_s + (mem * NB + row) * 16 + 4 * g); };
     double ep = 0.0, em = 0.0;
+    float fp = 0.0f, fm = 0.0f;   // the float sums of this lane's terms over the passes since the last double add
     auto pass = [&](TileIn& c, TileIn& n, int j) {
         j = __builtin_amdgcn_readfirstlane(j);
         float tt[RO];
@@ -449,22 +451,24 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
             op = mfma4(Wp.ao[ks], xp[ks], op);
             om = mfma4(Wm.ao[ks], xm[ks], om);
         }
-        // each member's channel terms cw (d d): one multiply and one fused multiply-add each, summed in float over the
-        // tile's outputs in this lane, then into the member's double
+        // each member's channel terms cw (d d) (a multiply, unless every cw is 1, and a fused multiply-add each), summed
+        // in float over this lane's outputs of the tile and over the loop's two passes, then into the member's double
         float tp = 0.0f, tm = 0.0f;
         const f4v cw = *reinterpret_cast<const f4v*>(cw_s + 4 * g);
+        constexpr bool kUnit = UnitCw && NO == 4 * RO;   // (with padding rows their zero weight is still needed)
 #pragma unroll
         for (int r = 0; r < RO; r++) {
             const float dp = out_of<S>(op[r], Clamp) - tt[r], dm = out_of<S>(om[r], Clamp) - tt[r];
-            tp = __builtin_fmaf(__fmul_rn(cw[r], dp), dp, tp);
-            tm = __builtin_fmaf(__fmul_rn(cw[r], dm), dm, tm);
+            tp = __builtin_fmaf(kUnit ? dp : __fmul_rn(cw[r], dp), dp, tp);
+            tm = __builtin_fmaf(kUnit ? dm : __fmul_rn(cw[r], dm), dm, tm);
         }
-        if (s0 + 16 * (wave + kPopWaves * j) + i16 < s1) { ep += (double)tp; em += (double)tm; }
+        if (s0 + 16 * (wave + kPopWaves * j) + i16 < s1) { fp += tp; fm += tm; }
     };
     for (int j = 0; j < mine; j += 2) {
         pass(in0, in1, j);
-        if (j + 1 >= mine) break;
-        pass(in1, in0, j + 1);
+        if (j + 1 < mine) pass(in1, in0, j + 1);
+        ep += (double)fp; em += (double)fm;
+        fp = 0.0f; fm = 0.0f;
     }
     ep = wave_sum(ep);
     em = wave_sum(em);

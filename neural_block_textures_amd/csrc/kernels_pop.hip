@@ -109,10 +109,13 @@ bool pop_pair_possible(const Impl& I) {
 
 template <int From>
 static void launch_pop_pair(Impl& I, const PopSource& src, int N, int M, int chunk, int chunks) {
+    bool unit = true;
+    for (int c = 0; c < I.dm.nout; c++) unit = unit && I.dm.cw[c] == 1.0f;
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         if constexpr (pop_pair_ok<S>()) {
-            auto kern = I.dm.clamp_out ? k_pop_pair<S, true, From> : k_pop_pair<S, false, From>;
+            auto kern = I.dm.clamp_out ? (unit ? k_pop_pair<S, true, From, true> : k_pop_pair<S, true, From, false>)
+                                       : (unit ? k_pop_pair<S, false, From, true> : k_pop_pair<S, false, From, false>);
             launch_timed(kern, I, dim3(N, chunks), dim3(64 * kPopWaves), 0, I.dm, src, M, I.Mcap, chunk, chunks, I.feat, I.btgt,
                          (const float*)I.lay1, I.part);
         }
