@@ -388,7 +388,7 @@ def run_gpu(w, steps, warmup, fd_steps=0, seconds=0.0, settle=0.0):
     loss, _ = tr.mlp_stats()
     img = tr.decode_full()
     assert np.isfinite(img).all() and np.isfinite(loss)
-    name = "k_pop_mfma" if tr.on_matrix_cores("pop_eval") else "k_pop_eval"
+    name = ("k_pop_pair" if tr.on_matrix_cores("pop_pair") else "k_pop_mfma") if tr.on_matrix_cores("pop_eval") else "k_pop_eval"
     out = {"z": z, "p": p, "tgt": tgt, "steps": steps, "el": el, "kernels": kernels, "fd": fd, "loss": loss, "pop_kernel": name,
            "refit": refit, "dct_codes": getattr(tr, "dct_codes", None), "settle": {"seconds": settle, "iterations": settle_iters}}
     if w.dct_q:
@@ -403,7 +403,7 @@ def roofline_of(w, r):
     pop_flop = ev["population"] * 2 * macs(w.layout)
     achieved = pop_flop / (pe["ms_mean"] * 1e-3) / 1e12
     # the VALU kernels (--valu) against the FP32 VALU peak without packed instructions
-    bound, peak = ("mfma", FP32_PEAK_TFLOPS) if r["pop_kernel"] == "k_pop_mfma" else ("valu", VALU_F32_PEAK_TFLOPS)
+    bound, peak = ("mfma", FP32_PEAK_TFLOPS) if r["pop_kernel"] != "k_pop_eval" else ("valu", VALU_F32_PEAK_TFLOPS)
     roof = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4), "traffic": None, "kernel": r["pop_kernel"],
             "flop_per_launch": pop_flop, "ms_per_launch": pe["ms_mean"]}
@@ -413,8 +413,9 @@ def roofline_of(w, r):
     if os.path.exists(tpath) and bound == "mfma":
         with open(tpath) as f:
             t = json.load(f)
-        roof["traffic"] = t.get("pop_eval_bytes_per_launch")
-        roof["traffic_source"] = os.path.relpath(tpath, ROOT)
+        if t.get("pop_eval_kernel", "").startswith(r["pop_kernel"] + "<"):   # counters of the kernel that ran
+            roof["traffic"] = t.get("pop_eval_bytes_per_launch")
+            roof["traffic_source"] = os.path.relpath(tpath, ROOT)
     return roof
 
 

@@ -639,8 +639,9 @@ __device__ __forceinline__ void round_pixel(const DevModel& m, int base, int lan
 }
 
 
-// Sh > 0: the shared first-layer k-steps of lat_shared_ksteps (the launch's mask must be 2: level 1 perturbed only)
-template <class S, int Act, bool Clamp, int Sh = 0>
+// Sh > 0: the shared first-layer k-steps of lat_shared_ksteps (the launch's mask must be 2: level 1 perturbed only).
+// UnitCw: every channel weight is 1, so a pixel's error terms are d d (fused into the sum where a lane holds several)
+template <class S, int Act, bool Clamp, int Sh = 0, bool UnitCw = false>
 __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* __restrict__ w, const float* __restrict__ zdec,
                                                       const float* __restrict__ eps, const float* __restrict__ tgt, float sg,
                                                       unsigned mask, float* __restrict__ dpix, int rounds) {
@@ -751,8 +752,9 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
                 mfma_hidden_from1<S, 2, Act>(W, a1, ak, x);
                 const float dp = out_of<S>(valu_out_g<S>(W, x[0], vo, g, i16), Clamp) - tt[0],
                             dm = out_of<S>(valu_out_g<S>(W, x[1], vo + kVoTile, g, i16), Clamp) - tt[0];
-                ep = __fmul_rn(cw[0], __fmul_rn(dp, dp));
-                em = __fmul_rn(cw[0], __fmul_rn(dm, dm));
+                constexpr bool kUnit = UnitCw && NO == 4;   // (lane groups past nout need their zero weight)
+                ep = kUnit ? __fmul_rn(dp, dp) : __fmul_rn(cw[0], __fmul_rn(dp, dp));
+                em = kUnit ? __fmul_rn(dm, dm) : __fmul_rn(cw[0], __fmul_rn(dm, dm));
             } else {
                 float x[2][Q::kKsH];
                 mfma_hidden_from1<S, 2, Act>(W, a1, ak, x);
@@ -761,8 +763,9 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
 #pragma unroll
                 for (int r = 0; r < out_regs<S>(); r++) {
                     const float dp = out_of<S>(o[0][r], Clamp) - tt[r], dm = out_of<S>(o[1][r], Clamp) - tt[r];
-                    ep = __builtin_fmaf(cw[r], __fmul_rn(dp, dp), ep);
-                    em = __builtin_fmaf(cw[r], __fmul_rn(dm, dm), em);
+                    constexpr bool kUnit = UnitCw && NO == 4 * out_regs<S>();   // (padding rows need their zero weight)
+                    ep = kUnit ? __builtin_fmaf(dp, dp, ep) : __builtin_fmaf(cw[r], __fmul_rn(dp, dp), ep);
+                    em = kUnit ? __builtin_fmaf(dm, dm, em) : __builtin_fmaf(cw[r], __fmul_rn(dm, dm), em);
                 }
             }
             float sp, sm;
@@ -794,7 +797,8 @@ constexpr int qat_occupancy() {
 // activation of act<Act>: the reference adds the float terms in double with its own activation, so a
 // choice can differ from the reference's only between candidates whose losses agree to a few float
 // roundings (the reference's own check accepts such rounding ties, main.cpp:3143-3144).
-template <class S, int Act, bool Clamp>
+// UnitCw: every channel weight is 1, so a candidate's error terms are d d (fused into the sum where a lane holds several)
+template <class S, int Act, bool Clamp, bool UnitCw = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(qat_occupancy<S, Act>()))) k_qat_mfma(DevModel m, const float* __restrict__ w, float* __restrict__ zdec,
                                                  const float* __restrict__ tgt, const int* __restrict__ qat_bits,
                                                  const float* __restrict__ grid) {
@@ -901,7 +905,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(qat_oc
 #pragma unroll
                     for (int v = 0; v < 2; v++) {
                         const float d = out_of<S>(valu_out_g<S>(W, x[v], vo + v * kVoTile, g, i16), Clamp) - tt[0];
-                        lv[v] = __fmul_rn(cw[0], __fmul_rn(d, d));   // cw (d d), main.cpp:2119
+                        constexpr bool kUnit = UnitCw && NO == 4;
+                        lv[v] = kUnit ? __fmul_rn(d, d) : __fmul_rn(cw[0], __fmul_rn(d, d));   // cw (d d), main.cpp:2119
                     }
                 } else {
                     f4v o[2];
@@ -912,7 +917,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(qat_oc
 #pragma unroll
                         for (int r = 0; r < out_regs<S>(); r++) {
                             const float d = out_of<S>(o[v][r], Clamp) - tt[r];
-                            lv[v] = __builtin_fmaf(cw[r], __fmul_rn(d, d), lv[v]);
+                            constexpr bool kUnit = UnitCw && NO == 4 * out_regs<S>();
+                            lv[v] = kUnit ? __builtin_fmaf(d, d, lv[v]) : __builtin_fmaf(cw[r], __fmul_rn(d, d), lv[v]);
                         }
                     }
                 }

@@ -52,8 +52,9 @@ __global__ void __launch_bounds__(kTPB) k_fd_sets(int P, float h, const float* _
 // pairs, one per wave, and the chains are added in a fixed order (waves, then segments), so the sum is
 // deterministic and differs from the single chain only in rounding.
 // Each wave first finishes its chain's pair losses from the population partials (lane q: pair i0 + q,
-// the member's chunk sums added in ascending order, divided by the loss norm): dl_i = l+ - l-, and the
-// blocks of weight tile 0 store dl and the pair means for the statistics.
+// the member's chunk sums added in ascending order, divided by the loss norm; with a single chain the four
+// waves share that work by quarters of the chunks): dl_i = l+ - l-, and the blocks of weight tile 0 store dl
+// and the pair means for the statistics.
 constexpr int kChain = 32;
 // With one segment (N <= 128 pairs) the block's sum is the gradient: the block writes it and takes the
 // weight's Adam step itself (k_es_grad_final's work, the same operations), and no second kernel runs.
@@ -63,11 +64,41 @@ __global__ void __launch_bounds__(kTPB) k_es_grad_part(int N, int P, float scale
                                                       float* __restrict__ grad, float* __restrict__ theta, float* __restrict__ m,
                                                       float* __restrict__ v, float lr, float c1, float c2) {
     __shared__ float lds[kTPB / 64][64];
+    __shared__ double quarters[kTPB / 64][2][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int k = blockIdx.x * 64 + lane;
     const int i0 = (blockIdx.y * (kTPB / 64) + wave) * kChain, i1 = min(N, i0 + kChain);
     float wl = 0.0f;   // lane q: ((float)dl_{i0 + q}) * scale
-    if (i0 + lane < i1) {
+    if (N <= kChain) {
+        // one chain, which wave 0 runs: the four waves add a quarter of each member's chunk sums (lane q: pair q),
+        // all of a quarter's loads in flight before its adds, then wave 0 adds the quarters in order
+        const int c4 = (chunks + 3) >> 2, j0 = min(chunks, wave * c4), j1 = min(chunks, j0 + c4);
+        double lp = 0.0, lm = 0.0;
+        if (lane < N) {
+            const double* pp = lpart + (size_t)(2 * lane) * chunks;
+            const double* pm = pp + chunks;
+            int j = j0;
+            for (; j + 16 <= j1; j += 16) {
+                double a[16], b[16];
+#pragma unroll
+                for (int q = 0; q < 16; q++) { a[q] = pp[j + q]; b[q] = pm[j + q]; }
+#pragma unroll
+                for (int q = 0; q < 16; q++) { lp += a[q]; lm += b[q]; }
+            }
+            for (; j < j1; j++) { lp += pp[j]; lm += pm[j]; }
+        }
+        quarters[wave][0][lane] = lp;
+        quarters[wave][1][lane] = lm;
+        __syncthreads();
+        if (wave == 0 && lane < N) {
+            lp = ((quarters[0][0][lane] + quarters[1][0][lane]) + quarters[2][0][lane]) + quarters[3][0][lane];
+            lm = ((quarters[0][1][lane] + quarters[1][1][lane]) + quarters[2][1][lane]) + quarters[3][1][lane];
+            lp /= norm; lm /= norm;
+            const double d = lp - lm;
+            if (blockIdx.x == 0) { dl[lane] = d; lsum[lane] = 0.5 * (lp + lm); }
+            wl = __fmul_rn((float)d, scale);
+        }
+    } else if (i0 + lane < i1) {
         const int i = i0 + lane;
         // the member's chunk sums in ascending order, loaded 8 at a time (one chain of adds each)
         const double* pp = lpart + (size_t)(2 * i) * chunks;

@@ -6,6 +6,13 @@
 
 namespace ntc_hip {
 
+// every channel weight of the model is 1
+static bool unit_cw(const Impl& I) {
+    bool unit = true;
+    for (int c = 0; c < I.dm.nout; c++) unit = unit && I.dm.cw[c] == 1.0f;
+    return unit;
+}
+
 bool qat_on_matrix_cores(const Impl& I) {
     if (!I.lv0_unit_cells || I.valu_only) return false;
     if (I.jit) return jit_mfma(I);
@@ -109,8 +116,7 @@ bool pop_pair_possible(const Impl& I) {
 
 template <int From>
 static void launch_pop_pair(Impl& I, const PopSource& src, int N, int M, int chunk, int chunks) {
-    bool unit = true;
-    for (int c = 0; c < I.dm.nout; c++) unit = unit && I.dm.cw[c] == 1.0f;
+    const bool unit = unit_cw(I);
     dispatch_shape(I.dm, [&](auto s) {
         using S = decltype(s);
         if constexpr (pop_pair_ok<S>()) {
@@ -153,13 +159,19 @@ static int lat_rounds_for(const Impl& I, int most, int K) {
 
 bool lat_pair_on_matrix_cores(const Impl& I) { return pop_on_matrix_cores(I); }
 
+template <class S, int Act, int Sh>
+static auto lat_kernel(bool clamp, bool unit) {
+    return clamp ? (unit ? k_lat_pair_mfma<S, Act, true, Sh, true> : k_lat_pair_mfma<S, Act, true, Sh, false>)
+                 : (unit ? k_lat_pair_mfma<S, Act, false, Sh, true> : k_lat_pair_mfma<S, Act, false, Sh, false>);
+}
+
 template <class S, int Act>
 static void launch_lat_mfma(Impl& I, int K, float sigma, unsigned mask) {
     // a step that perturbs level 1 only shares the first layer's level-0 and positional k-steps between the members
     constexpr int Sh = lat_shared_ksteps<S>();
-    auto kern = I.dm.clamp_out ? k_lat_pair_mfma<S, Act, true> : k_lat_pair_mfma<S, Act, false>;
+    auto kern = lat_kernel<S, Act, 0>(I.dm.clamp_out, unit_cw(I));
     if constexpr (Sh > 0) {
-        if (mask == 2u) kern = I.dm.clamp_out ? k_lat_pair_mfma<S, Act, true, Sh> : k_lat_pair_mfma<S, Act, false, Sh>;
+        if (mask == 2u) kern = lat_kernel<S, Act, Sh>(I.dm.clamp_out, unit_cw(I));
     }
     static_assert(lat_rounds<S>() >= 1, "a latent pair kernel takes at least one round");
     const int rounds = lat_rounds_for(I, lat_rounds<S>(), K), pix = 256 * rounds;
@@ -206,9 +218,11 @@ void launch_qat_mfma(Impl& I) {
         if constexpr (MfmaShape<S>::kOk)
         {
             const float leak = I.dm.leak;
-            const bool fold = leak >= 0.0f && leak <= 1.0f;
-            auto kern = I.dm.clamp_out ? (fold ? k_qat_mfma<S, kActFold, true> : k_qat_mfma<S, kActAny, true>)
-                                       : (fold ? k_qat_mfma<S, kActFold, false> : k_qat_mfma<S, kActAny, false>);
+            const bool fold = leak >= 0.0f && leak <= 1.0f, unit = unit_cw(I);
+            auto kern = I.dm.clamp_out ? (fold ? (unit ? k_qat_mfma<S, kActFold, true, true> : k_qat_mfma<S, kActFold, true, false>)
+                                               : k_qat_mfma<S, kActAny, true>)
+                                       : (fold ? (unit ? k_qat_mfma<S, kActFold, false, true> : k_qat_mfma<S, kActFold, false, false>)
+                                               : k_qat_mfma<S, kActAny, false>);
             hipLaunchKernelGGL(kern, dim3((unsigned)((I.npix + 255) / 256)), dim3(256), 0, I.stream, I.dm, I.w, I.zdec, I.tgt,
                                I.qat_bits, I.qat_grid);
         }
