@@ -37,7 +37,7 @@ FP32_PEAK_TFLOPS = 157.3
 VALU_F32_PEAK_TFLOPS = 78.6   # one FP32 FMA per lane per cycle (no packed instructions)
 METRIC = "member·pixel evals/sec + ES iterations/sec (512² 4-tex, pop 8192), % roofline"
 KERNELS = ("batch", "perturb", "pop_eval", "es_grad", "adam", "lat_eps", "lat_pair", "lat_gather", "qat_search", "decode",
-           "fd_sets", "qes_snap", "dct_snap", "dct_rate")
+           "fd_sets", "qes_snap", "dct_snap", "dct_rate", "shadow_pull")
 DCT_CODE = 8          # the scale code set before the first device refit replaces it with the probe's
 DCT_LAMBDA = 0.5      # the reference's default --dct-lambda at q 50: min(0.5, 7.5 S(q)^2)
 DCT_LO16 = 4          # the default --dct-lambda-lo 0.25 as round(16 W)
@@ -451,6 +451,17 @@ def all_configs(out_path: str, cpu_seconds: float):
                     f"{row['evals_per_iter']['total']:,} | `{rf['kernel']}` {rf['ms_per_launch']:.4f} ms | {rf['achieved']:.1f} | "
                     f"{100 * rf['frac']:.1f}% | {row['cpu_es_iters_per_s'] or 0:.3g} | {c.get('cores', '-')} | "
                     f"{row['speedup'] or 0:.0f}x | {c.get('sample', '-')} |\n")
+        f.write("\nKernel launches per ES iteration (HIP events around every launch of a further profiled stretch of the same run; "
+                "mean ms per launch x launches per iteration):\n\n| workload | " + " | ".join(KERNELS) + " |\n|---|" + "---|" * len(KERNELS) + "\n")
+        for row in rows:
+            ks = row["kernels"]
+            iters = max(1, ks.get("es_grad", ks.get("batch", {"launches": 1}))["launches"])
+            cells = []
+            for name in KERNELS:
+                k = ks.get(name)
+                cells.append(f"{k['ms_mean']:.4f} x {k['launches'] / iters:g}" if k and name != "pop_eval" else
+                             (f"{k['ms_mean']:.4f} x 1" if k else "-"))
+            f.write(f"| {row['workload']} | " + " | ".join(cells) + " |\n")
         for row in rows:
             rf = row.get("dct_refit")
             if rf:

@@ -281,6 +281,16 @@ __device__ __forceinline__ void adam_at(float* __restrict__ theta, float* __rest
     theta[i] = theta[i] - (lr * mh) / (__builtin_sqrtf(vh) + eps);
 }
 
+// Adam on values already loaded (the same operations as adam_at)
+__device__ __forceinline__ void adam_vals(float& theta, float& m, float& v, float gi, float lr, float c1, float c2) {
+    const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+    const float ob1 = 1.0f - b1, ob2 = 1.0f - b2;
+    m = __builtin_fmaf(b1, m, __fmul_rn(ob1, gi));
+    v = __builtin_fmaf(b2, v, __fmul_rn(__fmul_rn(ob2, gi), gi));
+    const float mh = m / c1, vh = v / c2;
+    theta = theta - (lr * mh) / (__builtin_sqrtf(vh) + eps);
+}
+
 __device__ __forceinline__ float activate(float x, float leak) { return x > 0.0f ? x : leak * x; }   // main.cpp:560
 __device__ __forceinline__ float output_of(float s, int clamp_out) {                                  // main.cpp:624-625
     return clamp_out ? fminf(1.0f, fmaxf(0.0f, s + 0.5f)) : 1.0f / (1.0f + expf(-s));

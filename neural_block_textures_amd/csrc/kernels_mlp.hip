@@ -68,6 +68,17 @@ __global__ void __launch_bounds__(kTPB) k_es_grad_part(int N, int P, float scale
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int k = blockIdx.x * 64 + lane;
     const int i0 = (blockIdx.y * (kTPB / 64) + wave) * kChain, i1 = min(N, i0 + kChain);
+    // the loads that do not wait for the pair losses go first: a full chain's Gaussians, and the Adam state of the
+    // weight this lane updates
+    const bool full = i1 - i0 == kChain && k < P;
+    float e[kChain];
+    if (full) {
+#pragma unroll
+        for (int q = 0; q < kChain; q++) e[q] = eps[(size_t)(i0 + q) * P + k];
+    }
+    const bool adam_here = gridDim.y == 1 && wave == 0 && k < P;
+    float th = 0.0f, mk = 0.0f, vk = 0.0f;
+    if (adam_here) { th = theta[k]; mk = m[k]; vk = v[k]; }
     float wl = 0.0f;   // lane q: ((float)dl_{i0 + q}) * scale
     if (N <= kChain) {
         // one chain, which wave 0 runs: the four waves add a quarter of each member's chunk sums (lane q: pair q),
@@ -120,15 +131,9 @@ __global__ void __launch_bounds__(kTPB) k_es_grad_part(int N, int P, float scale
     }
     float g = 0.0f;
     if (k < P) {
-        if (i1 - i0 == kChain) {   // a full chain: loads issued ahead of the dependent fma chain
-            float w[kChain], e[kChain];
+        if (full) {   // a full chain: its loads were issued ahead of the dependent fma chain
 #pragma unroll
-            for (int q = 0; q < kChain; q++) {
-                w[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), q));
-                e[q] = eps[(size_t)(i0 + q) * P + k];
-            }
-#pragma unroll
-            for (int q = 0; q < kChain; q++) g = __builtin_fmaf(w[q], e[q], g);
+            for (int q = 0; q < kChain; q++) g = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), q)), e[q], g);
         } else {
             for (int i = i0; i < i1; i++)
                 g = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), i - i0)), eps[(size_t)i * P + k], g);
@@ -140,9 +145,10 @@ __global__ void __launch_bounds__(kTPB) k_es_grad_part(int N, int P, float scale
         float s = lds[0][lane];
 #pragma unroll
         for (int q = 1; q < kTPB / 64; q++) s += lds[q][lane];
-        if (gridDim.y == 1) {
+        if (adam_here) {
             grad[k] = s;
-            adam_at(theta, m, v, (size_t)k, s, lr, c1, c2);
+            adam_vals(th, mk, vk, s, lr, c1, c2);
+            theta[k] = th; m[k] = mk; v[k] = vk;
         } else {
             part[(size_t)blockIdx.y * P + k] = s;
         }

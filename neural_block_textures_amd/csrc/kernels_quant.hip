@@ -322,6 +322,7 @@ void launch_dct_rate_pairs(Impl& I, int k0, int K, float sigma) {
     NTC_CHECK(hipGetLastError());
 }
 void launch_shadow_pull(Impl& I, size_t off, size_t n, float f) {
+    ProfScope ps(I, "shadow_pull");
     hipLaunchKernelGGL(k_shadow_pull, dim3(blocks_for(n, kTPB)), dim3(kTPB), 0, I.stream, I.z, I.zq, off, n, f);
     NTC_CHECK(hipGetLastError());
 }
