@@ -639,6 +639,71 @@ __device__ __forceinline__ void round_pixel(const DevModel& m, int base, int lan
 }
 
 
+// One 16-pixel tile of a latent pair: both members' MLPs on the tile's first-layer operands (Sh > 0: the shared
+// k-steps' bs, continued by each member's own bp / bm; Sh = 0: each member's whole first layer bp / bm), each lane's
+// channel terms cw (d d) (its out_regs in ascending order, or its one on the VALU output layer), the pixel's four
+// lane groups added pairwise for each member (group_sums), and (e+ - e-) inv_px written to out[p] by lane group 0.
+template <class S, int Act, bool Clamp, int Sh, bool UnitCw>
+__device__ __forceinline__ void lat_pair_tile(const DevModel& m, const MfmaWeights<S>& W, float ak, const float (&cw)[4],
+                                              const float (&bs)[Sh > 0 ? Sh : 1],
+                                              const float (&bp)[Sh > 0 ? MfmaShape<S>::kKs1 - Sh : MfmaShape<S>::kKs1],
+                                              const float (&bm)[Sh > 0 ? MfmaShape<S>::kKs1 - Sh : MfmaShape<S>::kKs1],
+                                              const float (&tt)[4], float* vo, float* sums, int g, int i16, int p,
+                                              float* __restrict__ out) {
+    using Q = MfmaShape<S>;
+    constexpr int NO = Q::kNout, kM = Q::kKs1 - Sh;
+    constexpr bool kVOut = valu_out<S>();
+    // the first layer's pre-activations of both members (D layout)
+    f4v a1[2][Q::kHt];
+    if constexpr (Sh > 0) {
+        f4v as[Q::kHt];
+#pragma unroll
+        for (int ot = 0; ot < Q::kHt; ot++) as[ot] = W.c1[ot];
+#pragma unroll
+        for (int ks = 0; ks < Sh; ks++)
+#pragma unroll
+            for (int ot = 0; ot < Q::kHt; ot++) as[ot] = mfma4(W.a1[ot][ks], bs[ks], as[ot]);
+#pragma unroll
+        for (int ot = 0; ot < Q::kHt; ot++) { a1[0][ot] = as[ot]; a1[1][ot] = as[ot]; }
+#pragma unroll
+        for (int ks = 0; ks < kM; ks++)
+#pragma unroll
+            for (int v = 0; v < 2; v++)
+#pragma unroll
+                for (int ot = 0; ot < Q::kHt; ot++) a1[v][ot] = mfma4(W.a1[ot][Sh + ks], v ? bm[ks] : bp[ks], a1[v][ot]);
+    } else {
+        float b1[2][Q::kKs1];
+#pragma unroll
+        for (int ks = 0; ks < Q::kKs1; ks++) { b1[0][ks] = bp[ks]; b1[1][ks] = bm[ks]; }
+        mfma_layer1<S, 2>(W, b1, a1);
+    }
+    float ep = 0.0f, em = 0.0f;
+    if constexpr (kVOut) {
+        float x[2][Q::kKsH];
+        mfma_hidden_from1<S, 2, Act>(W, a1, ak, x);
+        const float dp = out_of<S>(valu_out_g<S>(W, x[0], vo, g, i16), Clamp) - tt[0],
+                    dm = out_of<S>(valu_out_g<S>(W, x[1], vo + kVoTile, g, i16), Clamp) - tt[0];
+        constexpr bool kUnit = UnitCw && NO == 4;   // (lane groups past nout need their zero weight)
+        ep = kUnit ? __fmul_rn(dp, dp) : __fmul_rn(cw[0], __fmul_rn(dp, dp));
+        em = kUnit ? __fmul_rn(dm, dm) : __fmul_rn(cw[0], __fmul_rn(dm, dm));
+    } else {
+        float x[2][Q::kKsH];
+        mfma_hidden_from1<S, 2, Act>(W, a1, ak, x);
+        f4v o[2];
+        mfma_output<S, 2>(W, x, o);
+#pragma unroll
+        for (int r = 0; r < out_regs<S>(); r++) {
+            const float dp = out_of<S>(o[0][r], Clamp) - tt[r], dm = out_of<S>(o[1][r], Clamp) - tt[r];
+            constexpr bool kUnit = UnitCw && NO == 4 * out_regs<S>();   // (padding rows need their zero weight)
+            ep = kUnit ? __builtin_fmaf(dp, dp, ep) : __builtin_fmaf(cw[r], __fmul_rn(dp, dp), ep);
+            em = kUnit ? __builtin_fmaf(dm, dm, em) : __builtin_fmaf(cw[r], __fmul_rn(dm, dm), em);
+        }
+    }
+    float sp, sm;
+    group_sums(ep, em, sums, g, i16, sp, sm);
+    if (g == 0 && p < m.npix) out[p] = __fmul_rn(sp - sm, m.inv_px);
+}
+
 // Sh > 0: the shared first-layer k-steps of lat_shared_ksteps (the launch's mask must be 2: level 1 perturbed only).
 // UnitCw: every channel weight is 1, so a pixel's error terms are d d (fused into the sum where a lane holds several)
 template <class S, int Act, bool Clamp, int Sh = 0, bool UnitCw = false>
@@ -720,57 +785,7 @@ __global__ void __launch_bounds__(256) k_lat_pair_mfma(DevModel m, const float* 
             for (int r = 0; r < 4; r++) tt[r] = tn[r];
             if (t + 1 < 4) load_t(base + 16 * (t + 1), tn);
             const int p = base + 16 * t + i16;
-            // the first layer's pre-activations of both members (D layout)
-            f4v a1[2][Q::kHt];
-            if constexpr (Sh > 0) {
-                f4v as[Q::kHt];
-#pragma unroll
-                for (int ot = 0; ot < Q::kHt; ot++) as[ot] = W.c1[ot];
-#pragma unroll
-                for (int ks = 0; ks < Sh; ks++)
-#pragma unroll
-                    for (int ot = 0; ot < Q::kHt; ot++) as[ot] = mfma4(W.a1[ot][ks], bs[t][ks], as[ot]);
-#pragma unroll
-                for (int ot = 0; ot < Q::kHt; ot++) { a1[0][ot] = as[ot]; a1[1][ot] = as[ot]; }
-#pragma unroll
-                for (int ks = 0; ks < kM; ks++)
-#pragma unroll
-                    for (int v = 0; v < 2; v++)
-#pragma unroll
-                        for (int ot = 0; ot < Q::kHt; ot++) a1[v][ot] = mfma4(W.a1[ot][Sh + ks], v ? bm[t][ks] : bp[t][ks], a1[v][ot]);
-            } else {
-                float b1[2][Q::kKs1];
-#pragma unroll
-                for (int ks = 0; ks < Q::kKs1; ks++) { b1[0][ks] = bp[t][ks]; b1[1][ks] = bm[t][ks]; }
-                mfma_layer1<S, 2>(W, b1, a1);
-            }
-            // each lane's channel terms cw (d d) (its out_regs in ascending order, or its one on the VALU output
-            // layer), then the pixel's four lane groups added pairwise for each member (group_sums), then e+ - e-
-            float ep = 0.0f, em = 0.0f;
-            if constexpr (kVOut) {
-                float x[2][Q::kKsH];
-                mfma_hidden_from1<S, 2, Act>(W, a1, ak, x);
-                const float dp = out_of<S>(valu_out_g<S>(W, x[0], vo, g, i16), Clamp) - tt[0],
-                            dm = out_of<S>(valu_out_g<S>(W, x[1], vo + kVoTile, g, i16), Clamp) - tt[0];
-                constexpr bool kUnit = UnitCw && NO == 4;   // (lane groups past nout need their zero weight)
-                ep = kUnit ? __fmul_rn(dp, dp) : __fmul_rn(cw[0], __fmul_rn(dp, dp));
-                em = kUnit ? __fmul_rn(dm, dm) : __fmul_rn(cw[0], __fmul_rn(dm, dm));
-            } else {
-                float x[2][Q::kKsH];
-                mfma_hidden_from1<S, 2, Act>(W, a1, ak, x);
-                f4v o[2];
-                mfma_output<S, 2>(W, x, o);
-#pragma unroll
-                for (int r = 0; r < out_regs<S>(); r++) {
-                    const float dp = out_of<S>(o[0][r], Clamp) - tt[r], dm = out_of<S>(o[1][r], Clamp) - tt[r];
-                    constexpr bool kUnit = UnitCw && NO == 4 * out_regs<S>();   // (padding rows need their zero weight)
-                    ep = kUnit ? __builtin_fmaf(dp, dp, ep) : __builtin_fmaf(cw[r], __fmul_rn(dp, dp), ep);
-                    em = kUnit ? __builtin_fmaf(dm, dm, em) : __builtin_fmaf(cw[r], __fmul_rn(dm, dm), em);
-                }
-            }
-            float sp, sm;
-            group_sums(ep, em, sums, g, i16, sp, sm);
-            if (g == 0 && p < m.npix) out[p] = __fmul_rn(sp - sm, m.inv_px);
+            lat_pair_tile<S, Act, Clamp, Sh, UnitCw>(m, W, ak, cw, bs[t], bp[t], bm[t], tt, vo, sums, g, i16, p, out);
         }
     }
 }
