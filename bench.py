@@ -443,13 +443,13 @@ def all_configs(out_path: str, cpu_seconds: float):
         f.write("# ES iterations per second, all five workloads (one MI355X vs the reference's CPU loop)\n\n")
         f.write("Command (from the repository root on the MI355X box):\n\n```\n" + " ".join(["python3"] + sys.argv) + "\n```\n\n")
         f.write("| workload | GPU ES it/s | GPU ms/iter | member-pixel evals/iter | population kernel | TFLOP/s | % of 157.3 "
-                "| CPU ES it/s | CPU threads | speedup | CPU sample |\n|---|---|---|---|---|---|---|---|---|---|---|\n")
+                "| CPU ES it/s | CPU threads, ISA | speedup | CPU sample |\n|---|---|---|---|---|---|---|---|---|---|---|\n")
         for row in rows:
             c = row["cpu"] or {}
             rf = row["roofline"]
             f.write(f"| {row['workload']} | {row['gpu_es_iters_per_s']:.2f} | {row['gpu_ms_per_iter']:.3f} | "
                     f"{row['evals_per_iter']['total']:,} | `{rf['kernel']}` {rf['ms_per_launch']:.4f} ms | {rf['achieved']:.1f} | "
-                    f"{100 * rf['frac']:.1f}% | {row['cpu_es_iters_per_s'] or 0:.3g} | {c.get('cores', '-')} | "
+                    f"{100 * rf['frac']:.1f}% | {row['cpu_es_iters_per_s'] or 0:.3g} | {c.get('cores', '-')}, {c.get('isa') or c.get('kind', '-')} | "
                     f"{row['speedup'] or 0:.0f}x | {c.get('sample', '-')} |\n")
         f.write("\nKernel launches per ES iteration (HIP events around every launch of a further profiled stretch of the same run; "
                 "mean ms per launch x launches per iteration):\n\n| workload | " + " | ".join(KERNELS) + " |\n|---|" + "---|" * len(KERNELS) + "\n")
@@ -462,6 +462,12 @@ def all_configs(out_path: str, cpu_seconds: float):
                 cells.append(f"{k['ms_mean']:.4f} x {k['launches'] / iters:g}" if k and name != "pop_eval" else
                              (f"{k['ms_mean']:.4f} x 1" if k else "-"))
             f.write(f"| {row['workload']} | " + " | ".join(cells) + " |\n")
+        c = next((row["cpu"] for row in rows if row["cpu"]), None)
+        if c:
+            ids = c.get("cpuid") or {}
+            f.write(f"\nCPU baseline host: {c.get('cpu')} (cpuinfo family {ids.get('cpu_family', '?')}, model {ids.get('model', '?')}), "
+                    f"{c.get('nproc')} logical CPUs, {c.get('affinity_cpus')} in the affinity set; the reference's loop "
+                    f"{c.get('build', '(the oracle restatement)')}, the widest build the host supports.\n")
         for row in rows:
             rf = row.get("dct_refit")
             if rf:
