@@ -285,8 +285,11 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     }
 }
 
-// ---- The ES population with the pair's first layer shared (models with more than 4 outputs and at most two
-// 16-unit hidden tiles, whose minibatch's first-layer pre-activations stay in the L2). The two members of a pair differ
+// ---- The ES population with the pair's first layer shared (models with one or two 16-unit hidden tiles, except the
+// pixel-per-lane shapes; the launch takes it where a chunk's first-layer pre-activations stay in the L2). More than 4
+// outputs: the output tile on the matrix cores, its rows packed (out_at); at most 4: valu_out_g's sums and
+// reduce-scatter on the VALU, both members' output weights read from an LDS table (in registers they would cost a
+// wave per SIMD). The two members of a pair differ
 // in every weight by +-sigma eps, so their first layers are h+- = u +- d with u the unperturbed layer's pre-activations
 // (bias + w x, the same for every pair; the minibatch launch computes it once per step, lay1[unit][slot]) and d the
 // perturbation's: h- = 2 u - h+, one fused multiply-add per value instead of the - member's first-layer matrix
@@ -299,7 +302,9 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
 template <class S, bool = MfmaShape<S>::kOk>
 struct PopPairOk { static constexpr bool value = false; };
 template <class S>
-struct PopPairOk<S, true> { static constexpr bool value = !valu_out<S>() && MfmaShape<S>::kHt <= 2 && MfmaShape<S>::kH % 16 == 0; };
+struct PopPairOk<S, true> {
+    static constexpr bool value = MfmaShape<S>::kHt <= 2 && MfmaShape<S>::kH % 16 == 0 && !pop_own<S>();
+};
 template <class S>
 constexpr bool pop_pair_ok() { return PopPairOk<S>::value; }
 // bias rows per member: the first layer's kHt tiles, each deeper hidden layer's kHt, the output tile
@@ -311,7 +316,7 @@ constexpr int pair_p_pad() { return (MfmaShape<S>::kP + 3) & ~3; }
 
 // UnitCw: every channel weight is 1 (a single texture, or equally weighted ones), so cw (d d) is d d without a multiply
 template <class S, bool Clamp, int From, bool UnitCw>
-__global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_per_eu(4))) k_pop_pair(DevModel m, PopSource src, int M, int Mcap,
+__global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_per_eu(pop_occupancy<S>()))) k_pop_pair(DevModel m, PopSource src, int M, int Mcap,
                                                             int chunk, int chunks, const float* __restrict__ feat,
                                                             const float* __restrict__ btgt, const float* __restrict__ lay1,
                                                             double* __restrict__ part) {
@@ -323,6 +328,12 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     __shared__ __attribute__((aligned(16))) float wpm_s[2 * PP];          // the + member's parameters, then the - member's
     __shared__ __attribute__((aligned(16))) float bias_s[2 * NB * 16];    // [member][row][4 g + r]
     __shared__ __attribute__((aligned(16))) float cw_s[16];               // the channel weight of register r of group g
+    // at most 4 outputs: the output layer on the VALU (valu_out_g's sums and reduce-scatter), its weights from LDS:
+    // [member][lane group][bias, then k-step 0 .. kKsH - 1][output 0 .. 3], and each wave's two reduce-scatter tiles
+    constexpr bool kVOut = valu_out<S>();
+    constexpr int kWo = kVOut ? 2 * 4 * (Q::kKsH + 1) * 4 : 4;
+    __shared__ __attribute__((aligned(16))) float wo_s[kWo];
+    __shared__ __attribute__((aligned(16))) float vo_s[kVOut ? kPopWaves * 2 * kVoTile : 4];
     const int lane = tid_x() & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
     const int pair = bid_x(), ch = bid_y();
@@ -395,11 +406,42 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
         }
     }
     __syncthreads();
+    if constexpr (kVOut) {   // the output layer's table from the staged (scaled) parameters
+        for (int i = tid_x(); i < kWo; i += 64 * kPopWaves) {
+            const int c = i & 3, ks = (i >> 2) % (Q::kKsH + 1) - 1, gg = (i >> 2) / (Q::kKsH + 1) % 4, mem = i / (4 * (Q::kKsH + 1) * 4);
+            const float* wm = wpm_s + mem * PP + kPout;
+            float v = 0.0f;
+            if (c < NO) {
+                if (ks < 0) v = gg == 0 ? wm[NO * H + c] : 0.0f;   // the bias, in lane group 0 (valu_out_g's W.bo)
+                else if (hidden_input<Q>(ks, gg) < H) v = wm[c * H + hidden_input<Q>(ks, gg)];
+            }
+            wo_s[i] = v;
+        }
+        __syncthreads();
+    }
     MfmaWeights<S> Wp, Wm;   // the A operands of both members (their bias fields unused)
     mfma_load<S>(Wp, wpm_s, lane);
     mfma_load<S>(Wm, wpm_s + PP, lane);
     const float ak = act_k_of<kActFold>(m);
     auto bias = [&](int mem, int row) { return *reinterpret_cast<const f4v*>(bias_s + (mem * NB + row) * 16 + 4 * g); };
+    // valu_out_g of member mem with its weights from wo_s: output g of pixel i16 in lane (g, i16), zero past nout
+    auto vout = [&](int mem, const float (&x)[Q::kKsH]) {
+        const float* wg = wo_s + (mem * 4 + g) * (Q::kKsH + 1) * 4;
+        float* t = vo_s + (wave * 2 + mem) * kVoTile;
+        f4v p = *reinterpret_cast<const f4v*>(wg);
+#pragma unroll
+        for (int ks = 0; ks < Q::kKsH; ks++) {
+            const f4v wv = *reinterpret_cast<const f4v*>(wg + 4 * (ks + 1));
+#pragma unroll
+            for (int c = 0; c < NO; c++) p[c] = __builtin_fmaf(wv[c], x[ks], p[c]);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) t[i16 * kOwnRow + 4 * c + g] = p[c];
+        wave_lds_fence();
+        const f4v v = *reinterpret_cast<const f4v*>(t + i16 * kOwnRow + 4 * g);
+        wave_lds_fence();
+        return (v[0] + v[2]) + (v[1] + v[3]);
+    };
     double ep = 0.0, em = 0.0;
     float fp = 0.0f, fm = 0.0f;   // the float sums of this lane's terms over the passes since the last double add
     auto pass = [&](TileIn& c, TileIn& n, int j) {
@@ -445,11 +487,18 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
 #pragma unroll
                 for (int r = 0; r < 4; r++) { xp[4 * ot + r] = act<kActFold>(ap[ot][r], ak); xm[4 * ot + r] = act<kActFold>(am[ot][r], ak); }
         }
-        f4v op = bias(0, NB - 1), om = bias(1, NB - 1);
+        f4v op, om;
+        if constexpr (kVOut) {
+            op[0] = vout(0, xp);
+            om[0] = vout(1, xm);
+        } else {
+            op = bias(0, NB - 1);
+            om = bias(1, NB - 1);
 #pragma unroll
-        for (int ks = 0; ks < Q::kKsH; ks++) {
-            op = mfma4(Wp.ao[ks], xp[ks], op);
-            om = mfma4(Wm.ao[ks], xm[ks], om);
+            for (int ks = 0; ks < Q::kKsH; ks++) {
+                op = mfma4(Wp.ao[ks], xp[ks], op);
+                om = mfma4(Wm.ao[ks], xm[ks], om);
+            }
         }
         // each member's channel terms cw (d d) (a multiply, unless every cw is 1, and a fused multiply-add each), summed
         // in float over this lane's outputs of the tile and over the loop's two passes, then into the member's double

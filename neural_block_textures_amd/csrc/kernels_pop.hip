@@ -100,18 +100,21 @@ void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks) {
     launch_pop_matrix<kSets>(I, src, pairs, M, chunk, chunks);
 }
 
-// The pair-sharing population kernel (k_pop_pair) takes an ES step of a fixed shape it supports whose minibatch's
-// first layer stays in the L2 (H x Mcap floats within 2 MiB); NTC_HIP_POP_PAIR=0 keeps k_pop_mfma for every step.
+// The pair-sharing population kernel (k_pop_pair) takes the ES steps of the fixed shapes it supports
+// (pop_pair_possible: the trainer then keeps a first-layer array of H x Mcap floats) whose chunks' first layers stay
+// in the L2 (pop_pair_step: H x chunk floats within 2 MiB of an XCD's 4 MiB; the blocks of one chunk run together,
+// so an XCD's working set is about one chunk's minibatch). NTC_HIP_POP_PAIR=0 keeps k_pop_mfma for every step.
 bool pop_pair_possible(const Impl& I) {
     if (I.jit || I.valu_only || !(I.dm.leak >= 0.0f && I.dm.leak <= 1.0f)) return false;
     const char* env = getenv("NTC_HIP_POP_PAIR");
     if (env && env[0] == '0') return false;
     bool ok = false;
-    dispatch_shape(I.dm, [&](auto s) {
-        using S = decltype(s);
-        if constexpr (pop_pair_ok<S>()) ok = (size_t)MfmaShape<S>::kH * (size_t)I.Mcap * sizeof(float) <= ((size_t)2 << 20);
-    });
+    dispatch_shape(I.dm, [&](auto s) { ok = pop_pair_ok<decltype(s)>(); });
     return ok;
+}
+
+bool pop_pair_step(const Impl& I, int chunk) {
+    return I.pop_pair && pop_on_matrix_cores(I) && (size_t)I.d.hidden[0] * (size_t)chunk * sizeof(float) <= ((size_t)2 << 20);
 }
 
 template <int From>
@@ -135,7 +138,7 @@ void launch_pop_eval_es(Impl& I, int it, float sigma, int N, int M, int chunk, i
     src.nt = I.noise; src.seed = I.d.seed; src.step = (uint32_t)it; src.sigma = sigma;
     src.w0 = I.w; src.eps = I.eps_mlp;
     ProfScope ps(I, "pop_eval", true);
-    if (I.pop_pair && pop_on_matrix_cores(I)) {   // the step's minibatch launch wrote the first layer
+    if (pop_pair_step(I, chunk)) {   // the step's minibatch launch wrote the first layer
         if (pop_reads_eps(chunks)) launch_pop_pair<kReadEps>(I, src, N, M, chunk, chunks);
         else launch_pop_pair<kDraw>(I, src, N, M, chunk, chunks);
         return;

@@ -517,7 +517,7 @@ void Trainer::mlp_step(int it, float sigma, float lr, int N, int M) {
     const int chunk = pop_chunk(I, N, M), chunks = (M + chunk - 1) / chunk;
     const bool mfma = pop_on_matrix_cores(I);
     // with the Gaussians the population kernel reads, and the first layer the pair-sharing kernel reads
-    launch_batch(I, it, M, mfma && pop_reads_eps(chunks) ? N : 0, mfma && I.pop_pair);
+    launch_batch(I, it, M, mfma && pop_reads_eps(chunks) ? N : 0, pop_pair_step(I, chunk));
     ensure_part(I, (size_t)2 * N * chunks);
     if (mfma) {
         launch_pop_eval_es(I, it, sigma, N, M, chunk, chunks);   // stages the perturbed weights itself

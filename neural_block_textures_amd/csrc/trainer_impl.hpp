@@ -86,7 +86,7 @@ struct ntc_cuda::Trainer::Impl {
     int* bidx = nullptr;
     int Mcap = 0;
     // the minibatch's unperturbed first-layer pre-activations (H x Mcap + slack), for the population kernel that
-    // shares them between a pair's members (k_pop_pair; pop_pair: the model's shape and minibatch take it)
+    // shares them between a pair's members (k_pop_pair; pop_pair: the model's shape takes it)
     float* lay1 = nullptr;
     bool pop_pair = false;
     float* wsets = nullptr;
@@ -213,8 +213,10 @@ std::vector<uint32_t> noise_fix_summary(const std::vector<uint32_t>& fix);
 void launch_fill(Impl& I, float* p, size_t n, float v);
 // the minibatch of step it; eps_pairs > 0: the same launch draws the step's Gaussians of that many pairs (EpsJob)
 void launch_batch(Impl& I, int it, int M, int eps_pairs = 0, bool lay1 = false);
-// whether ES steps of this model take the pair-sharing population kernel (k_pop_pair) with minibatches of Mcap slots
+// whether this model's shape takes the pair-sharing population kernel (k_pop_pair; the trainer then keeps the
+// minibatch's first layer, lay1), and whether an ES step with chunks of `chunk` slots does
 bool pop_pair_possible(const Impl& I);
+bool pop_pair_step(const Impl& I, int chunk);
 void launch_perturb(Impl& I, int it, float sigma, int N);
 // the Gaussians of one ES step (NS_MLP, it, pair, k) into eps_mlp, N x P
 void launch_fd_sets(Impl& I, float h);

@@ -83,7 +83,8 @@ def test_mlp_es_step(orc, name):
     assert abs(loss - 0.5 * (lp + lm).mean()) < 1e-12 and dstd > 0
 
 
-@pytest.mark.parametrize("name", ["rgb_16x2", "material", "dct_17", "chief1_36", "runtime", "jit_widths", "material_valu"])
+@pytest.mark.parametrize("name", ["rgb_16x2", "material", "dct_plane", "two_level", "dct_17", "chief1_36", "runtime", "jit_widths",
+                                  "material_valu"])
 def test_mlp_es_small_batches(orc, name):
     """minibatches of less than one 16-slot tile, one slot past a tile and a few tiles, and one or a few pairs, on
     one trainer in a row (each call sizes its own chunks): member losses to the bar, the update one chain exactly, and
@@ -245,6 +246,19 @@ def test_matrix_core_choice(orc, name, mfma):
     tr = trainer(lay, z, p, tgt)
     assert tr.on_matrix_cores("pop_eval") == mfma
     assert tr.on_matrix_cores("lat_pair") == mfma
+
+
+@pytest.mark.parametrize("name,pair", [("material", True), ("dct_plane", True), ("two_level", True), ("rgb_16x2", False),
+                                       ("large", False), ("dct_17", False), ("material_valu", False)])
+def test_pair_population_kernel_choice(orc, name, pair):
+    """ES steps share a pair's first layer (k_pop_pair) on the fixed shapes with one or two 16-unit hidden tiles: the
+    12-output material and the 3-output 32-wide ones; not the pixel-per-lane 16-wide shape, the 64-wide one, a 17-wide
+    one or the VALU kernels"""
+    lay = LAYOUTS[name]
+    z, p, tgt = data(lay, 8)
+    tr = trainer(lay, z, p, tgt)
+    assert tr.on_matrix_cores("pop_pair") == pair
+    tr.close()
 
 
 @pytest.mark.parametrize("name", ["jit_valu_7", "jit_mfma_28", "jit_widths", "runtime"])
