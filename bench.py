@@ -388,7 +388,9 @@ def run_gpu(w, steps, warmup, fd_steps=0, seconds=0.0, settle=0.0):
     loss, _ = tr.mlp_stats()
     img = tr.decode_full()
     assert np.isfinite(img).all() and np.isfinite(loss)
-    name = ("k_pop_pair" if tr.on_matrix_cores("pop_pair") else "k_pop_mfma") if tr.on_matrix_cores("pop_eval") else "k_pop_eval"
+    name = "k_pop_eval"
+    if tr.on_matrix_cores("pop_eval"):
+        name = ("k_pop_pair_own" if tr.on_matrix_cores("pop_pair_own") else "k_pop_pair") if tr.on_matrix_cores("pop_pair") else "k_pop_mfma"
     out = {"z": z, "p": p, "tgt": tgt, "steps": steps, "el": el, "kernels": kernels, "fd": fd, "loss": loss, "pop_kernel": name,
            "refit": refit, "dct_codes": getattr(tr, "dct_codes", None), "settle": {"seconds": settle, "iterations": settle_iters}}
     if w.dct_q:

@@ -193,7 +193,8 @@ void ntc_trainer_set_profiling_every(ntc_trainer* t, int n);
 int ntc_trainer_kernel_time(ntc_trainer* t, const char* name, double* total_ms, long long* launches);
 // 1 if the stage ("pop_eval": the ES and central-difference populations, "lat_pair", "qat_search") runs on
 // the FP32 matrix cores for this model, else 0; "pop_pair": 1 if its ES steps with the pairs and minibatch sized at
-// init take the population kernel that shares a pair's first layer (k_pop_pair)
+// init take a population kernel that shares a pair's first layer (k_pop_pair, or k_pop_pair_own for the pixel-per-lane
+// shapes); "pop_pair_own": 1 if that kernel is k_pop_pair_own
 int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage);
 /* on = 0: every stage of this trainer runs on the VALU kernels from the next call on (the matrix-core
  * kernels' parity and speed are then measured against them); on = 1 (the default): the matrix cores

@@ -194,7 +194,10 @@ int ntc_trainer_on_matrix_cores(ntc_trainer* t, const char* stage) {
     if (s == "pop_eval") return ntc_hip::pop_on_matrix_cores(I) ? 1 : 0;
     if (s == "lat_pair") return ntc_hip::lat_pair_on_matrix_cores(I) ? 1 : 0;
     if (s == "qat_search") return ntc_hip::qat_on_matrix_cores(I) ? 1 : 0;
-    if (s == "pop_pair") return ntc_hip::pop_pair_step(I, ntc_hip::pop_chunk(I, I.pairs_cap, I.Mcap)) ? 1 : 0;
+    if (s == "pop_pair" || s == "pop_pair_own") {
+        const bool pair = ntc_hip::pop_pair_step(I, ntc_hip::pop_chunk(I, I.pairs_cap, I.Mcap));
+        return (pair && (s == "pop_pair" || ntc_hip::pop_pair_own_shape(I))) ? 1 : 0;
+    }
     return 0;
 }
 

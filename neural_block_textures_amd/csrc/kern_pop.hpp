@@ -315,6 +315,52 @@ template <class S>
 constexpr int pair_p_pad() { return (MfmaShape<S>::kP + 3) & ~3; }
 
 // UnitCw: every channel weight is 1 (a single texture, or equally weighted ones), so cw (d d) is d d without a multiply
+// Stages both members of an ES pair in LDS: wpm_s = w0 + sigma eps, then (PP floats on) w0 - sigma eps (main.cpp:1852-1856),
+// scaled as k_pop_mfma scales its registers (the hidden layers by the folded activation's (1 + leak) / 2, the output
+// layer by -log2 e for the hardware sigmoid); the biases also to their operand rows bias_s [member][row][4 g + r]
+// (the output tile's padding rows zero), and cw_s[4 g + r] = the channel weight of output register r of lane group g.
+// The Gaussians are drawn here (kDraw: the chunk-0 block writes them for the update) or read (kReadEps).
+template <class S, bool Clamp, int From>
+__device__ __forceinline__ void pair_stage(const DevModel& m, const PopSource& src, int pair, int ch, float* __restrict__ wpm_s,
+                                           float* __restrict__ bias_s, float* __restrict__ cw_s) {
+    using Q = MfmaShape<S>;
+    constexpr int H = Q::kH, NIN = Q::kIn, NO = Q::kNout, RO = out_regs<S>(), NB = pair_bias_rows<S>(), PP = pair_p_pad<S>();
+    constexpr int kPout = H * NIN + H + (Q::kNL - 1) * (H * H + H);   // the first output-layer parameter
+    const uint64_t head = noise_head(src.seed, NS_MLP, src.step, (uint32_t)pair);
+    float* eg = src.eps + (size_t)pair * Q::kP;
+    const float fb = fold_scale(m.leak);
+    if (tid_x() < 16) {   // the output tile's padding rows; the channel weights (zero on padding)
+        const int gg = tid_x() >> 2, r = tid_x() & 3, c = out_at<S>(gg, r);
+        if (c < 0) { bias_s[(NB - 1) * 16 + tid_x()] = 0.0f; bias_s[(2 * NB - 1) * 16 + tid_x()] = 0.0f; }
+        cw_s[tid_x()] = c < 0 ? 0.0f : m.cw[c];
+    }
+    for (int k = tid_x(); k < Q::kP; k += 64 * kPopWaves) {
+        float e;
+        if constexpr (From == kDraw) {
+            e = gauss_at(src.nt, head, (uint64_t)k);
+            if (ch == 0) eg[k] = e;
+        } else {
+            e = eg[k];
+        }
+        const float w0 = src.w0[k];
+        const float sc = k < kPout ? fb : (Clamp ? 1.0f : kNegLog2e);
+        const float vp = __builtin_fmaf(src.sigma, e, w0) * sc, vm = __builtin_fmaf(-src.sigma, e, w0) * sc;
+        wpm_s[k] = vp;
+        wpm_s[PP + k] = vm;
+        int row = -1, col = 0;   // a bias: its operand row and column
+        if (k >= H * NIN && k < H * NIN + H) {
+            row = (k - H * NIN) >> 4; col = (k - H * NIN) & 15;
+        } else if (k >= H * NIN + H && k < kPout) {
+            const int q = k - (H * NIN + H), l = q / (H * H + H), o = q - l * (H * H + H) - H * H;
+            if (o >= 0) { row = Q::kHt * (1 + l) + (o >> 4); col = o & 15; }
+        } else if (k >= kPout + NO * H) {
+            const int c = k - (kPout + NO * H);
+            row = NB - 1; col = 4 * (c / RO) + c % RO;   // output c sits in register c % RO of lane group c / RO
+        }
+        if (row >= 0) { bias_s[row * 16 + col] = vp; bias_s[(NB + row) * 16 + col] = vm; }
+    }
+}
+
 template <class S, bool Clamp, int From, bool UnitCw>
 __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_per_eu(pop_occupancy<S>()))) k_pop_pair(DevModel m, PopSource src, int M, int Mcap,
                                                             int chunk, int chunks, const float* __restrict__ feat,
@@ -367,44 +413,7 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     };
     TileIn in0, in1;
     load(in0, 0);
-    // stage both members: w0 +- sigma eps, scaled as k_pop_mfma scales its registers (the hidden layers by the folded
-    // activation's (1 + leak) / 2, the output layer by -log2 e for the hardware sigmoid); the biases also to their
-    // operand rows
-    {
-        const uint64_t head = noise_head(src.seed, NS_MLP, src.step, (uint32_t)pair);
-        float* eg = src.eps + (size_t)pair * Q::kP;
-        const float fb = fold_scale(m.leak);
-        if (tid_x() < 16) {   // the output tile's padding rows; the channel weights (zero on padding)
-            const int gg = tid_x() >> 2, r = tid_x() & 3, c = out_at<S>(gg, r);
-            if (c < 0) { bias_s[(NB - 1) * 16 + tid_x()] = 0.0f; bias_s[(2 * NB - 1) * 16 + tid_x()] = 0.0f; }
-            cw_s[tid_x()] = c < 0 ? 0.0f : m.cw[c];
-        }
-        for (int k = tid_x(); k < Q::kP; k += 64 * kPopWaves) {
-            float e;
-            if constexpr (From == kDraw) {
-                e = gauss_at(src.nt, head, (uint64_t)k);
-                if (ch == 0) eg[k] = e;
-            } else {
-                e = eg[k];
-            }
-            const float w0 = src.w0[k];
-            const float sc = k < kPout ? fb : (Clamp ? 1.0f : kNegLog2e);
-            const float vp = __builtin_fmaf(src.sigma, e, w0) * sc, vm = __builtin_fmaf(-src.sigma, e, w0) * sc;
-            wpm_s[k] = vp;
-            wpm_s[PP + k] = vm;
-            int row = -1, col = 0;   // a bias: its operand row and column
-            if (k >= H * NIN && k < H * NIN + H) {
-                row = (k - H * NIN) >> 4; col = (k - H * NIN) & 15;
-            } else if (k >= H * NIN + H && k < kPout) {
-                const int q = k - (H * NIN + H), l = q / (H * H + H), o = q - l * (H * H + H) - H * H;
-                if (o >= 0) { row = Q::kHt * (1 + l) + (o >> 4); col = o & 15; }
-            } else if (k >= kPout + NO * H) {
-                const int c = k - (kPout + NO * H);
-                row = NB - 1; col = 4 * (c / RO) + c % RO;   // output c sits in register c % RO of lane group c / RO
-            }
-            if (row >= 0) { bias_s[row * 16 + col] = vp; bias_s[(NB + row) * 16 + col] = vm; }
-        }
-    }
+    pair_stage<S, Clamp, From>(m, src, pair, ch, wpm_s, bias_s, cw_s);
     __syncthreads();
     if constexpr (kVOut) {   // the output layer's table from the staged (scaled) parameters
         for (int i = tid_x(); i < kWo; i += 64 * kPopWaves) {
@@ -521,6 +530,133 @@ __global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_pe
     }
     ep = wave_sum(ep);
     em = wave_sum(em);
+    if (lane == 0) { red[0][wave] = ep; red[1][wave] = em; }
+    __syncthreads();
+    if (tid_x() == 0) {
+        part[(size_t)(2 * pair) * chunks + ch] = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+        part[(size_t)(2 * pair + 1) * chunks + ch] = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    }
+}
+
+// ---- The pair population kernel of the pixel-per-lane shapes (at most 4 outputs, one 16-unit hidden tile: rgb256's
+// 6-16-16-3). As k_pop_pair, both members of the pair in each wave and the - member's first layer as 2 u - h+; a pass
+// takes two of the wave's tiles, so four chains run after the first layer. The output layer's exchange (mfma_out_own)
+// takes the + member's two tiles as its tiles 0 and 1 and the - member's as 2 and 3, and each lane's 4x4x1 A operands
+// are the output weights of the member its lane group holds: lane (g, j) ends with the outputs of pixel j of the pass's
+// tile g & 1 for member g >> 1, and adds that pixel's channel terms to its member's sum.
+template <class S, bool = MfmaShape<S>::kOk>
+struct PopPairOwnOk { static constexpr bool value = false; };
+template <class S>
+struct PopPairOwnOk<S, true> { static constexpr bool value = pop_own<S>() && MfmaShape<S>::kH == 16; };
+template <class S>
+constexpr bool pop_pair_own_ok() { return PopPairOwnOk<S>::value; }
+
+template <class S, bool Clamp, int From, bool UnitCw>
+__global__ void __launch_bounds__(64 * kPopWaves) __attribute__((amdgpu_waves_per_eu(pop_occupancy<S>()))) k_pop_pair_own(
+        DevModel m, PopSource src, int M, int Mcap, int chunk, int chunks, const float* __restrict__ feat, const float* __restrict__ btgt,
+        const float* __restrict__ lay1, double* __restrict__ part) {
+    using Q = MfmaShape<S>;
+    static_assert(From != kSets && pop_pair_own_ok<S>() && Q::kHt == 1, "an ES step of a pixel-per-lane shape");
+    constexpr int H = Q::kH, NIN = Q::kIn, NO = Q::kNout, NB = pair_bias_rows<S>(), PP = pair_p_pad<S>();
+    __shared__ double red[2][kPopWaves];
+    __shared__ __attribute__((aligned(16))) float wpm_s[2 * PP];          // the + member's parameters, then the - member's
+    __shared__ __attribute__((aligned(16))) float bias_s[2 * NB * 16];    // [member][row][4 g + r]
+    __shared__ __attribute__((aligned(16))) float cw_s[16];
+    __shared__ __attribute__((aligned(16))) float own_s[kPopWaves * kOwnWave];   // each wave's output-layer exchange
+    const int lane = tid_x() & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
+    const int pair = bid_x(), ch = bid_y();
+    const int i16 = lane & 15, g = lane >> 4;
+    const int s0 = ch * chunk, s1 = min(M, s0 + chunk);
+    const int tiles = (s1 - s0 + 15) >> 4;
+    const int mine = (tiles - wave + kPopWaves - 1) / kPopWaves;   // this wave's tiles: wave + 4 q, q < mine
+    // lane byte offsets: feature rows 4 ks + g, first-layer rows 4 g + r, and the targets of pixel i16 of the pass's tile
+    // g & 1 (64 slots after its tile 0)
+    const uint32_t fo = 4u * ((uint32_t)g * (uint32_t)Mcap + (uint32_t)i16);
+    const uint32_t uo = 4u * (4u * (uint32_t)g * (uint32_t)Mcap + (uint32_t)i16);
+    const uint32_t to = 4u * ((uint32_t)i16 + 64u * (uint32_t)(g & 1));
+    const __amdgpu_buffer_rsrc_t rf = buffer_of(feat, 4u * ((uint32_t)minibatch_rows(NIN) * (uint32_t)Mcap + (uint32_t)kMinibatchSlack));
+    const __amdgpu_buffer_rsrc_t rt = buffer_of(btgt, 4u * ((uint32_t)NO * (uint32_t)Mcap + (uint32_t)kMinibatchSlack));
+    const __amdgpu_buffer_rsrc_t ru = buffer_of(lay1, 4u * ((uint32_t)H * (uint32_t)Mcap + (uint32_t)kMinibatchSlack));
+    // the inputs of a pass's two tiles, loaded one pass ahead; the targets at the start of their own pass
+    struct TileIn { float b1[2][Q::kKs1]; float u[2][4]; };
+    auto tile_off = [&](int q) {   // tile wave + 4 q (uniform)
+        return (uint32_t)__builtin_amdgcn_readfirstlane((int)(4u * (uint32_t)(s0 + 16 * (wave + kPopWaves * q))));
+    };
+    auto load = [&](TileIn& in, int j) {   // tiles 2 j and 2 j + 1 (a tile past the wave's last reads its last)
+#pragma unroll
+        for (int v = 0; v < 2; v++) {
+            const uint32_t so = tile_off(min(2 * j + v, mine - 1));
+#pragma unroll
+            for (int ks = 0; ks < Q::kKs1; ks++) in.b1[v][ks] = buffer_f32(rf, fo, so + 16u * (uint32_t)ks * (uint32_t)Mcap);
+#pragma unroll
+            for (int r = 0; r < 4; r++) in.u[v][r] = buffer_f32(ru, uo, so + 4u * (uint32_t)r * (uint32_t)Mcap);
+        }
+    };
+    TileIn in0, in1;
+    if (mine > 0) load(in0, 0);
+    pair_stage<S, Clamp, From>(m, src, pair, ch, wpm_s, bias_s, cw_s);
+    __syncthreads();
+    MfmaWeights<S> Wp, Wm, Wo;   // the A operands of both members; the output layer of the member of this lane group
+    mfma_load<S>(Wp, wpm_s, lane);
+    mfma_load<S>(Wm, wpm_s + PP, lane);
+    mfma_load<S>(Wo, wpm_s + (g >> 1) * PP, lane);
+    const float ak = act_k_of<kActFold>(m);
+    auto bias = [&](int mem, int row) { return *reinterpret_cast<const f4v*>(bias_s + (mem * NB + row) * 16 + 4 * g); };
+    float cw[NO];
+#pragma unroll
+    for (int r = 0; r < NO; r++) cw[r] = m.cw[r];
+    double e = 0.0;   // this lane's member's sum
+    auto pass = [&](TileIn& c, TileIn& n, int j) {
+        j = __builtin_amdgcn_readfirstlane(j);
+        float tt[NO];
+        {
+            const uint32_t so = tile_off(2 * j);
+#pragma unroll
+            for (int r = 0; r < NO; r++) tt[r] = buffer_f32(rt, to, so + 4u * (uint32_t)r * (uint32_t)Mcap);
+        }
+        load(n, 2 * j + 2 < mine ? j + 1 : j);
+        float x[4][Q::kKsH];   // the last hidden layer: + member's tiles 0, 1, then the - member's
+#pragma unroll
+        for (int v = 0; v < 2; v++) {
+            f4v hp = bias(0, 0), hm;
+#pragma unroll
+            for (int ks = 0; ks < Q::kKs1; ks++) hp = mfma4(Wp.a1[0][ks], c.b1[v][ks], hp);
+#pragma unroll
+            for (int r = 0; r < 4; r++) hm[r] = __builtin_fmaf(2.0f, c.u[v][r], -hp[r]);
+#pragma unroll
+            for (int r = 0; r < 4; r++) { x[v][r] = act<kActFold>(hp[r], ak); x[2 + v][r] = act<kActFold>(hm[r], ak); }
+        }
+#pragma unroll
+        for (int l = 0; l < Q::kNL - 1; l++) {
+            f4v a[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) a[t] = bias(t >> 1, 1 + l);
+#pragma unroll
+            for (int ks = 0; ks < Q::kKsH; ks++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) a[t] = mfma4(t < 2 ? Wp.ah[l][0][ks] : Wm.ah[l][0][ks], x[t][ks], a[t]);
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) x[t][r] = act<kActFold>(a[t][r], ak);
+        }
+        const f4v o = mfma_out_own<S>(Wo, x, own_s + wave * kOwnWave, g, i16);
+        // the lane's pixel: its channel terms cw (d d) (a multiply, unless every cw is 1, and a fused multiply-add each)
+        float tsum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < NO; r++) {
+            const float d = out_of<S>(o[r], Clamp) - tt[r];
+            tsum = __builtin_fmaf(UnitCw ? d : __fmul_rn(cw[r], d), d, tsum);
+        }
+        const int q = 2 * j + (g & 1);
+        if (q < mine && s0 + 16 * (wave + kPopWaves * q) + i16 < s1) e += (double)tsum;
+    };
+    for (int j = 0; 2 * j < mine; j += 2) {
+        pass(in0, in1, j);
+        if (2 * j + 2 < mine) pass(in1, in0, j + 1);
+    }
+    const double ep = wave_sum(g < 2 ? e : 0.0), em = wave_sum(g < 2 ? 0.0 : e);
     if (lane == 0) { red[0][wave] = ep; red[1][wave] = em; }
     __syncthreads();
     if (tid_x() == 0) {

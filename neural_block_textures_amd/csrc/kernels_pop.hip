@@ -100,7 +100,7 @@ void launch_pop_eval(Impl& I, int pairs, int M, int chunk, int chunks) {
     launch_pop_matrix<kSets>(I, src, pairs, M, chunk, chunks);
 }
 
-// The pair-sharing population kernel (k_pop_pair) takes the ES steps of the fixed shapes it supports
+// The pair-sharing population kernels (k_pop_pair, k_pop_pair_own) take the ES steps of the fixed shapes they support
 // (pop_pair_possible: the trainer then keeps a first-layer array of H x Mcap floats) whose chunks' first layers stay
 // in the L2 (pop_pair_step: H x chunk floats within 2 MiB of an XCD's 4 MiB; the blocks of one chunk run together,
 // so an XCD's working set is about one chunk's minibatch). NTC_HIP_POP_PAIR=0 keeps k_pop_mfma for every step.
@@ -109,8 +109,14 @@ bool pop_pair_possible(const Impl& I) {
     const char* env = getenv("NTC_HIP_POP_PAIR");
     if (env && env[0] == '0') return false;
     bool ok = false;
-    dispatch_shape(I.dm, [&](auto s) { ok = pop_pair_ok<decltype(s)>(); });
+    dispatch_shape(I.dm, [&](auto s) { ok = pop_pair_ok<decltype(s)>() || pop_pair_own_ok<decltype(s)>(); });
     return ok;
+}
+
+bool pop_pair_own_shape(const Impl& I) {
+    bool own = false;
+    dispatch_shape(I.dm, [&](auto s) { own = pop_pair_own_ok<decltype(s)>(); });
+    return own;
 }
 
 bool pop_pair_step(const Impl& I, int chunk) {
@@ -125,6 +131,11 @@ static void launch_pop_pair(Impl& I, const PopSource& src, int N, int M, int chu
         if constexpr (pop_pair_ok<S>()) {
             auto kern = I.dm.clamp_out ? (unit ? k_pop_pair<S, true, From, true> : k_pop_pair<S, true, From, false>)
                                        : (unit ? k_pop_pair<S, false, From, true> : k_pop_pair<S, false, From, false>);
+            launch_timed(kern, I, dim3(N, chunks), dim3(64 * kPopWaves), 0, I.dm, src, M, I.Mcap, chunk, chunks, I.feat, I.btgt,
+                         (const float*)I.lay1, I.part);
+        } else if constexpr (pop_pair_own_ok<S>()) {
+            auto kern = I.dm.clamp_out ? (unit ? k_pop_pair_own<S, true, From, true> : k_pop_pair_own<S, true, From, false>)
+                                       : (unit ? k_pop_pair_own<S, false, From, true> : k_pop_pair_own<S, false, From, false>);
             launch_timed(kern, I, dim3(N, chunks), dim3(64 * kPopWaves), 0, I.dm, src, M, I.Mcap, chunk, chunks, I.feat, I.btgt,
                          (const float*)I.lay1, I.part);
         }

@@ -217,6 +217,8 @@ void launch_batch(Impl& I, int it, int M, int eps_pairs = 0, bool lay1 = false);
 // minibatch's first layer, lay1), and whether an ES step with chunks of `chunk` slots does
 bool pop_pair_possible(const Impl& I);
 bool pop_pair_step(const Impl& I, int chunk);
+// whether that kernel is the pixel-per-lane shapes' k_pop_pair_own
+bool pop_pair_own_shape(const Impl& I);
 void launch_perturb(Impl& I, int it, float sigma, int N);
 // the Gaussians of one ES step (NS_MLP, it, pair, k) into eps_mlp, N x P
 void launch_fd_sets(Impl& I, float h);

@@ -479,7 +479,8 @@ class Trainer:
         self._lib.ntc_trainer_set_profiling(self._h, 1 if on else 0)
 
     def on_matrix_cores(self, stage: str) -> bool:
-        """whether the stage ("pop_eval", "lat_pair", "qat_search") runs on the FP32 matrix cores"""
+        """whether the stage ("pop_eval", "lat_pair", "qat_search") runs on the FP32 matrix cores; "pop_pair": whether ES
+        steps take a kernel that shares a pair's first layer, "pop_pair_own": whether that is k_pop_pair_own"""
         return bool(self._lib.ntc_trainer_on_matrix_cores(self._h, stage.encode()))
 
     def set_matrix_cores(self, on: bool):

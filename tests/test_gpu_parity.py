@@ -248,16 +248,17 @@ def test_matrix_core_choice(orc, name, mfma):
     assert tr.on_matrix_cores("lat_pair") == mfma
 
 
-@pytest.mark.parametrize("name,pair", [("material", True), ("dct_plane", True), ("two_level", True), ("rgb_16x2", False),
+@pytest.mark.parametrize("name,pair", [("material", True), ("dct_plane", True), ("two_level", True), ("rgb_16x2", True),
                                        ("large", False), ("dct_17", False), ("material_valu", False)])
 def test_pair_population_kernel_choice(orc, name, pair):
-    """ES steps share a pair's first layer (k_pop_pair) on the fixed shapes with one or two 16-unit hidden tiles: the
-    12-output material and the 3-output 32-wide ones; not the pixel-per-lane 16-wide shape, the 64-wide one, a 17-wide
-    one or the VALU kernels"""
+    """ES steps share a pair's first layer on the fixed shapes with one or two 16-unit hidden tiles (k_pop_pair: the
+    12-output material and the 3-output 32-wide ones; k_pop_pair_own: the pixel-per-lane 16-wide one); not the 64-wide
+    one, a 17-wide one or the VALU kernels"""
     lay = LAYOUTS[name]
     z, p, tgt = data(lay, 8)
     tr = trainer(lay, z, p, tgt)
     assert tr.on_matrix_cores("pop_pair") == pair
+    assert tr.on_matrix_cores("pop_pair_own") == (pair and name == "rgb_16x2")
     tr.close()
 
 
