@@ -107,15 +107,28 @@ __global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevMod
                     for (int i = 0; i < kGatherRun; i++) d += v[i];
                 }
             } else {
-                for (int py = y0; py < y1; py++) {
+                // runs of 16 in raster order (a row's last run padded with +0), two buffers: the next run's loads are
+                // in flight while the current run is added
+                float va[16], vb[16];
+                auto load_run = [&](float (&v)[16], int py, int px) {
                     const float* rw = dp + (size_t)py * m.W;
-                    for (int px = x0; px < x1; px += 16) {
-                        float v[16];
 #pragma unroll
-                        for (int i = 0; i < 16; i++) v[i] = px + i < x1 ? rw[px + i] : 0.0f;
+                    for (int i = 0; i < 16; i++) v[i] = px + i < x1 ? rw[px + i] : 0.0f;
+                };
+                auto step = [&](int& py, int& px) { px += 16; if (px >= x1) { px = x0; py++; } };
+                int py = y0, px = x0;
+                load_run(va, py, px);
+                while (true) {
+                    step(py, px);
+                    if (py < y1) load_run(vb, py, px);
 #pragma unroll
-                        for (int i = 0; i < 16; i++) d += v[i];
-                    }
+                    for (int i = 0; i < 16; i++) d += va[i];
+                    if (py >= y1) break;
+                    step(py, px);
+                    if (py < y1) load_run(va, py, px);
+#pragma unroll
+                    for (int i = 0; i < 16; i++) d += vb[i];
+                    if (py >= y1) break;
                 }
             }
             dsum[q][j] = d;
