@@ -209,11 +209,14 @@ __global__ void __launch_bounds__(kTPB) k_dct_clamp0(float* __restrict__ z, floa
 
 // dct_snap_block (main.cpp:918-940) per (block, channel), one wave each: clamp the shadow in place, forward DCT of
 // (s + 1) * 32, quantize (+ truncation), symbols out, reconstruct zq; with the rate term on, the block's
-// proxy bits and its two counts (added up on the host when asked: no atomics).
+// proxy bits and its two counts (added up on the host when asked: no atomics). pull != 0: the shadow is first pulled
+// toward the current plane, z + pull (zq - z) as k_shadow_pull computes it (--dct-shadow-pull followed by the re-snap,
+// main.cpp:4142-4146, in one launch: each value of the plane belongs to one wave, which reads its zq before
+// replacing it).
 __global__ void __launch_bounds__(64 * kDctWaves) k_dct_snap(DevDct D, DevLevel L0, float* __restrict__ z, float* __restrict__ zq,
                                                             int16_t* __restrict__ sym, const uint8_t* __restrict__ code,
                                                             const int* __restrict__ step, int32_t* __restrict__ bits,
-                                                            int* __restrict__ tn) {
+                                                            int* __restrict__ tn, float pull) {
     __shared__ DctTables T;
     load_tables(D, T);
     const int lane = threadIdx.x & 63;
@@ -221,7 +224,9 @@ __global__ void __launch_bounds__(64 * kDctWaves) k_dct_snap(DevDct D, DevLevel 
     if (i >= D.n) return;
     const int b = i / D.C, c = i % D.C, bx = b % D.BW, by = b / D.BW;
     const size_t idx = lvl0_index(L0, bx, by, lane & 7, lane >> 3, c);
-    const float s = dct_clampf(z[idx], -1.0f, 1.0f);
+    float zv = z[idx];
+    if (pull != 0.0f) zv = __builtin_fmaf(pull, zq[idx] - zv, zv);
+    const float s = dct_clampf(zv, -1.0f, 1.0f);
     z[idx] = s;
     const float Cf = wave_fwd8(T, (s + 1.0f) * 32.0f, lane);
     const int cd = code[i];
@@ -304,10 +309,10 @@ void launch_dct_clamp0(Impl& I) {
     hipLaunchKernelGGL(k_dct_clamp0, dim3(blocks_for(n0, kTPB)), dim3(kTPB), 0, I.stream, I.z, I.zq, (size_t)I.d.lv[0].off, n0);
     NTC_CHECK(hipGetLastError());
 }
-void launch_dct_snap(Impl& I) {
+void launch_dct_snap(Impl& I, float pull) {
     ProfScope ps(I, "dct_snap");
     hipLaunchKernelGGL(k_dct_snap, dim3(blocks_for(I.ddct.n, kDctWaves)), dim3(64 * kDctWaves), 0, I.stream, I.ddct, I.dm.lv[0], I.z, I.zq,
-                       I.dct_sym, I.dct_code, I.dct_step, I.dct_bits, I.dct_tn);
+                       I.dct_sym, I.dct_code, I.dct_step, I.dct_bits, I.dct_tn, pull);
     NTC_CHECK(hipGetLastError());
 }
 void launch_dct_recon(Impl& I) {

@@ -446,6 +446,13 @@ void Trainer::shadow_pull(size_t off, size_t n, float f) {
     Impl& I = *im;
     if (!I.zq || n == 0) return;
     if (off + n > I.nz) die("shadow_pull range outside the latent");
+    const size_t n0 = (size_t)I.d.lv[0].W * I.d.lv[0].H * I.d.lv[0].C;
+    if (I.dct && I.dct_live && off == (size_t)I.dm.lv[0].off && n == n0 && f != 0.0f) {
+        // the live plane as a whole: the pull inside the re-snap's launch (the other levels' shadow did not move, so
+        // their snapped values stand)
+        launch_dct_snap(I, f);
+        return;
+    }
     launch_shadow_pull(I, off, n, f);
     snap_latent_impl(I);
 }

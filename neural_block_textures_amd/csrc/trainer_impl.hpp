@@ -259,7 +259,8 @@ void launch_qat_search(Impl& I);
 // kernels_quant.hip
 void launch_qes_snap(Impl& I);
 void launch_dct_clamp0(Impl& I);
-void launch_dct_snap(Impl& I);
+// pull != 0: the level-0 shadow pulled toward the current plane first (a --dct-shadow-pull over the whole plane)
+void launch_dct_snap(Impl& I, float pull = 0.0f);
 void launch_dct_recon(Impl& I);
 // the decoder sensitivity probe over the decode buffer: codes (and block gains, when gain != null) into device buffers
 void launch_dct_probe(Impl& I, uint8_t* code, float* gain);

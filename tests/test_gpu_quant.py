@@ -91,6 +91,13 @@ def test_dct_plane(orc, C0, q, deadzone, lam, rate):
     zs5, zq5, _, _ = H.snap(np.concatenate([zp, zd3[n0:]]))
     zd5, _ = tr.download_model()
     assert np.array_equal(zd5[:n0], zs5) and np.array_equal(tr.download_zq()[:n0], zq5)
+    # the whole plane pulls inside the re-snap's launch; a part of it through the pull kernel and then the re-snap
+    tr.shadow_pull(0, n0 // 2, 0.02)
+    zp = zs5.copy()
+    orc._shadow_pull(zp.ctypes.data, zq5.ctypes.data, n0 // 2, 0.02)
+    zs6, zq6, _, _ = H.snap(np.concatenate([zp, zd5[n0:]]))
+    zd6, _ = tr.download_model()
+    assert np.array_equal(zd6[:n0], zs6) and np.array_equal(tr.download_zq()[:n0], zq6)
 
 
 @pytest.mark.parametrize("C0,q", [(1, [50]), (2, [75, 30])])
