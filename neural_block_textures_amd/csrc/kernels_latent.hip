@@ -41,8 +41,9 @@ __global__ void __launch_bounds__(kTPB) k_lat_eps(NoiseFix nt, DevModel m, uint6
 // of four pairs at once (each sum in raster order), then apply the four pairs in order to the texels'
 // channels (four threads per texel, each on every fourth channel). A texel's gradient is then final
 // (one block owns it), so with `adam` the block also takes the texel's Adam step (the latent ES step's
-// update, main.cpp:2036-2037). With `first` the gradient starts from zero rather than from grad (the step's
-// first group of pairs).
+// update, main.cpp:2036-2037), and with zq_copy writes the new value to the decode copy too (a level that is neither
+// --qes nor DCT coded, where the snap would copy it). With `first` the gradient starts from zero rather than from grad
+// (the step's first group of pairs).
 //
 // Blocks past the gather's own (blockIdx.x >= gblocks) draw the next latent step's Gaussians for the perturbed
 // levels (the entries lo .. hi - 1 whose level is in `mask`; block d = pair d / eb, entries lo + 128 (d % eb) ..):
@@ -59,7 +60,8 @@ __global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevMod
                                                                          int rate, float rate_scale, int dct_bw, int dct_n,
                                                                          const int32_t* __restrict__ dbits, float* __restrict__ grad,
                                                                          int first, int adam, float* __restrict__ z, float* __restrict__ zm,
-                                                                         float* __restrict__ zv, float lr, float c1, float c2, LatAhead ah) {
+                                                                         float* __restrict__ zv, float lr, float c1, float c2, LatAhead ah,
+                                                                         float* __restrict__ zq_copy) {
     if ((int)blockIdx.x >= ah.gblocks) {   // a draw-ahead block (uniform: the whole block returns here)
         const int d = (int)blockIdx.x - ah.gblocks, k = d / ah.eb;
         const uint64_t head = noise_head(ah.seed, NS_LAT, ah.next_step, (uint32_t)k);
@@ -151,7 +153,10 @@ __global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevMod
                     }
                 }
                 grad[i] = gc;
-                if (adam && last) adam_at(z, zm, zv, i, gc, lr, c1, c2);
+                if (adam && last) {
+                    adam_at(z, zm, zv, i, gc, lr, c1, c2);
+                    if (zq_copy) zq_copy[i] = z[i];   // a level the decode copy takes as it is
+                }
             }
         }
         __syncthreads();
@@ -178,7 +183,8 @@ void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask) {
     NTC_CHECK(hipGetLastError());
 }
 
-void launch_lat_gather(Impl& I, int level, int k0, int K, float scale, bool rate, float lr, int t, int ahead_K, unsigned mask) {
+void launch_lat_gather(Impl& I, int level, int k0, int K, float scale, bool rate, float lr, int t, int ahead_K, unsigned mask,
+                       float* zq_copy) {
     const size_t ntx = (size_t)I.d.lv[level].W * I.d.lv[level].H;
     const float c1 = t > 0 ? 1.0f - powf(0.9f, (float)t) : 1.0f, c2 = t > 0 ? 1.0f - powf(0.999f, (float)t) : 1.0f;
     LatAhead ah{};
@@ -205,7 +211,7 @@ void launch_lat_gather(Impl& I, int level, int k0, int K, float scale, bool rate
                        scale, I.dpix, I.eps_lat,
                        I.ranges, rate ? 1 : 0, I.ddct.rate_scale, I.ddct.BW, I.ddct.n, rate ? I.dct_dbits + (size_t)k0 * I.ddct.n : nullptr,
                        I.zgrad, k0 == 0 ? 1 : 0, t > 0 ? 1 : 0, I.z, I.zm,
-                       I.zv, lr, c1, c2, ah);
+                       I.zv, lr, c1, c2, ah, zq_copy);
     NTC_CHECK(hipGetLastError());
 }
 

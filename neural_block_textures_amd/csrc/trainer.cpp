@@ -598,6 +598,7 @@ void Trainer::lat_step(int /*it*/, float sigma, float lr, int K) {
     const bool rate = I.dct_live && I.dct_rate_es;
     I.dct_evals = rate ? I.ddct.n * K : 0;
     if (!mask) launch_fill(I, I.zgrad, I.nz, 0.0f);
+    bool direct_zq = false;
     if (mask) {
         const float scale = 1.0f / (2.0f * (float)K * sigma);
         ++I.lat_t;
@@ -616,6 +617,9 @@ void Trainer::lat_step(int /*it*/, float sigma, float lr, int K) {
         if (ahead) std::swap(I.eps_lat, I.eps_ahead);
         int last_level = 0;
         for (int l = 0; l < I.d.nlev; l++) if ((mask >> l) & 1u) last_level = l;
+        // a DCT model without --qes whose step moves every level past the plane: the gathers' Adam steps write those
+        // levels' decode copy themselves, and the snap after the step is the plane's alone
+        direct_zq = I.dct && !I.qes && (mask | 1u) == (1u << I.d.nlev) - 1;
         for (int k0 = 0; k0 < K; k0 += G) {
             const int g = std::min(G, K - k0);
             const bool last = k0 + g == K;
@@ -626,7 +630,7 @@ void Trainer::lat_step(int /*it*/, float sigma, float lr, int K) {
             for (int l = 0; l < I.d.nlev; l++)
                 if ((mask >> l) & 1u)
                     launch_lat_gather(I, l, k0, g, scale, rate && l == 0, lr, last ? I.lat_t : 0,
-                                      (G >= K && l == last_level) ? K : 0, mask);
+                                      (G >= K && l == last_level) ? K : 0, mask, direct_zq && l > 0 ? I.zq : nullptr);
         }
         I.ahead_step = G >= K ? I.lat_step_no + 1 : -1;
         I.ahead_K = K;
@@ -634,7 +638,12 @@ void Trainer::lat_step(int /*it*/, float sigma, float lr, int K) {
     } else {
         launch_adam(I, I.z, I.zgrad, I.zm, I.zv, I.nz, lr, ++I.lat_t);
     }
-    snap_latent_impl(I);
+    if (direct_zq) {
+        if (I.dct_live) launch_dct_snap(I);
+        else launch_dct_clamp0(I);
+    } else {
+        snap_latent_impl(I);
+    }
     I.lat_step_no++;
 }
 

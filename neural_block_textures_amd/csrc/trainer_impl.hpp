@@ -253,7 +253,7 @@ void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask);
 // the footprint gather of one level for the group of pairs k0 .. k0 + K - 1 (added to the gradient so far); with
 // t > 0 (the step's last group) also the Adam step t (learning rate lr) of its texels
 void launch_lat_gather(Impl& I, int level, int k0, int K, float scale, bool rate, float lr = 0.0f, int t = 0, int ahead_K = 0,
-                       unsigned mask = 0);
+                       unsigned mask = 0, float* zq_copy = nullptr);
 void launch_qat_search(Impl& I);
 
 // kernels_quant.hip
