@@ -32,7 +32,7 @@ __global__ void __launch_bounds__(kTPB) k_lat_eps(NoiseFix nt, DevModel m, uint6
     if ((mask >> l) & 1u) eps[(size_t)k * m.nz + i] = gauss_at(nt, noise_head(seed, NS_LAT, step, (uint32_t)(k0 + k)), (uint64_t)i);
 }
 
-// Footprint gather for one level (the gather form of the reference's raster-order scatter,
+// Footprint gather per level (the gather form of the reference's raster-order scatter,
 // main.cpp:2011-2037): the loss difference a texel's taps collect from pair k is the sum of dpix[k]
 // over the pixel rectangle that reads the texel, in raster order (the rectangle comes from the host's
 // range table, built with the same tap arithmetic); then grad += (d * scale) * eps per channel, pair
@@ -49,21 +49,29 @@ __global__ void __launch_bounds__(kTPB) k_lat_eps(NoiseFix nt, DevModel m, uint6
 // levels (the entries lo .. hi - 1 whose level is in `mask`; block d = pair d / eb, entries lo + 128 (d % eb) ..):
 // the values k_lat_eps would draw for step next_step, written to eps_next. They run beside the gather's blocks,
 // which leave most of the chip idle, so the next step needs no draw launch of its own.
+//
+// One launch gathers every perturbed level of the step (GatherLevels: blocks start[i] .. start[i + 1] - 1 take level
+// lv[i]); the rate term goes to level 0, and zq_copy[i] (or null) is level lv[i]'s decode copy.
 constexpr int kGatherTex = 16, kGatherPairs = 4, kGatherRun = 32, kAheadPerBlock = 128;
 struct LatAhead {
     NoiseFix nt; uint64_t seed; uint32_t next_step; unsigned mask;
-    float* eps_next; int gblocks, eb; long long lo, hi;
+    float* eps_next; int eb; long long lo, hi;
 };
-__global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevModel m, int level, int K, float scale,
+struct GatherLevels {
+    int n;
+    int lv[kMaxLevels];
+    int start[kMaxLevels + 1];
+    float* zq_copy[kMaxLevels];
+};
+__global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevModel m, GatherLevels G, int K, float scale,
                                                                          const float* __restrict__ dpix,
                                                                          const float* __restrict__ eps, const int* __restrict__ ranges,
-                                                                         int rate, float rate_scale, int dct_bw, int dct_n,
+                                                                         int rate0, float rate_scale, int dct_bw, int dct_n,
                                                                          const int32_t* __restrict__ dbits, float* __restrict__ grad,
                                                                          int first, int adam, float* __restrict__ z, float* __restrict__ zm,
-                                                                         float* __restrict__ zv, float lr, float c1, float c2, LatAhead ah,
-                                                                         float* __restrict__ zq_copy) {
-    if ((int)blockIdx.x >= ah.gblocks) {   // a draw-ahead block (uniform: the whole block returns here)
-        const int d = (int)blockIdx.x - ah.gblocks, k = d / ah.eb;
+                                                                         float* __restrict__ zv, float lr, float c1, float c2, LatAhead ah) {
+    if ((int)blockIdx.x >= G.start[G.n]) {   // a draw-ahead block (uniform: the whole block returns here)
+        const int d = (int)blockIdx.x - G.start[G.n], k = d / ah.eb;
         const uint64_t head = noise_head(ah.seed, NS_LAT, ah.next_step, (uint32_t)k);
         const long long i0 = ah.lo + (long long)(d - k * ah.eb) * kAheadPerBlock, i1 = min(ah.hi, i0 + kAheadPerBlock);
         for (long long i = i0 + threadIdx.x; i < i1; i += kGatherTex * kGatherPairs)
@@ -71,9 +79,14 @@ __global__ void __launch_bounds__(kGatherTex * kGatherPairs) k_lat_gather(DevMod
         return;
     }
     __shared__ float dsum[kGatherPairs][kGatherTex];
+    int li = 0;   // this block's level (uniform)
+    while (li + 1 < G.n && (int)blockIdx.x >= G.start[li + 1]) li++;
+    const int level = G.lv[li];
     const DevLevel& L = m.lv[level];
+    const int rate = rate0 && level == 0;
+    float* const zq_copy = G.zq_copy[li];
     const int j = threadIdx.x % kGatherTex, q = threadIdx.x / kGatherTex;
-    const int t = blockIdx.x * kGatherTex + j;
+    const int t = ((int)blockIdx.x - G.start[li]) * kGatherTex + j;
     const bool live = t < L.W * L.H;
     const int tt = live ? t : 0;
     const int tx = tt % L.W, ty = tt / L.W;
@@ -183,14 +196,21 @@ void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask) {
     NTC_CHECK(hipGetLastError());
 }
 
-void launch_lat_gather(Impl& I, int level, int k0, int K, float scale, bool rate, float lr, int t, int ahead_K, unsigned mask,
-                       float* zq_copy) {
-    const size_t ntx = (size_t)I.d.lv[level].W * I.d.lv[level].H;
+void launch_lat_gather(Impl& I, unsigned mask, int k0, int K, float scale, bool rate, float lr, int t, int ahead_K, float* zq_rest) {
     const float c1 = t > 0 ? 1.0f - powf(0.9f, (float)t) : 1.0f, c2 = t > 0 ? 1.0f - powf(0.999f, (float)t) : 1.0f;
+    GatherLevels G{};
+    size_t grid = 0;
+    for (int l = 0; l < I.d.nlev; l++)
+        if ((mask >> l) & 1u) {
+            G.lv[G.n] = l;
+            G.start[G.n] = (int)grid;
+            G.zq_copy[G.n] = l > 0 ? zq_rest : nullptr;
+            grid += (size_t)blocks_for((size_t)I.d.lv[l].W * I.d.lv[l].H, kGatherTex);
+            G.n++;
+        }
+    G.start[G.n] = (int)grid;
     LatAhead ah{};
-    ah.gblocks = blocks_for(ntx, kGatherTex);
     ah.eb = 1;
-    size_t grid = (size_t)ah.gblocks;
     if (ahead_K > 0) {   // the next step's Gaussians: the range of entries the perturbed levels span
         ah.nt = I.noise; ah.seed = I.d.seed; ah.next_step = (uint32_t)(I.lat_step_no + 1); ah.mask = mask; ah.eps_next = I.eps_ahead;
         ah.lo = (long long)I.nz; ah.hi = 0;
@@ -201,17 +221,17 @@ void launch_lat_gather(Impl& I, int level, int k0, int K, float scale, bool rate
             }
         ah.eb = blocks_for((size_t)(ah.hi - ah.lo), kAheadPerBlock);
         grid += (size_t)ah.eb * (size_t)ahead_K;
-        if (grid > 0x7fffffff) {
-            fprintf(stderr, "ntc_hip backend: latent gather launch of %zu blocks\n", grid);
-            exit(1);
-        }
+    }
+    if (grid > 0x7fffffff) {
+        fprintf(stderr, "ntc_hip backend: latent gather launch of %zu blocks\n", grid);
+        exit(1);
     }
     ProfScope ps(I, "lat_gather");
-    hipLaunchKernelGGL(k_lat_gather, dim3((unsigned)grid), dim3(kGatherTex * kGatherPairs), 0, I.stream, I.dm, level, K,
+    hipLaunchKernelGGL(k_lat_gather, dim3((unsigned)grid), dim3(kGatherTex * kGatherPairs), 0, I.stream, I.dm, G, K,
                        scale, I.dpix, I.eps_lat,
                        I.ranges, rate ? 1 : 0, I.ddct.rate_scale, I.ddct.BW, I.ddct.n, rate ? I.dct_dbits + (size_t)k0 * I.ddct.n : nullptr,
                        I.zgrad, k0 == 0 ? 1 : 0, t > 0 ? 1 : 0, I.z, I.zm,
-                       I.zv, lr, c1, c2, ah, zq_copy);
+                       I.zv, lr, c1, c2, ah);
     NTC_CHECK(hipGetLastError());
 }
 

@@ -615,8 +615,6 @@ void Trainer::lat_step(int /*it*/, float sigma, float lr, int K) {
         // (the levels outside the mask keep the zeros of the first step's draw: nothing writes them).
         const bool ahead = I.ahead_step == I.lat_step_no && I.ahead_K == K && G >= K && I.eps_ahead;
         if (ahead) std::swap(I.eps_lat, I.eps_ahead);
-        int last_level = 0;
-        for (int l = 0; l < I.d.nlev; l++) if ((mask >> l) & 1u) last_level = l;
         // a DCT model without --qes whose step moves every level past the plane: the gathers' Adam steps write those
         // levels' decode copy themselves, and the snap after the step is the plane's alone
         direct_zq = I.dct && !I.qes && (mask | 1u) == (1u << I.d.nlev) - 1;
@@ -627,10 +625,7 @@ void Trainer::lat_step(int /*it*/, float sigma, float lr, int K) {
             launch_lat_pair(I, g, sigma, mask);
             I.lat_last_K = g;
             if (rate) launch_dct_rate_pairs(I, k0, g, sigma);
-            for (int l = 0; l < I.d.nlev; l++)
-                if ((mask >> l) & 1u)
-                    launch_lat_gather(I, l, k0, g, scale, rate && l == 0, lr, last ? I.lat_t : 0,
-                                      (G >= K && l == last_level) ? K : 0, mask, direct_zq && l > 0 ? I.zq : nullptr);
+            launch_lat_gather(I, mask, k0, g, scale, rate, lr, last ? I.lat_t : 0, G >= K ? K : 0, direct_zq ? I.zq : nullptr);
         }
         I.ahead_step = G >= K ? I.lat_step_no + 1 : -1;
         I.ahead_K = K;

@@ -250,10 +250,12 @@ void launch_copy_calibration(Impl& I, const float* src, float* dst, size_t n);
 void launch_lat_eps(Impl& I, int k0, int K, unsigned mask);
 void launch_lat_pair_valu(Impl& I, int K, float sigma, unsigned mask);
 void launch_lat_pair(Impl& I, int K, float sigma, unsigned mask);
-// the footprint gather of one level for the group of pairs k0 .. k0 + K - 1 (added to the gradient so far); with
-// t > 0 (the step's last group) also the Adam step t (learning rate lr) of its texels
-void launch_lat_gather(Impl& I, int level, int k0, int K, float scale, bool rate, float lr = 0.0f, int t = 0, int ahead_K = 0,
-                       unsigned mask = 0, float* zq_copy = nullptr);
+// the footprint gather of the levels in mask, in one launch, for the group of pairs k0 .. k0 + K - 1 (added to the
+// gradient so far; rate: level 0's DCT rate term too); with t > 0 (the step's last group) also the Adam step t
+// (learning rate lr) of their texels, and with zq_rest the new values of the levels past 0 in that decode copy;
+// ahead_K > 0: extra blocks draw the next step's Gaussians of that many pairs
+void launch_lat_gather(Impl& I, unsigned mask, int k0, int K, float scale, bool rate, float lr = 0.0f, int t = 0, int ahead_K = 0,
+                       float* zq_rest = nullptr);
 void launch_qat_search(Impl& I);
 
 // kernels_quant.hip
