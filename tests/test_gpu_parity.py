@@ -262,6 +262,18 @@ def test_pair_population_kernel_choice(orc, name, pair):
     tr.close()
 
 
+def test_pair_population_kernel_chunk_in_l2(orc):
+    """the pair kernels read each chunk's first layer (H x chunk floats) from the L2: a step whose chunk would take more
+    than 2 MiB evaluates on k_pop_mfma (2048 pairs of 65536 slots: one chunk, 8 MiB for 32 units), a step of the same
+    model with fewer pairs (smaller chunks) on k_pop_pair"""
+    lay = LAYOUTS["dct_plane"]
+    z, p, tgt = data(lay, 8)
+    for pairs, pair in ((2048, False), (64, True)):
+        tr = trainer(lay, z, p, tgt, max_pairs=pairs, max_batch=65536)
+        assert tr.on_matrix_cores("pop_pair") == pair, pairs
+        tr.close()
+
+
 @pytest.mark.parametrize("name", ["jit_valu_7", "jit_mfma_28", "jit_widths", "runtime"])
 def test_specialised_shape_in_use(orc, name):
     """a shape the library does not list runs on kernels specialised for it at init (hidden layers of one width:
