@@ -6,7 +6,7 @@ and refits, the shadow pull, in main.cpp:4063-4148's order, --rng hash), from or
 reference's main.cpp compiled with its own -O3 -ffast-math flags for x86-64-v3. Run from the repository root in the
 build container (the reference tree is read there only):
 
-    make -C oracle ref && python tests/golden/make_final_psnr.py material512 [--state DIR]
+    make -C oracle ref && python tests/golden/make_final_psnr.py material512 [--state DIR] [--isa x86-64-v4]
 
 Schedules (the reference's flags; C3-C5 of the workload descriptions):
   rgb256            200 iterations.
@@ -102,7 +102,7 @@ def dct_state(w, lam, lo16):
     return d, h
 
 
-def run(name: str, state_dir: str):
+def run(name: str, state_dir: str, isa: str = "x86-64-v3"):
     w = workloads()[name]
     s = SCHEDULES[name]
     lay = w.layout
@@ -111,7 +111,7 @@ def run(name: str, state_dir: str):
     pairs = s.get("pairs") or w.mlp_pairs
     z, p, tgt = inputs(w)
     orc = oracle()
-    ref = reference(fast=True)
+    ref = reference(fast=True, isa=isa)
     L = ref.lib
     cfg = OrTrainCfg()
     cfg.seed, cfg.mlp_pairs, cfg.mlp_batch, cfg.mlp_sigma, cfg.mlp_lr = w.seed, pairs, w.mlp_batch, w.mlp_sigma, w.mlp_lr
@@ -129,7 +129,7 @@ def run(name: str, state_dir: str):
     else:
         h = L.ref_train_create(C.byref(mc), C.byref(cfg), z.ctypes.data, p.ctypes.data, tgt.ctypes.data)
     os.makedirs(state_dir, exist_ok=True)
-    tag = digest(z, p, tgt).tobytes().hex()[:16]
+    tag = digest(z, p, tgt).tobytes().hex()[:16] + ("" if isa == "x86-64-v3" else "_" + isa)
     spath = os.path.join(state_dir, f"{name}_{tag}.state")
     jpath = os.path.join(state_dir, f"{name}_{tag}.json")
     log = {"checkpoints": [], "psnr": [], "mse": [], "done": 0, "seconds": 0.0}
@@ -169,14 +169,14 @@ def run(name: str, state_dir: str):
                    pairs=np.int32(pairs), fp16_end=np.int32(bool(s.get("fp16_end"))), checkpoints=np.array(log["checkpoints"], np.int32),
                    psnr=np.array(log["psnr"]), mse=np.array(log["mse"]), start_psnr=np.float64(ps0), start_mse=np.float64(mse0),
                    final_psnr=np.float64(ps_f), final_mse=np.float64(mse_f), cpu_seconds=np.float64(time.time() - t0),
-                   threads=np.int32(L.ref_omp_threads()))
+                   threads=np.int32(L.ref_omp_threads()), isa=np.array(isa))
         if w.dct_q:
             code = np.zeros(keep["code"].size, np.uint8)
             L.ref_train_get_dct_codes(h, code.ctypes.data)
             out.update(dct_start=np.int32(s["dct_start"]), dct_refit=np.int32(s["dct_refit"]),
                        dct_refit_until=np.int32(s["dct_refit_until"]), dct_lambda=np.float32(s["dct_lambda"]),
                        lo16=np.int32(s["lo16"]), shadow_pull=np.float32(s["shadow_pull"]), final_codes=code)
-        path = os.path.join(OUT, f"final_psnr_{name}.npz")
+        path = os.path.join(OUT, f"final_psnr_{name}{'' if isa == 'x86-64-v3' else '_' + isa.split('-')[-1]}.npz")
         np.savez_compressed(path, **out)
         print(f"{name}: {iters} iterations, start psnr {ps0:.4f} dB, final psnr {ps_f:.4f} dB (mse {mse_f:.4f}), "
               f"{time.time() - t0:.0f} s -> {os.path.relpath(path, ROOT)}", flush=True)
@@ -189,9 +189,13 @@ def main():
     ap.add_argument("workloads", nargs="+", choices=sorted(SCHEDULES))
     ap.add_argument("--state", default=os.path.join(tempfile.gettempdir(), "ntc_final_psnr"),
                     help="where the loop's state is kept between checkpoints")
+    ap.add_argument("--isa", default="x86-64-v3", choices=["x86-64-v3", "x86-64-v4"],
+                    help="the reference build (its own -O3 -ffast-math flags) for this x86-64 level; the fixtures the "
+                         "tests hold to their bars are the x86-64-v3 build's, an x86-64-v4 run (final_psnr_<workload>_v4.npz) "
+                         "measures how far two builds of the reference's own loop end apart")
     a = ap.parse_args()
     for name in a.workloads:
-        run(name, a.state)
+        run(name, a.state, a.isa)
 
 
 if __name__ == "__main__":
